@@ -1,0 +1,433 @@
+// extern "C" surface of include/omg_hip.h: converts between the C structs
+// and the engine's types and turns every omg::Error into a status code plus
+// a thread-local message.
+#include "../../include/omg_hip.h"
+
+#include <cstdlib>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "engine.h"
+
+struct omg_builder {
+    std::unique_ptr<omg::Builder> b;
+};
+struct omg_engine {
+    std::unique_ptr<omg::Engine> e;
+};
+struct omg_weight {
+    omg::DevTensor t;
+};
+struct omg_weights {
+    omg::Weights w;
+    std::vector<const std::pair<const std::string, omg::QTensor>*> order;  // catalogue order
+    void index() {
+        order.clear();
+        for (const auto& spec : w.config.tensors()) {
+            auto it = w.tensors.find(spec.name);
+            if (it != w.tensors.end()) order.push_back(&*it);
+        }
+    }
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+template <class F>
+int guard(F&& f) {
+    try {
+        f();
+        return OMG_OK;
+    } catch (const omg::Error& e) {
+        g_err = e.what();
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        g_err = "out of host memory";
+        return OMG_E_INVALID;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return OMG_E_INVALID;
+    }
+}
+
+struct Groups {
+    std::vector<std::vector<omg::BranchIn>> branches;
+    std::vector<omg::GroupIn> groups;
+};
+
+Groups convert(const omg_group* g, size_t n) {
+    if (n && !g) omg::fail(omg::E_INVALID, "null groups");
+    Groups out;
+    out.branches.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+        if (g[i].prefix_len && !g[i].prefix) omg::fail(omg::E_INVALID, "null prefix");
+        if (g[i].nbranches && !g[i].branches) omg::fail(omg::E_INVALID, "null branches");
+        for (size_t b = 0; b < g[i].nbranches; ++b) {
+            const omg_branch& br = g[i].branches[b];
+            if ((br.ntokens && !br.tokens) || (br.nwant && !br.want)) omg::fail(omg::E_INVALID, "null branch data");
+            out.branches[i].push_back({br.tokens, int64_t(br.ntokens), br.want, int64_t(br.nwant)});
+        }
+    }
+    for (size_t i = 0; i < n; ++i)
+        out.groups.push_back({g[i].prefix, int64_t(g[i].prefix_len), out.branches[i].data(), int64_t(g[i].nbranches)});
+    return out;
+}
+
+omg::Engine& eng(omg_engine* e) {
+    if (!e || !e->e) omg::fail(omg::E_INVALID, "null engine");
+    return *e->e;
+}
+
+omg::QTensor make_tensor(int dtype, const int64_t* shape, size_t ndim, const void* data, size_t nbytes,
+                         const void* scales, size_t nscale) {
+    if (dtype < 0 || dtype > 2) omg::fail(omg::E_INVALID, "unknown dtype");
+    omg::QTensor t;
+    t.dtype = omg::Dtype(dtype);
+    t.shape.assign(shape, shape + ndim);
+    const uint8_t* d = static_cast<const uint8_t*>(data);
+    const uint8_t* s = static_cast<const uint8_t*>(scales);
+    if (nbytes && !d) omg::fail(omg::E_INVALID, "null tensor data");
+    if (nscale && !s) omg::fail(omg::E_INVALID, "null tensor scales");
+    t.data.assign(d, d + nbytes);
+    t.scales.assign(s, s + nscale);
+    return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* omg_last_error(void) { return g_err.c_str(); }
+
+omg_builder* omg_builder_new(const char* config_json) {
+    omg_builder* out = nullptr;
+    guard([&] {
+        if (!config_json) omg::fail(omg::E_INVALID, "null config");
+        auto cfg = omg::Config::from_json(omg::Json::parse(config_json));
+        out = new omg_builder{std::make_unique<omg::Builder>(std::move(cfg))};
+    });
+    return out;
+}
+
+int omg_builder_push(omg_builder* b, const char* name, int dtype, const int64_t* shape, size_t ndim,
+                     const void* data, size_t nbytes, const void* scales, size_t nscale_bytes) {
+    return guard([&] {
+        if (!b || !b->b || !name || (ndim && !shape)) omg::fail(omg::E_INVALID, "null argument");
+        b->b->push(name, make_tensor(dtype, shape, ndim, data, nbytes, scales, nscale_bytes));
+    });
+}
+
+omg_weights* omg_synth(const char* config_json, uint64_t seed, int linear_dtype, int embed_dtype) {
+    omg_weights* out = nullptr;
+    guard([&] {
+        if (!config_json) omg::fail(omg::E_INVALID, "null config");
+        if (linear_dtype < 0 || linear_dtype > 2 || embed_dtype < 0 || embed_dtype > 2)
+            omg::fail(omg::E_INVALID, "unknown dtype");
+        auto cfg = omg::Config::from_json(omg::Json::parse(config_json));
+        auto w = std::make_unique<omg_weights>();
+        w->w = omg::synth_weights(cfg, seed, omg::Dtype(linear_dtype), omg::Dtype(embed_dtype));
+        w->index();
+        out = w.release();
+    });
+    return out;
+}
+
+omg_weights* omg_load_dir(const char* dir) {
+    omg_weights* out = nullptr;
+    guard([&] {
+        if (!dir) omg::fail(omg::E_INVALID, "null dir");
+        auto w = std::make_unique<omg_weights>();
+        w->w = omg::load_dir(dir);
+        w->index();
+        out = w.release();
+    });
+    return out;
+}
+
+size_t omg_weights_count(const omg_weights* w) { return w ? w->order.size() : 0; }
+
+int omg_weights_get(const omg_weights* w, size_t i, const char** name, int* dtype, int64_t* shape, size_t* ndim,
+                    const uint8_t** data, size_t* nbytes, const uint8_t** scales, size_t* nscale_bytes) {
+    return guard([&] {
+        if (!w || i >= w->order.size()) omg::fail(omg::E_INVALID, "weights index out of range");
+        const auto& kv = *w->order[i];
+        if (name) *name = kv.first.c_str();
+        if (dtype) *dtype = int(kv.second.dtype);
+        if (ndim) *ndim = kv.second.shape.size();
+        if (shape)
+            for (size_t k = 0; k < kv.second.shape.size() && k < 4; ++k) shape[k] = kv.second.shape[k];
+        if (data) *data = kv.second.data.data();
+        if (nbytes) *nbytes = kv.second.data.size();
+        if (scales) *scales = kv.second.scales.data();
+        if (nscale_bytes) *nscale_bytes = kv.second.scales.size();
+    });
+}
+
+void omg_weights_free(omg_weights* w) { delete w; }
+
+int omg_builder_push_weights(omg_builder* b, const omg_weights* w) {
+    return guard([&] {
+        if (!b || !b->b || !w) omg::fail(omg::E_INVALID, "null argument");
+        for (const auto& kv : w->w.tensors) b->b->push(kv.first, kv.second);
+    });
+}
+
+size_t omg_builder_missing(omg_builder* b, char* buf, size_t len) {
+    if (!b || !b->b) return 0;
+    const auto m = b->b->missing();
+    std::string s;
+    for (const auto& n : m) s += n + "\n";
+    if (buf && len) {
+        const size_t k = std::min(len - 1, s.size());
+        std::memcpy(buf, s.data(), k);
+        buf[k] = 0;
+    }
+    return m.size();
+}
+
+omg_engine* omg_builder_finish(omg_builder* b, size_t capacity, size_t max_rows) {
+    omg_engine* out = nullptr;
+    guard([&] {
+        if (!b || !b->b) omg::fail(omg::E_INVALID, "null builder");
+        std::unique_ptr<omg::Builder> keep = std::move(b->b);
+        delete b;
+        out = new omg_engine{keep->finish(int64_t(capacity), int64_t(max_rows))};
+    });
+    return out;
+}
+
+void omg_builder_free(omg_builder* b) { delete b; }
+
+omg_engine* omg_open_dir(const char* dir, size_t capacity, size_t max_rows) {
+    omg_engine* out = nullptr;
+    guard([&] {
+        if (!dir) omg::fail(omg::E_INVALID, "null dir");
+        omg::Weights w = omg::load_dir(dir);
+        omg::Builder b(w.config);
+        for (auto& kv : w.tensors) b.push(kv.first, kv.second);
+        out = new omg_engine{b.finish(int64_t(capacity), int64_t(max_rows))};
+    });
+    return out;
+}
+
+void omg_close(omg_engine* e) { delete e; }
+
+int omg_config(const omg_engine* e, omg_config_t* out) {
+    return guard([&] {
+        if (!e || !e->e || !out) omg::fail(omg::E_INVALID, "null argument");
+        const omg::Config& c = e->e->config();
+        out->vocab = uint32_t(c.vocab);
+        out->d = uint32_t(c.d);
+        out->layers = uint32_t(c.layers);
+        out->heads = uint32_t(c.heads);
+        out->kv_heads = uint32_t(c.kv_heads);
+        out->head_dim = uint32_t(c.max_head_dim());
+        out->bos = c.bos;
+        out->capacity = uint64_t(e->e->capacity());
+        out->max_rows = uint64_t(e->e->max_rows());
+    });
+}
+
+int omg_warmup(omg_engine* e) {
+    return guard([&] { eng(e).warmup(); });
+}
+
+int omg_evaluate_groups(omg_engine* e, const omg_group* groups, size_t ngroups, int want,
+                        const uint32_t* label_ids, size_t nlabels, float* out, size_t out_floats,
+                        int* prefix_sources) {
+    return guard([&] {
+        Groups g = convert(groups, ngroups);
+        if (!out && out_floats) omg::fail(omg::E_INVALID, "null output");
+        eng(e).evaluate_groups(g.groups.data(), int64_t(ngroups), want, label_ids, int64_t(nlabels), out,
+                               int64_t(out_floats), prefix_sources);
+    });
+}
+
+int omg_evaluate(omg_engine* e, const uint32_t* prefix, size_t prefix_len, const omg_branch* branches,
+                 size_t nbranches, int want, const uint32_t* label_ids, size_t nlabels, float* out,
+                 size_t out_floats) {
+    const omg_group g{prefix, prefix_len, branches, nbranches};
+    return omg_evaluate_groups(e, &g, 1, want, label_ids, nlabels, out, out_floats, nullptr);
+}
+
+int omg_prefix_source(const omg_engine* e) { return (e && e->e) ? e->e->prefix_source() : OMG_SRC_NONE; }
+
+int omg_is_resident(const omg_engine* e, const uint32_t* prefix, size_t n) {
+    return (e && e->e && (prefix || !n)) ? int(e->e->is_resident(prefix, int64_t(n))) : 0;
+}
+
+void omg_evict_resident(omg_engine* e) {
+    if (e && e->e) e->e->evict_resident();
+}
+
+int omg_set_state_cache(omg_engine* e, size_t bytes, const char* dir, const char* model_id) {
+    return guard([&] { eng(e).set_state_cache(bytes, dir ? dir : "", model_id ? model_id : ""); });
+}
+
+int omg_save_state(omg_engine* e, const uint32_t* prefix, size_t n, const char* model_id, uint8_t** bytes,
+                   size_t* len) {
+    return guard([&] {
+        if (!bytes || !len || (n && !prefix)) omg::fail(omg::E_INVALID, "null argument");
+        const omg::SavedState s = eng(e).save_state(prefix, int64_t(n));
+        const std::vector<uint8_t> b = s.to_bytes(model_id ? model_id : eng(e).model_id());
+        uint8_t* p = static_cast<uint8_t*>(std::malloc(b.size() ? b.size() : 1));
+        if (!p) omg::fail(omg::E_INVALID, "out of host memory");
+        std::memcpy(p, b.data(), b.size());
+        *bytes = p;
+        *len = b.size();
+    });
+}
+
+int omg_restore_state(omg_engine* e, const uint8_t* bytes, size_t len, const char* model_id) {
+    return guard([&] {
+        if (!bytes && len) omg::fail(omg::E_INVALID, "null bytes");
+        const omg::SavedState s =
+            omg::SavedState::from_bytes(bytes, len, model_id ? model_id : eng(e).model_id());
+        eng(e).restore_state(s);
+    });
+}
+
+void omg_free_bytes(uint8_t* p) { std::free(p); }
+
+int omg_quantize(int dtype, const float* values, size_t n, uint8_t* data, uint8_t* scales) {
+    return guard([&] {
+        if (!values || !data || !scales) omg::fail(omg::E_INVALID, "null argument");
+        const std::vector<int64_t> shape{int64_t(n)};
+        omg::QTensor t;
+        if (dtype == OMG_DTYPE_Q8)
+            t = omg::quantize_q8(shape, values);
+        else if (dtype == OMG_DTYPE_Q4)
+            t = omg::quantize_q4(shape, values);
+        else
+            omg::fail(omg::E_INVALID, "omg_quantize: dtype must be Q8 or Q4");
+        std::memcpy(data, t.data.data(), t.data.size());
+        std::memcpy(scales, t.scales.data(), t.scales.size());
+    });
+}
+
+int omg_pack(const omg_group* groups, size_t ngroups, size_t first, int resident, uint32_t* ids,
+             int32_t* meta, int64_t* wanted, size_t* n_ids, size_t* n_wanted) {
+    return guard([&] {
+        if (!n_ids || !n_wanted) omg::fail(omg::E_INVALID, "null sizes");
+        if (first >= ngroups) omg::fail(omg::E_INVALID, "first group out of range");
+        Groups g = convert(groups, ngroups);
+        const omg::Packed pk = omg::pack_groups(g.groups.data(), int64_t(ngroups), int64_t(first), resident != 0);
+        if (pk.ids.size() > *n_ids || pk.wanted.size() > *n_wanted)
+            omg::fail(omg::E_CAPACITY, "omg_pack: output arrays too small");
+        std::memcpy(ids, pk.ids.data(), pk.ids.size() * 4);
+        std::memcpy(meta, pk.meta.data(), pk.meta.size() * 4);
+        for (size_t r = 0; r < pk.wanted.size(); ++r)
+            for (int k = 0; k < 4; ++k) wanted[4 * r + size_t(k)] = pk.wanted[r][size_t(k)];
+        *n_ids = pk.ids.size();
+        *n_wanted = pk.wanted.size();
+    });
+}
+
+uint64_t omg_state_key(const char* model_id, const uint32_t* prefix, size_t n) {
+    return omg::state_key(model_id ? model_id : "", prefix, int64_t(n));
+}
+
+int omg_state_check(const uint8_t* bytes, size_t len, const char* model_id, size_t* prefix_len, size_t* nlayers) {
+    return guard([&] {
+        if (!bytes && len) omg::fail(omg::E_INVALID, "null bytes");
+        const omg::SavedState s = omg::SavedState::from_bytes(bytes, len, model_id ? model_id : "");
+        if (prefix_len) *prefix_len = s.prefix.size();
+        if (nlayers) *nlayers = s.layers.size();
+    });
+}
+
+int omg_pass_prepare(omg_engine* e, const omg_group* groups, size_t ngroups, int want, const uint32_t* label_ids,
+                     size_t nlabels, int first_resident) {
+    return guard([&] {
+        Groups g = convert(groups, ngroups);
+        eng(e).prepare(g.groups.data(), int64_t(ngroups), want, label_ids, int64_t(nlabels), first_resident != 0);
+    });
+}
+
+int omg_pass_launch(omg_engine* e) {
+    return guard([&] { eng(e).launch_prepared(); });
+}
+
+int omg_sync(omg_engine* e) {
+    return guard([&] { eng(e).sync(); });
+}
+
+int omg_profile(omg_engine* e, int on) {
+    return guard([&] { eng(e).set_profile(on != 0); });
+}
+
+size_t omg_profile_report(omg_engine* e, char* buf, size_t len) {
+    if (!e || !e->e) return 0;
+    const std::string s = e->e->profile_report();
+    if (buf && len) {
+        const size_t k = std::min(len - 1, s.size());
+        std::memcpy(buf, s.data(), k);
+        buf[k] = 0;
+    }
+    return s.size();
+}
+
+omg_weight* omg_weight_upload(int dtype, int64_t rows, int64_t cols, const void* data, const void* scales) {
+    omg_weight* out = nullptr;
+    guard([&] {
+        if (rows <= 0 || cols <= 0 || cols % 32) omg::fail(omg::E_INVALID, "weight: bad shape");
+        const int64_t n = rows * cols;
+        const int64_t shape[2] = {rows, cols};
+        const size_t nbytes = size_t(omg::payload_bytes(omg::Dtype(dtype), n));
+        omg::QTensor t = make_tensor(dtype, shape, 2, data, nbytes, scales, dtype == OMG_DTYPE_F16 ? 0 : size_t(n / 32 * 2));
+        auto w = std::make_unique<omg_weight>();
+        w->t.w.dtype = dtype;
+        w->t.w.rows = rows;
+        w->t.w.cols = cols;
+        if (dtype == OMG_DTYPE_Q4) {
+            std::vector<uint8_t> rep(t.data.size());
+            omg::repack_q4(t.data.data(), rep.data(), n);
+            w->t.data = omg::DevBuf(rep.size());
+            OMG_HIP(hipMemcpy(w->t.data.p, rep.data(), rep.size(), hipMemcpyHostToDevice));
+        } else {
+            w->t.data = omg::DevBuf(t.data.size());
+            OMG_HIP(hipMemcpy(w->t.data.p, t.data.data(), t.data.size(), hipMemcpyHostToDevice));
+        }
+        if (dtype != OMG_DTYPE_F16) {
+            w->t.scales = omg::DevBuf(t.scales.size());
+            OMG_HIP(hipMemcpy(w->t.scales.p, t.scales.data(), t.scales.size(), hipMemcpyHostToDevice));
+        }
+        w->t.w.data = w->t.data.p;
+        w->t.w.scales = w->t.scales.as<uint16_t>();
+        out = w.release();
+    });
+    return out;
+}
+
+void omg_weight_free(omg_weight* w) { delete w; }
+
+int omg_dev_gemm(const omg_weight* w, const void* x_f16, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                 void* stream) {
+    return guard([&] {
+        if (!w || !x_f16 || !y) omg::fail(omg::E_INVALID, "null argument");
+        omg::launch_gemm(static_cast<hipStream_t>(stream), static_cast<const omg::half_t*>(x_f16), ldx, w->t.w, y, ldy,
+                         m);
+    });
+}
+
+int omg_dev_gemm_geglu(const omg_weight* wg, const omg_weight* wu, const void* x_f16, int64_t ldx, int64_t m,
+                       void* act_f16, int64_t ldact, void* stream) {
+    return guard([&] {
+        if (!wg || !wu || !x_f16 || !act_f16) omg::fail(omg::E_INVALID, "null argument");
+        omg::launch_gemm_geglu(static_cast<hipStream_t>(stream), static_cast<const omg::half_t*>(x_f16), ldx, wg->t.w,
+                               wu->t.w, static_cast<omg::half_t*>(act_f16), ldact, m);
+    });
+}
+
+int omg_dev_embed_norm(const omg_weight* embed, const uint32_t* ids, int64_t t, float scale, const float* w,
+                       float eps, float* x, void* hn_f16, void* stream) {
+    return guard([&] {
+        if (!embed || !ids || !w || !x || !hn_f16) omg::fail(omg::E_INVALID, "null argument");
+        omg::launch_embed_norm(static_cast<hipStream_t>(stream), embed->t.w, ids, t, scale, w, eps, x,
+                               static_cast<omg::half_t*>(hn_f16));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,751 @@
+// The decision-path engine: request packing, the per-layer launch plan,
+// readout, resident prefix and the f16 K/V state machinery
+// (crates/omg-wgpu/src/engine.rs).
+#include "engine.h"
+
+#include <sys/stat.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <fstream>
+
+namespace omg {
+
+// ------------------------------------------------------------------ pack
+
+Packed pack_groups(const GroupIn* groups, int64_t n, int64_t first, bool resident) {
+    Packed pk;
+    for (int64_t g = 0; g < n; ++g) {
+        pk.total += groups[g].prefix_len;
+        for (int64_t b = 0; b < groups[g].nbranches; ++b) pk.total += groups[g].branches[b].ntokens;
+    }
+    if (n == 0 || pk.total == 0) fail(E_INVALID, "empty request");
+    const int64_t p0 = groups[first].prefix_len;
+    pk.base = resident ? p0 : 0;
+    pk.ids.reserve(size_t(pk.total - pk.base));
+    pk.meta.reserve(size_t(4 * (pk.total - pk.base)));
+    auto push = [&](int64_t pos, int32_t seq, int64_t row_lo, uint32_t tok) {
+        const int64_t row = pk.base + int64_t(pk.ids.size());
+        pk.meta.push_back(int32_t(pos));
+        pk.meta.push_back(seq);
+        pk.meta.push_back(int32_t(row_lo));
+        pk.meta.push_back(int32_t(row + 1));
+        pk.ids.push_back(tok);
+    };
+    for (int64_t k = 0; k < n; ++k) {
+        const int64_t gi = k == 0 ? first : (k <= first ? k - 1 : k);
+        const GroupIn& g = groups[gi];
+        if (g.nbranches >= (int64_t(1) << SEQ_GROUP_SHIFT))
+            fail(E_CAPACITY, std::to_string(g.nbranches) + " branches in one group; the engine addresses at most " +
+                                 std::to_string((1 << SEQ_GROUP_SHIFT) - 1));
+        const int32_t seq_hi = int32_t(k << SEQ_GROUP_SHIFT);
+        const int64_t row_lo = k == 0 ? 0 : pk.base + int64_t(pk.ids.size());
+        if (!(k == 0 && pk.base > 0)) {
+            pk.decoded.push_back({gi, pk.base + int64_t(pk.ids.size())});
+            for (int64_t i = 0; i < g.prefix_len; ++i) push(i, seq_hi, row_lo, g.prefix[i]);
+        }
+        for (int64_t bi = 0; bi < g.nbranches; ++bi) {
+            const BranchIn& b = g.branches[bi];
+            const int64_t start = int64_t(pk.ids.size());
+            for (int64_t j = 0; j < b.ntokens; ++j)
+                push(g.prefix_len + j, seq_hi | int32_t(bi + 1), row_lo, b.tokens[j]);
+            for (int64_t s = 0; s < b.nwant; ++s) {
+                if (int64_t(b.want[s]) >= b.ntokens)
+                    fail(E_INVALID, "branch " + std::to_string(bi) + ": wanted position " + std::to_string(b.want[s]) +
+                                        " past its " + std::to_string(b.ntokens) + " tokens");
+                pk.wanted.push_back({gi, bi, s, start + int64_t(b.want[s])});
+            }
+        }
+    }
+    return pk;
+}
+
+// ----------------------------------------------------------------- state
+
+size_t SavedState::byte_len() const {
+    size_t n = prefix.size() * 4;
+    for (const Layer& l : layers) n += l.bytes.size();
+    return n;
+}
+
+static void put_u32(std::vector<uint8_t>& o, uint32_t v) {
+    for (int i = 0; i < 4; ++i) o.push_back(uint8_t(v >> (8 * i)));
+}
+
+std::vector<uint8_t> SavedState::to_bytes(const std::string& model_id) const {
+    std::vector<uint8_t> out;
+    out.reserve(byte_len() + 64 + model_id.size());
+    const char magic[6] = {'G', 'R', 'W', 'S', '1', '\0'};
+    out.insert(out.end(), magic, magic + 6);
+    put_u32(out, uint32_t(model_id.size()));
+    out.insert(out.end(), model_id.begin(), model_id.end());
+    put_u32(out, uint32_t(prefix.size()));
+    for (uint32_t t : prefix) put_u32(out, t);
+    put_u32(out, uint32_t(layers.size()));
+    for (const Layer& l : layers) {
+        put_u32(out, l.layer);
+        put_u32(out, l.row0);
+        put_u32(out, uint32_t(l.bytes.size()));
+        out.insert(out.end(), l.bytes.begin(), l.bytes.end());
+    }
+    return out;
+}
+
+SavedState SavedState::from_bytes(const uint8_t* b, size_t n, const std::string& model_id) {
+    size_t at = 0;
+    auto take = [&](size_t k) {
+        if (at + k > n) fail(E_STATE, "state file truncated");
+        const uint8_t* p = b + at;
+        at += k;
+        return p;
+    };
+    auto u32 = [&]() {
+        const uint8_t* p = take(4);
+        return uint32_t(p[0]) | uint32_t(p[1]) << 8 | uint32_t(p[2]) << 16 | uint32_t(p[3]) << 24;
+    };
+    if (std::memcmp(take(6), "GRWS1\0", 6) != 0) fail(E_STATE, "not a omg state file");
+    const uint32_t idn = u32();
+    const uint8_t* id = take(idn);
+    if (std::string(reinterpret_cast<const char*>(id), idn) != model_id)
+        fail(E_STATE, "state file is for a different model");
+    SavedState s;
+    const uint32_t np = u32();
+    const uint8_t* pp = take(size_t(np) * 4);
+    for (uint32_t i = 0; i < np; ++i)
+        s.prefix.push_back(uint32_t(pp[4 * i]) | uint32_t(pp[4 * i + 1]) << 8 | uint32_t(pp[4 * i + 2]) << 16 |
+                           uint32_t(pp[4 * i + 3]) << 24);
+    const uint32_t nl = u32();
+    for (uint32_t i = 0; i < nl; ++i) {
+        Layer l;
+        l.layer = u32();
+        l.row0 = u32();
+        const uint32_t len = u32();
+        const uint8_t* d = take(len);
+        l.bytes.assign(d, d + len);
+        s.layers.push_back(std::move(l));
+    }
+    return s;
+}
+
+std::optional<SavedState> StateCache::get(const std::vector<uint32_t>& prefix) {
+    for (size_t i = 0; i < entries.size(); ++i) {
+        if (entries[i].prefix == prefix) {
+            SavedState s = std::move(entries[i]);
+            entries.erase(entries.begin() + long(i));
+            entries.push_back(s);
+            return s;
+        }
+    }
+    return std::nullopt;
+}
+
+void StateCache::put(SavedState s) {
+    const size_t len = s.byte_len();
+    if (len > budget) return;
+    for (size_t i = 0; i < entries.size(); ++i)
+        if (entries[i].prefix == s.prefix) {
+            used -= entries[i].byte_len();
+            entries.erase(entries.begin() + long(i));
+            break;
+        }
+    while (used + len > budget && !entries.empty()) {
+        used -= entries.front().byte_len();
+        entries.erase(entries.begin());
+    }
+    used += len;
+    entries.push_back(std::move(s));
+}
+
+uint64_t state_key(const std::string& model_id, const uint32_t* prefix, int64_t n) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    auto eat = [&](uint8_t b) {
+        h ^= b;
+        h *= 0x00000100000001b3ull;
+    };
+    for (char c : model_id) eat(uint8_t(c));
+    eat(0);
+    for (int64_t i = 0; i < n; ++i)
+        for (int s = 0; s < 4; ++s) eat(uint8_t(prefix[i] >> (8 * s)));
+    return h;
+}
+
+// ---------------------------------------------------------------- device
+
+DevBuf::DevBuf(size_t n, bool zero) : bytes(n) {
+    OMG_HIP(hipMalloc(&p, std::max<size_t>(n, 16)));
+    if (zero) OMG_HIP(hipMemset(p, 0, std::max<size_t>(n, 16)));
+}
+DevBuf::~DevBuf() {
+    if (p) (void)hipFree(p);
+}
+DevBuf& DevBuf::operator=(DevBuf&& o) noexcept {
+    if (this != &o) {
+        if (p) (void)hipFree(p);
+        p = o.p;
+        bytes = o.bytes;
+        o.p = nullptr;
+        o.bytes = 0;
+    }
+    return *this;
+}
+
+static DevBuf upload_bytes(const void* src, size_t n) {
+    DevBuf b(n);
+    if (n) OMG_HIP(hipMemcpy(b.p, src, n, hipMemcpyHostToDevice));
+    return b;
+}
+
+// --------------------------------------------------------------- builder
+
+Builder::Builder(Config cfg) : cfg_(std::move(cfg)) {
+    cfg_.validate();
+    for (const TensorSpec& s : cfg_.tensors()) expected_[s.name] = s.shape;
+}
+
+void Builder::push(const std::string& name, const QTensor& t) {
+    auto it = expected_.find(name);
+    if (it == expected_.end()) fail(E_INVALID, "unexpected tensor " + name);
+    if (t.shape != it->second) fail(E_INVALID, name + ": shape mismatch");
+    const int64_t n = t.numel();
+    if (int64_t(t.data.size()) != payload_bytes(t.dtype, n)) fail(E_INVALID, name + ": payload size mismatch");
+    if (t.dtype != F16 && int64_t(t.scales.size()) != n / BLOCK * 2) fail(E_INVALID, name + ": scale size mismatch");
+    if (t.shape.size() == 1) {
+        // Norm weights are applied as (offset + w) in f32 (rmsnorm.wgsl:34-39).
+        if (t.dtype != F16) fail(E_INVALID, name + ": 1-D tensors must be f16");
+        std::vector<float> v(static_cast<size_t>(n));
+        for (int64_t i = 0; i < n; ++i) v[size_t(i)] = cfg_.norm_offset + t.get(i);
+        norms_[name] = upload_bytes(v.data(), v.size() * 4);
+        linears_.erase(name);
+        return;
+    }
+    if (t.shape[1] % 32 != 0) fail(E_INVALID, name + ": inner dimension is not a multiple of 32");
+    DevTensor d;
+    d.w.dtype = int(t.dtype);
+    d.w.rows = t.shape[0];
+    d.w.cols = t.shape[1];
+    if (t.dtype == Q4) {
+        std::vector<uint8_t> rep(t.data.size());
+        repack_q4(t.data.data(), rep.data(), n);
+        d.data = upload_bytes(rep.data(), rep.size());
+    } else {
+        d.data = upload_bytes(t.data.data(), t.data.size());
+    }
+    if (t.dtype != F16) d.scales = upload_bytes(t.scales.data(), t.scales.size());
+    d.w.data = d.data.p;
+    d.w.scales = d.scales.as<uint16_t>();
+    linears_[name] = std::move(d);
+    norms_.erase(name);
+}
+
+std::vector<std::string> Builder::missing() const {
+    std::vector<std::string> v;
+    for (const auto& kv : expected_)
+        if (!linears_.count(kv.first) && !norms_.count(kv.first)) v.push_back(kv.first);
+    return v;
+}
+
+std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
+    const auto miss = missing();
+    if (!miss.empty()) {
+        std::string m = std::to_string(miss.size()) + " tensors missing, e.g.";
+        for (size_t i = 0; i < miss.size() && i < 4; ++i) m += " " + miss[i];
+        fail(E_MISSING, m);
+    }
+    if (capacity <= 0 || max_rows <= 0) fail(E_INVALID, "capacity and max_rows must be positive");
+    std::unique_ptr<Engine> e(new Engine());
+    Engine& E = *e;
+    const Config& c = cfg_;
+    E.cfg_ = c;
+    E.capacity_ = capacity;
+    E.max_rows_ = max_rows;
+    E.cap_pad_ = (capacity + 63) / 64 * 64;
+    OMG_HIP(hipStreamCreateWithFlags(&E.stream_, hipStreamNonBlocking));
+    auto take_lin = [&](const std::string& n) { return std::move(linears_.at(n)); };
+    auto take_norm = [&](const std::string& n) { return std::move(norms_.at(n)); };
+    if (linears_.count("embed") == 0) fail(E_INVALID, "embed must be a 2-D tensor");
+    E.embed_ = take_lin("embed");
+    E.final_norm_ = take_norm("final_norm");
+    for (int64_t l = 0; l < c.layers; ++l) {
+        auto n = [&](const char* s) { return "blk." + std::to_string(l) + "." + s; };
+        Engine::Layer L;
+        L.qkv = take_lin(n("qkv"));
+        L.o = take_lin(n("o"));
+        L.gate = take_lin(n("gate"));
+        L.up = take_lin(n("up"));
+        L.down = take_lin(n("down"));
+        if (L.gate.w.dtype != L.up.w.dtype)
+            fail(E_INVALID, "layer " + std::to_string(l) + ": gate and up projections must share a storage type");
+        L.attn_norm = take_norm(n("attn_norm"));
+        L.q_norm = take_norm(n("q_norm"));
+        if (c.has_kv(l)) L.k_norm = take_norm(n("k_norm"));
+        L.post_attn_norm = take_norm(n("post_attn_norm"));
+        L.ffn_norm = take_norm(n("ffn_norm"));
+        L.post_ffn_norm = take_norm(n("post_ffn_norm"));
+        E.layers_.push_back(std::move(L));
+    }
+    // RoPE inverse frequencies theta^(-i / (hd/2)) (reference.rs:159-168),
+    // one table per attention type.
+    const int64_t hd = c.max_head_dim();
+    std::vector<float> fl(size_t(hd / 2)), fg(size_t(hd / 2));
+    for (int64_t i = 0; i < hd / 2; ++i) {
+        fl[size_t(i)] = std::pow(c.theta_local, -float(i) / float(hd / 2));
+        fg[size_t(i)] = std::pow(c.theta_global, -float(i) / float(hd / 2));
+    }
+    E.inv_freq_local_ = upload_bytes(fl.data(), fl.size() * 4);
+    E.inv_freq_global_ = upload_bytes(fg.data(), fg.size() * 4);
+    const int64_t cap = capacity, d = c.d;
+    E.ids_ = DevBuf(size_t(cap) * 4);
+    E.meta_ = DevBuf(size_t(E.cap_pad_) * 16, true);
+    E.x_ = DevBuf(size_t(cap * d) * 4);
+    E.hn_ = DevBuf(size_t(cap * d) * 2);
+    E.qkv_ = DevBuf(size_t(cap * c.max_qkv()) * 4);
+    E.q16_ = DevBuf(size_t(cap * c.heads * hd) * 2);
+    E.attn_ = DevBuf(size_t(cap * c.heads * hd) * 2);
+    E.a_ = DevBuf(size_t(cap * d) * 4);
+    E.act_ = DevBuf(size_t(cap * c.max_ff()) * 2);
+    E.rows_ = DevBuf(size_t(max_rows * d) * 4);
+    const int64_t width = std::max(c.vocab, d);
+    E.logits_ = DevBuf(size_t(max_rows * width) * 4);
+    E.wanted_ = DevBuf(size_t(max_rows) * 4);
+    E.labels_ = DevBuf(size_t(c.vocab) * 4);
+    E.kv_stage_ = DevBuf(size_t(E.cap_pad_ * 2 * c.kv_heads * hd) * 2);
+    // The K/V cache starts zeroed: a masked key's probability is exactly 0
+    // and its V row must be finite for the 0 * V product to vanish.
+    for (int64_t l = 0; l < c.layers; ++l) {
+        if (c.has_kv(l)) {
+            const size_t bytes = size_t(c.kv_heads * E.cap_pad_ * c.head_dim[size_t(l)]) * 2;
+            E.kc_.emplace_back(bytes, true);
+            E.vt_.emplace_back(bytes, true);
+        } else {
+            E.kc_.emplace_back();
+            E.vt_.emplace_back();
+        }
+    }
+    E.h_in_bytes_ = size_t(cap) * 4 + size_t(cap) * 16 + size_t(max_rows) * 4 + size_t(c.vocab) * 4;
+    OMG_HIP(hipHostMalloc(&E.h_in_, E.h_in_bytes_, hipHostMallocDefault));
+    E.h_out_bytes_ = size_t(max_rows * width) * 4;
+    OMG_HIP(hipHostMalloc(&E.h_out_, E.h_out_bytes_, hipHostMallocDefault));
+    OMG_HIP(hipDeviceSynchronize());
+    return e;
+}
+
+// ---------------------------------------------------------------- engine
+
+Engine::~Engine() {
+    for (Timed& t : pending_) {
+        (void)hipEventDestroy(t.a);
+        (void)hipEventDestroy(t.b);
+    }
+    for (hipEvent_t ev : event_pool_) (void)hipEventDestroy(ev);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (h_in_) (void)hipHostFree(h_in_);
+    if (h_out_) (void)hipHostFree(h_out_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+template <class F>
+void Engine::step(const char* name, F&& f) {
+    if (!profile_) {
+        f();
+        return;
+    }
+    auto ev = [&]() {
+        if (event_pool_.empty()) {
+            hipEvent_t e;
+            OMG_HIP(hipEventCreate(&e));
+            return e;
+        }
+        hipEvent_t e = event_pool_.back();
+        event_pool_.pop_back();
+        return e;
+    };
+    Timed t{name, ev(), ev()};
+    OMG_HIP(hipEventRecord(t.a, stream_));
+    f();
+    OMG_HIP(hipEventRecord(t.b, stream_));
+    pending_.push_back(t);
+}
+
+void Engine::collect_profile() {
+    for (Timed& t : pending_) {
+        float ms = 0.0f;
+        OMG_HIP(hipEventElapsedTime(&ms, t.a, t.b));
+        auto& tot = totals_[t.name];
+        tot.first += 1;
+        tot.second += double(ms);
+        event_pool_.push_back(t.a);
+        event_pool_.push_back(t.b);
+    }
+    pending_.clear();
+}
+
+void Engine::set_profile(bool on) {
+    sync();
+    profile_ = on;
+    totals_.clear();
+}
+
+std::string Engine::profile_report() const {
+    std::string s;
+    char line[256];
+    for (const auto& kv : totals_) {
+        std::snprintf(line, sizeof line, "%s %lld %.6f\n", kv.first.c_str(), (long long)kv.second.first,
+                      kv.second.second);
+        s += line;
+    }
+    return s;
+}
+
+void Engine::sync() {
+    OMG_HIP(hipStreamSynchronize(stream_));
+    if (!pending_.empty()) collect_profile();
+}
+
+std::pair<int64_t, int64_t> Engine::state_rows(int64_t layer, int64_t p) const {
+    if (cfg_.sliding[size_t(layer)] && cfg_.window > 0) return {std::max<int64_t>(0, p - cfg_.window), p};
+    return {0, p};
+}
+
+bool Engine::is_resident(const uint32_t* prefix, int64_t n) const {
+    if (n == 0 || !resident_) return false;
+    return int64_t(resident_->size()) == n && std::equal(prefix, prefix + n, resident_->begin());
+}
+
+std::pair<int64_t, int> Engine::admit(const GroupIn* groups, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        if (is_resident(groups[i].prefix, groups[i].prefix_len)) return {i, SRC_RESIDENT};
+    for (int64_t i = 0; i < n; ++i) {
+        const int src = restore_from_cache(groups[i].prefix, groups[i].prefix_len);
+        if (src != SRC_NONE) return {i, src};
+    }
+    return {0, SRC_NONE};
+}
+
+Packed Engine::pack_checked(const GroupIn* groups, int64_t n, int64_t first, bool resident) const {
+    int64_t total = 0;
+    for (int64_t g = 0; g < n; ++g) {
+        total += groups[g].prefix_len;
+        for (int64_t b = 0; b < groups[g].nbranches; ++b) total += groups[g].branches[b].ntokens;
+    }
+    if (total > capacity_)
+        fail(E_CAPACITY, std::to_string(total) + " tokens exceed the engine capacity " + std::to_string(capacity_));
+    Packed pk = pack_groups(groups, n, first, resident);
+    if (int64_t(pk.wanted.size()) > max_rows_)
+        fail(E_CAPACITY, std::to_string(pk.wanted.size()) + " rows requested, engine reads back at most " +
+                             std::to_string(max_rows_));
+    for (uint32_t id : pk.ids)
+        if (int64_t(id) >= cfg_.vocab)
+            fail(E_INVALID, "token id " + std::to_string(id) + " outside the vocabulary of " + std::to_string(cfg_.vocab));
+    return pk;
+}
+
+void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
+    const int64_t t = pk.total - pk.base, nr = int64_t(pk.wanted.size());
+    uint8_t* h = static_cast<uint8_t*>(h_in_);
+    // The previous pass may still read the staging buffer.
+    OMG_HIP(hipStreamSynchronize(stream_));
+    size_t off = 0;
+    std::memcpy(h + off, pk.ids.data(), size_t(t) * 4);
+    OMG_HIP(hipMemcpyAsync(ids_.p, h + off, size_t(t) * 4, hipMemcpyHostToDevice, stream_));
+    off += size_t(capacity_) * 4;
+    std::memcpy(h + off, pk.meta.data(), size_t(t) * 16);
+    OMG_HIP(hipMemcpyAsync(meta_.as<uint8_t>() + pk.base * 16, h + off, size_t(t) * 16, hipMemcpyHostToDevice, stream_));
+    off += size_t(capacity_) * 16;
+    int32_t* w = reinterpret_cast<int32_t*>(h + off);
+    for (int64_t r = 0; r < nr; ++r) w[r] = int32_t(pk.wanted[size_t(r)][3]);
+    if (nr) OMG_HIP(hipMemcpyAsync(wanted_.p, w, size_t(nr) * 4, hipMemcpyHostToDevice, stream_));
+    off += size_t(max_rows_) * 4;
+    if (nlabels > 0) {
+        if (nlabels > cfg_.vocab) fail(E_INVALID, "more labels than vocabulary rows");
+        for (int64_t i = 0; i < nlabels; ++i)
+            if (int64_t(labels[i]) >= cfg_.vocab) fail(E_INVALID, "label id outside the vocabulary");
+        std::memcpy(h + off, labels, size_t(nlabels) * 4);
+        OMG_HIP(hipMemcpyAsync(labels_.p, h + off, size_t(nlabels) * 4, hipMemcpyHostToDevice, stream_));
+    }
+}
+
+void Engine::forward(int64_t t, int64_t base) {
+    const Config& c = cfg_;
+    const int64_t d = c.d;
+    step("embed_norm", [&] {
+        launch_embed_norm(stream_, embed_.w, ids_.as<uint32_t>(), t, std::sqrt(float(d)),
+                          layers_[0].attn_norm.as<float>(), c.eps, x_.as<float>(), hn_.as<half_t>());
+    });
+    for (int64_t l = 0; l < c.layers; ++l) {
+        Layer& L = layers_[size_t(l)];
+        const int64_t hd = c.head_dim[size_t(l)], qw = c.qkv_width(l), ff = c.ff[size_t(l)];
+        const int64_t src = c.kv_source[size_t(l)];
+        step("mm_qkv", [&] { launch_gemm(stream_, hn_.as<half_t>(), d, L.qkv.w, qkv_.as<float>(), qw, t); });
+        step("qk_prep", [&] {
+            QkArgs q{};
+            q.qkv = qkv_.as<float>();
+            q.qkv_stride = qw;
+            q.meta = meta_.as<int32_t>();
+            q.q_norm = L.q_norm.as<float>();
+            q.k_norm = c.has_kv(l) ? L.k_norm.as<float>() : nullptr;
+            q.inv_freq = (c.sliding[size_t(l)] ? inv_freq_local_ : inv_freq_global_).as<float>();
+            q.rope_dims = c.rope_dims[size_t(l)];
+            q.eps = c.eps;
+            q.q_scale = c.query_scale;
+            q.heads = int(c.heads);
+            q.kv_heads = int(c.kv_heads);
+            q.hd = int(hd);
+            q.has_kv = c.has_kv(l);
+            q.v_norm = c.v_norm;
+            q.t = t;
+            q.base = base;
+            q.cap_pad = cap_pad_;
+            q.q16 = q16_.as<half_t>();
+            q.kc = kc_[size_t(src)].as<half_t>();
+            q.vt = vt_[size_t(src)].as<half_t>();
+            launch_qk_prep(stream_, q);
+        });
+        step("attention", [&] {
+            AttnArgs a{};
+            a.q16 = q16_.as<half_t>();
+            a.kc = kc_[size_t(src)].as<half_t>();
+            a.vt = vt_[size_t(src)].as<half_t>();
+            a.meta = meta_.as<int32_t>();
+            a.out = attn_.as<half_t>();
+            a.t = t;
+            a.base = base;
+            a.cap_pad = cap_pad_;
+            a.heads = int(c.heads);
+            a.kv_heads = int(c.kv_heads);
+            a.hd = int(hd);
+            a.window = c.sliding[size_t(l)] ? int(c.window) : 0;
+            launch_attention(stream_, a);
+        });
+        step("mm_o", [&] {
+            launch_gemm(stream_, attn_.as<half_t>(), c.heads * hd, L.o.w, a_.as<float>(), d, t);
+        });
+        step("norm", [&] {
+            launch_residual_norm(stream_, a_.as<float>(), L.post_attn_norm.as<float>(), x_.as<float>(),
+                                 L.ffn_norm.as<float>(), hn_.as<half_t>(), t, d, c.eps, 1.0f);
+        });
+        step("mm_gate_up", [&] {
+            launch_gemm_geglu(stream_, hn_.as<half_t>(), d, L.gate.w, L.up.w, act_.as<half_t>(), ff, t);
+        });
+        step("mm_down", [&] { launch_gemm(stream_, act_.as<half_t>(), ff, L.down.w, a_.as<float>(), d, t); });
+        // The last layer's stream is normed at the wanted rows only (readout).
+        const float* next = l + 1 < c.layers ? layers_[size_t(l + 1)].attn_norm.as<float>() : nullptr;
+        step("norm", [&] {
+            launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), next,
+                                 hn_.as<half_t>(), t, d, c.eps, 1.0f);
+        });
+    }
+}
+
+void Engine::readout(const PassPlan& p) {
+    if (p.nrows == 0) return;
+    const Config& c = cfg_;
+    step("final_rows", [&] {
+        launch_final_rows(stream_, x_.as<float>(), wanted_.as<int32_t>(), p.nrows, c.d, final_norm_.as<float>(),
+                          c.eps, rows_.as<float>());
+    });
+    if (p.want == WANT_LOGITS) {
+        step("logits", [&] {
+            launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, nullptr, c.vocab, c.softcap,
+                          logits_.as<float>());
+        });
+    } else if (p.want == WANT_LABELS) {
+        step("logits", [&] {
+            launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, labels_.as<uint32_t>(), p.nlabels,
+                          c.softcap, logits_.as<float>());
+        });
+    }
+}
+
+void Engine::evaluate_groups(const GroupIn* groups, int64_t n, int want, const uint32_t* labels,
+                             int64_t nlabels, float* out, int64_t out_floats, int* sources) {
+    if (n <= 0) fail(E_INVALID, "empty request");
+    if (want != WANT_LOGITS && want != WANT_HIDDEN && want != WANT_LABELS) fail(E_INVALID, "unknown want");
+    if (want == WANT_LABELS && (nlabels <= 0 || !labels)) fail(E_INVALID, "label readout without label ids");
+    auto [first, source] = admit(groups, n);
+    Packed pk = pack_checked(groups, n, first, source != SRC_NONE);
+    const int64_t width = want == WANT_HIDDEN ? cfg_.d : (want == WANT_LOGITS ? cfg_.vocab : nlabels);
+    const int64_t nrows = int64_t(pk.wanted.size());
+    if (nrows * width > out_floats)
+        fail(E_INVALID, "output buffer holds " + std::to_string(out_floats) + " floats, " +
+                            std::to_string(nrows * width) + " needed");
+    upload(pk, labels, want == WANT_LABELS ? nlabels : 0);
+    const int64_t t = pk.total - pk.base;
+    forward(t, pk.base);
+    PassPlan plan{t, pk.base, nrows, nlabels, want};
+    readout(plan);
+    if (nrows) {
+        const DevBuf& src = want == WANT_HIDDEN ? rows_ : logits_;
+        OMG_HIP(hipMemcpyAsync(h_out_, src.p, size_t(nrows * width) * 4, hipMemcpyDeviceToHost, stream_));
+    }
+    sync();
+    // Dense output in the caller's (group, branch, want) order.
+    std::vector<int64_t> goff(static_cast<size_t>(n) + 1, 0);
+    std::vector<std::vector<int64_t>> boff(static_cast<size_t>(n));
+    for (int64_t g = 0; g < n; ++g) {
+        int64_t acc = 0;
+        for (int64_t b = 0; b < groups[g].nbranches; ++b) {
+            boff[size_t(g)].push_back(acc);
+            acc += groups[g].branches[b].nwant;
+        }
+        goff[size_t(g) + 1] = goff[size_t(g)] + acc;
+    }
+    const float* h = static_cast<const float*>(h_out_);
+    for (int64_t r = 0; r < nrows; ++r) {
+        const auto& w = pk.wanted[size_t(r)];
+        const int64_t dst = goff[size_t(w[0])] + boff[size_t(w[0])][size_t(w[1])] + w[2];
+        std::memcpy(out + dst * width, h + r * width, size_t(width) * 4);
+    }
+    // engine.rs:1928-1939: cache rows 0..p0 now hold the first group's
+    // prefix; every prefix decoded here goes to the state cache.
+    resident_ = std::vector<uint32_t>(groups[first].prefix, groups[first].prefix + groups[first].prefix_len);
+    for (const auto& dgrp : pk.decoded)
+        remember(groups[dgrp.first].prefix, groups[dgrp.first].prefix_len, dgrp.second);
+    if (source == SRC_NONE) source = SRC_DECODED;
+    if (sources)
+        for (int64_t g = 0; g < n; ++g) sources[g] = g == first ? source : SRC_DECODED;
+    last_source_ = source;
+}
+
+void Engine::warmup() {
+    const uint32_t bos = cfg_.bos < uint32_t(cfg_.vocab) ? cfg_.bos : 0;
+    const uint32_t tok = 0, want = 0;
+    BranchIn b{&tok, 1, &want, 1};
+    GroupIn g{&bos, 1, &b, 1};
+    std::vector<float> out(size_t(cfg_.vocab));
+    evaluate_groups(&g, 1, WANT_LOGITS, nullptr, 0, out.data(), int64_t(out.size()), nullptr);
+}
+
+void Engine::prepare(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
+                     bool resident_first) {
+    if (n <= 0) fail(E_INVALID, "empty request");
+    if (resident_first && !is_resident(groups[0].prefix, groups[0].prefix_len))
+        fail(E_INVALID, "prepare: group 0's prefix is not resident");
+    Packed pk = pack_checked(groups, n, 0, resident_first);
+    upload(pk, labels, want == WANT_LABELS ? nlabels : 0);
+    prepared_ = PassPlan{pk.total - pk.base, pk.base, int64_t(pk.wanted.size()), nlabels, want};
+    sync();
+}
+
+void Engine::launch_prepared() {
+    if (prepared_.t <= 0) fail(E_INVALID, "no prepared pass");
+    forward(prepared_.t, prepared_.base);
+    readout(prepared_);
+}
+
+// ----------------------------------------------------------- state cache
+
+void Engine::set_state_cache(size_t bytes, const std::string& dir, const std::string& model_id) {
+    states_ = StateCache{};
+    states_.budget = bytes;
+    state_dir_ = dir;
+    model_id_ = model_id;
+}
+
+SavedState Engine::save_state_at(const uint32_t* prefix, int64_t p, int64_t row0) {
+    const Config& c = cfg_;
+    if (row0 + p > capacity_) fail(E_INVALID, "state rows outside the cache");
+    SavedState s;
+    s.prefix.assign(prefix, prefix + p);
+    sync();
+    for (int64_t l = 0; l < c.layers; ++l) {
+        if (!c.has_kv(l)) continue;
+        const auto [r0, r1] = state_rows(l, p);
+        const int64_t hd = c.head_dim[size_t(l)];
+        const int64_t row_bytes = 2 * c.kv_heads * hd * 2;
+        SavedState::Layer L{uint32_t(l), uint32_t(r0), std::vector<uint8_t>(size_t((r1 - r0) * row_bytes))};
+        if (r1 > r0) {
+            launch_kv_gather(stream_, kc_[size_t(l)].as<half_t>(), vt_[size_t(l)].as<half_t>(), cap_pad_,
+                             int(c.kv_heads), int(hd), row0 + r0, r1 - r0, kv_stage_.as<half_t>());
+            OMG_HIP(hipMemcpyAsync(L.bytes.data(), kv_stage_.p, L.bytes.size(), hipMemcpyDeviceToHost, stream_));
+            OMG_HIP(hipStreamSynchronize(stream_));
+        }
+        s.layers.push_back(std::move(L));
+    }
+    return s;
+}
+
+void Engine::restore_state(const SavedState& s) {
+    const Config& c = cfg_;
+    const int64_t p = int64_t(s.prefix.size());
+    if (p > capacity_)
+        fail(E_STATE, "state of " + std::to_string(p) + " tokens exceeds the engine capacity " + std::to_string(capacity_));
+    for (const SavedState::Layer& L : s.layers) {
+        const int64_t l = L.layer;
+        if (l >= c.layers || !c.has_kv(l))
+            fail(E_STATE, "state has K/V for layer " + std::to_string(l) + ", which owns none");
+    }
+    sync();
+    for (const SavedState::Layer& L : s.layers) {
+        const int64_t l = L.layer, hd = c.head_dim[size_t(l)];
+        const int64_t row_bytes = 2 * c.kv_heads * hd * 2;
+        const auto [r0, r1] = state_rows(l, p);
+        if (int64_t(L.row0) != r0 || int64_t(L.bytes.size()) != (r1 - r0) * row_bytes)
+            fail(E_STATE, "state layer " + std::to_string(l) + ": " + std::to_string(L.bytes.size()) + " bytes at row " +
+                              std::to_string(L.row0) + ", expected " + std::to_string((r1 - r0) * row_bytes) +
+                              " at " + std::to_string(r0));
+    }
+    for (const SavedState::Layer& L : s.layers) {
+        const int64_t l = L.layer, hd = c.head_dim[size_t(l)];
+        const auto [r0, r1] = state_rows(l, p);
+        if (r1 <= r0) continue;
+        OMG_HIP(hipMemcpyAsync(kv_stage_.p, L.bytes.data(), L.bytes.size(), hipMemcpyHostToDevice, stream_));
+        launch_kv_scatter(stream_, kc_[size_t(l)].as<half_t>(), vt_[size_t(l)].as<half_t>(), cap_pad_,
+                          int(c.kv_heads), int(hd), r0, r1 - r0, kv_stage_.as<half_t>());
+        OMG_HIP(hipStreamSynchronize(stream_));
+    }
+    std::vector<int32_t> meta(size_t(4 * p));
+    for (int64_t i = 0; i < p; ++i) {
+        meta[size_t(4 * i)] = int32_t(i);
+        meta[size_t(4 * i + 1)] = 0;
+        meta[size_t(4 * i + 2)] = 0;
+        meta[size_t(4 * i + 3)] = int32_t(i + 1);
+    }
+    if (p) OMG_HIP(hipMemcpy(meta_.p, meta.data(), meta.size() * 4, hipMemcpyHostToDevice));
+    resident_ = s.prefix;
+}
+
+int Engine::restore_from_cache(const uint32_t* prefix, int64_t n) {
+    if (n == 0 || !(states_.budget > 0 || !state_dir_.empty())) return SRC_NONE;
+    const std::vector<uint32_t> key(prefix, prefix + n);
+    if (auto s = states_.get(key)) {
+        try {
+            restore_state(*s);
+            return SRC_RAM;
+        } catch (const Error&) {
+            return SRC_NONE;
+        }
+    }
+    if (state_dir_.empty()) return SRC_NONE;
+    char name[64];
+    std::snprintf(name, sizeof name, "/%016llx.state", (unsigned long long)state_key(model_id_, prefix, n));
+    std::ifstream f(state_dir_ + name, std::ios::binary);
+    if (!f) return SRC_NONE;
+    std::vector<uint8_t> bytes((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+    try {
+        SavedState s = SavedState::from_bytes(bytes.data(), bytes.size(), model_id_);
+        if (s.prefix != key) return SRC_NONE;
+        restore_state(s);
+        states_.put(std::move(s));
+        return SRC_DISK;
+    } catch (const Error&) {
+        return SRC_NONE;
+    }
+}
+
+void Engine::remember(const uint32_t* prefix, int64_t n, int64_t row0) {
+    if (n == 0 || !(states_.budget > 0 || !state_dir_.empty())) return;
+    SavedState s = save_state_at(prefix, n, row0);
+    if (!state_dir_.empty()) {
+        ::mkdir(state_dir_.c_str(), 0755);
+        char name[64];
+        std::snprintf(name, sizeof name, "/%016llx.state", (unsigned long long)state_key(model_id_, prefix, n));
+        const std::vector<uint8_t> bytes = s.to_bytes(model_id_);
+        std::ofstream f(state_dir_ + name, std::ios::binary);
+        if (!f) fail(E_IO, "writing " + state_dir_ + name);
+        f.write(reinterpret_cast<const char*>(bytes.data()), std::streamsize(bytes.size()));
+    }
+    states_.put(std::move(s));
+}
+
+}  // namespace omg

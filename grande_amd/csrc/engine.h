@@ -1,0 +1,212 @@
+// The decision-path engine on one MI355X: the C++ counterpart of
+// crates/omg-wgpu/src/engine.rs (EngineBuilder, Engine, SavedState,
+// StateCache).  One HIP stream; weights and a capacity-sized workspace live
+// in HBM for the life of the engine; a request uploads its token ids and
+// per-token metadata, runs the whole network, and reads back only the
+// wanted rows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <map>
+#include <memory>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+#include "model.h"
+
+namespace omg {
+
+// engine.rs:21-24: bits of a sequence id that number the branch; the bits
+// above number the group within the pass.
+constexpr int SEQ_GROUP_SHIFT = 12;
+
+enum WantKind { WANT_LOGITS = 0, WANT_HIDDEN = 1, WANT_LABELS = 2 };
+enum Source { SRC_NONE = 0, SRC_RESIDENT = 1, SRC_RAM = 2, SRC_DISK = 3, SRC_DECODED = 4 };
+
+struct BranchIn {
+    const uint32_t* tokens;
+    int64_t ntokens;
+    const uint32_t* want;
+    int64_t nwant;
+};
+struct GroupIn {
+    const uint32_t* prefix;
+    int64_t prefix_len;
+    const BranchIn* branches;
+    int64_t nbranches;
+};
+
+// One pass's packed layout (engine.rs:1512-1571).
+struct Packed {
+    int64_t base = 0, total = 0;
+    std::vector<uint32_t> ids;
+    std::vector<int32_t> meta;                        // 4 per token: pos, seq, first key row, row + 1
+    std::vector<std::array<int64_t, 4>> wanted;       // group, branch, slot, workspace row
+    std::vector<std::pair<int64_t, int64_t>> decoded; // group, cache row of its prefix
+};
+// Order: `first`, then the other groups in order (engine.rs:1479-1482).
+Packed pack_groups(const GroupIn* groups, int64_t n, int64_t first, bool resident);
+
+// engine.rs:503-580: a prefix's K/V rows as f16 per layer that owns K/V.
+struct SavedState {
+    std::vector<uint32_t> prefix;
+    struct Layer {
+        uint32_t layer, row0;
+        std::vector<uint8_t> bytes;
+    };
+    std::vector<Layer> layers;
+    size_t byte_len() const;
+    std::vector<uint8_t> to_bytes(const std::string& model_id) const;
+    static SavedState from_bytes(const uint8_t* b, size_t n, const std::string& model_id);
+};
+
+// engine.rs:582-620: LRU keyed by the exact prefix, most recent last.
+struct StateCache {
+    size_t budget = 0, used = 0;
+    std::vector<SavedState> entries;
+    std::optional<SavedState> get(const std::vector<uint32_t>& prefix);
+    void put(SavedState s);
+};
+
+uint64_t state_key(const std::string& model_id, const uint32_t* prefix, int64_t n);  // engine.rs:625-641
+
+// Owned device allocation.
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    explicit DevBuf(size_t n, bool zero = false);
+    ~DevBuf();
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) {
+        o.p = nullptr;
+        o.bytes = 0;
+    }
+    DevBuf& operator=(DevBuf&& o) noexcept;
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+struct DevTensor {
+    DevWeight w;
+    DevBuf data, scales;
+};
+
+class Engine;
+
+// engine.rs:763-1335: receives weights one tensor at a time (uploaded as
+// they arrive) and allocates the workspace at finish.
+class Builder {
+   public:
+    explicit Builder(Config cfg);
+    void push(const std::string& name, const QTensor& t);
+    std::vector<std::string> missing() const;
+    std::unique_ptr<Engine> finish(int64_t capacity, int64_t max_rows);
+    const Config& config() const { return cfg_; }
+
+   private:
+    friend class Engine;
+    Config cfg_;
+    std::map<std::string, std::vector<int64_t>> expected_;
+    std::map<std::string, DevTensor> linears_;
+    std::map<std::string, DevBuf> norms_;  // f32, norm offset folded in
+};
+
+struct PassPlan {
+    int64_t t = 0, base = 0, nrows = 0, nlabels = 0;
+    int want = WANT_HIDDEN;
+};
+
+class Engine {
+   public:
+    ~Engine();
+    const Config& config() const { return cfg_; }
+    int64_t capacity() const { return capacity_; }
+    int64_t max_rows() const { return max_rows_; }
+
+    // engine.rs:1404-1444.  Output rows are dense in the caller's (group,
+    // branch, want) order; width d (hidden), vocab (logits) or nlabels.
+    void evaluate_groups(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
+                         float* out, int64_t out_floats, int* sources);
+    void warmup();  // engine.rs:1356-1366
+
+    void set_state_cache(size_t bytes, const std::string& dir, const std::string& model_id);
+    SavedState save_state(const uint32_t* prefix, int64_t n) { return save_state_at(prefix, n, 0); }
+    void restore_state(const SavedState& s);
+    bool is_resident(const uint32_t* prefix, int64_t n) const;
+    int prefix_source() const { return last_source_; }
+    void evict_resident() { resident_.reset(); }
+    const std::string& model_id() const { return model_id_; }
+
+    // Measurement surface: pack + upload a request once, then replay its
+    // device work (forward + readout, no host transfers).
+    void prepare(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
+                 bool resident_first);
+    void launch_prepared();
+    void sync();
+    void set_profile(bool on);
+    std::string profile_report() const;
+    hipStream_t stream() const { return stream_; }
+
+   private:
+    friend class Builder;
+    Engine() = default;
+    std::pair<int64_t, int> admit(const GroupIn* groups, int64_t n);
+    int restore_from_cache(const uint32_t* prefix, int64_t n);
+    void remember(const uint32_t* prefix, int64_t n, int64_t row0);
+    SavedState save_state_at(const uint32_t* prefix, int64_t n, int64_t row0);
+    std::pair<int64_t, int64_t> state_rows(int64_t layer, int64_t p) const;
+    Packed pack_checked(const GroupIn* groups, int64_t n, int64_t first, bool resident) const;
+    void upload(const Packed& pk, const uint32_t* labels, int64_t nlabels);
+    void forward(int64_t t, int64_t base);
+    void readout(const PassPlan& plan);
+    template <class F>
+    void step(const char* name, F&& f);
+
+    Config cfg_;
+    int64_t capacity_ = 0, max_rows_ = 0, cap_pad_ = 0;
+    hipStream_t stream_ = nullptr;
+    DevTensor embed_;
+    DevBuf final_norm_;
+    struct Layer {
+        DevTensor qkv, o, gate, up, down;
+        DevBuf attn_norm, q_norm, k_norm, post_attn_norm, ffn_norm, post_ffn_norm;
+    };
+    std::vector<Layer> layers_;
+    DevBuf inv_freq_local_, inv_freq_global_;
+    // workspace
+    DevBuf ids_, meta_, x_, hn_, qkv_, q16_, attn_, a_, act_, rows_, logits_, wanted_, labels_, kv_stage_;
+    std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
+    // pinned host staging
+    void* h_in_ = nullptr;
+    size_t h_in_bytes_ = 0;
+    void* h_out_ = nullptr;
+    size_t h_out_bytes_ = 0;
+    // resident prefix / state cache (engine.rs:483-496)
+    std::optional<std::vector<uint32_t>> resident_;
+    int last_source_ = SRC_NONE;
+    StateCache states_;
+    std::string state_dir_;
+    std::string model_id_ = "hip";
+    // measurement
+    PassPlan prepared_;
+    bool profile_ = false;
+    struct Timed {
+        const char* name;
+        hipEvent_t a, b;
+    };
+    std::vector<Timed> pending_;
+    std::vector<hipEvent_t> event_pool_;
+    std::map<std::string, std::pair<int64_t, double>> totals_;
+    void collect_profile();
+};
+
+}  // namespace omg

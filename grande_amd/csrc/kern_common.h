@@ -1,0 +1,70 @@
+// Device-side helpers shared by the gfx950 kernels: vector types for the
+// MFMA builtins, wave64 reductions and the weight decoders.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.h"
+
+namespace omg {
+
+typedef half_t half8 __attribute__((ext_vector_type(8)));
+typedef half_t half4 __attribute__((ext_vector_type(4)));
+typedef half_t half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+__device__ inline float half_bits_to_f32(uint16_t h) {
+    return float(__builtin_bit_cast(half_t, h));
+}
+
+__device__ inline half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+// One Q4 device word (elements 8w..8w+7, see kernels.h) as eight f16 values
+// (q - 8) * d.  1024 + q is built exactly as an f16 by or-ing the nibble
+// into the mantissa of 1024.0 (0x6400); subtracting 1032 leaves q - 8
+// exactly, so the only rounding is the product with d, as in the
+// reference's f16 decode (shaders/weight.wgsl:50-54).
+__device__ inline half8 dq4_word(uint32_t w, half2v dd) {
+    const uint32_t m = 0x000F000Fu, magic = 0x64006400u;
+    const half2v off = {half_t(1032.0f), half_t(1032.0f)};
+    const half2v h0 = (as_half2((w & m) | magic) - off) * dd;
+    const half2v h1 = (as_half2(((w >> 4) & m) | magic) - off) * dd;
+    const half2v h2 = (as_half2(((w >> 8) & m) | magic) - off) * dd;
+    const half2v h3 = (as_half2(((w >> 12) & m) | magic) - off) * dd;
+    return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
+}
+
+// The same four elements as f32: element 8w+p of a Q4 device word.
+__device__ inline float q4_elem_f32(uint32_t w, int p, float d) {
+    const int sh = (p & 1) ? 16 + 4 * (p >> 1) : 4 * (p >> 1);
+    return (float((w >> sh) & 0xfu) - 8.0f) * d;
+}
+
+// Eight Q8 codes (two little-endian words) times the block scale, f16.
+__device__ inline half8 dq8_words(uint32_t w0, uint32_t w1, half_t d) {
+    half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[i] = half_t(float(int8_t(w0 >> (8 * i)))) * d;
+        r[4 + i] = half_t(float(int8_t(w1 >> (8 * i)))) * d;
+    }
+    return r;
+}
+
+}  // namespace omg

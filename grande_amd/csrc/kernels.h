@@ -1,0 +1,94 @@
+// Launchers for the gfx950 kernels of the decision-path forward.  Every
+// launcher checks on the host that the shapes it is given fit what its
+// kernel and grid assume, and throws omg::Error otherwise.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace omg {
+
+typedef _Float16 half_t;
+
+// Storage codes of a device weight (model.rs Dtype::code).
+constexpr int F16_DT = 0, Q8_DT = 1, Q4_DT = 2;
+
+// A linear weight on the device, row-major [rows, cols] = [out, in].
+//   F16: data = half_t[rows*cols].
+//   Q8:  data = int8[rows*cols] (natural order), scales = f16[rows*cols/32].
+//   Q4:  data = 16 B per 32-element block, [rows][cols/32][16 B]; inside a
+//        block, 32-bit word w holds elements 8w..8w+7 with element 8w+p at
+//        bit 4*(p/2) (p even) or 16+4*(p/2) (p odd), so two shifts and a
+//        mask yield them as f16 pairs in order.  scales as Q8.
+struct DevWeight {
+    int dtype = 0;
+    int64_t rows = 0, cols = 0;
+    const void* data = nullptr;
+    const uint16_t* scales = nullptr;
+};
+
+// Repack one Q4_0 tensor (model.rs layout: byte j = element j | element
+// j+16 << 4) into the device layout above.  n = element count.
+void repack_q4(const uint8_t* src, uint8_t* dst, int64_t n);
+
+// ---- residual-stream kernels (norm.hip) ----
+// x[r] = deq(E[ids[r]]) * sqrt(d) (f32, bit-exact), hn[r] = f16(rmsnorm(x[r]) * w).
+void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, int64_t t,
+                       float embed_scale, const float* w, float eps, float* x, half_t* hn);
+// y = rmsnorm(a[r]) * w1;  x[r] = (y + x[r]) * scale;  if w2: hn[r] = f16(rmsnorm(x[r]) * w2).
+void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float* x, const float* w2,
+                          half_t* hn, int64_t t, int64_t d, float eps, float scale);
+// Per token: q heads normed + roped + scaled into q16; on K/V layers, k
+// heads normed + roped and v heads (optionally normed) into the f16 cache.
+struct QkArgs {
+    const float* qkv;
+    int64_t qkv_stride;
+    const int32_t* meta;  // 4 ints per cache row: pos, seq, first key row, own row + 1
+    const float* q_norm;
+    const float* k_norm;
+    const float* inv_freq;  // rope_dims/2 entries
+    int64_t rope_dims;
+    float eps, q_scale;
+    int heads, kv_heads, hd;
+    bool has_kv, v_norm;
+    int64_t t, base, cap_pad;
+    half_t* q16;  // [t][heads][hd]
+    half_t* kc;   // [kv_heads][cap_pad][hd]
+    half_t* vt;   // [kv_heads][cap_pad/64][hd][64]
+};
+void launch_qk_prep(hipStream_t s, const QkArgs& a);
+// rows[i] = rmsnorm(x[wanted[i]]) * w, f32.
+void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int64_t n, int64_t d,
+                       const float* w, float eps, float* rows);
+// out[r][j] = rows[r] . deq(E[col(j)]) in f32 (+ softcap), col(j) = cols ? cols[j] : j.
+void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows,
+                   const uint32_t* cols, int64_t ncols, float softcap, float* out);
+// K/V cache rows <-> the reference's state row format [K heads | V heads] f16.
+void launch_kv_gather(hipStream_t s, const half_t* kc, const half_t* vt, int64_t cap_pad, int kv_heads,
+                      int hd, int64_t row0, int64_t rows, half_t* out);
+void launch_kv_scatter(hipStream_t s, half_t* kc, half_t* vt, int64_t cap_pad, int kv_heads, int hd,
+                       int64_t row0, int64_t rows, const half_t* in);
+
+// ---- MFMA GEMMs (gemm.hip) ----
+// y[M][N] (f32) = f16(X)[M][K] . deq(W)[N][K]^T, f32 accumulation.
+void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
+                 int64_t m);
+// act[M][F] (f16) = gelu_tanh(X . Wg^T) * (X . Wu^T).
+void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,
+                       const DevWeight& wu, half_t* act, int64_t ldact, int64_t m);
+
+// ---- block-causal attention (attention.hip) ----
+struct AttnArgs {
+    const half_t* q16;   // [t][heads][hd]
+    const half_t* kc;    // [kv_heads][cap_pad][hd]
+    const half_t* vt;    // [kv_heads][cap_pad/64][hd][64]
+    const int32_t* meta; // per cache row
+    half_t* out;         // [t][heads][hd]
+    int64_t t, base, cap_pad;
+    int heads, kv_heads, hd;
+    int window;          // 0 = global layer
+};
+void launch_attention(hipStream_t s, const AttnArgs& a);
+
+}  // namespace omg

@@ -1,0 +1,394 @@
+// Row-wise kernels of the forward: embedding gather + first norm, the fused
+// residual norms, q/k preparation with the f16 K/V cache write, the
+// readout (final norm at the wanted rows, label / vocabulary logits) and
+// the K/V <-> state-row conversions.  One wave64 per row; reductions are
+// wave-level shuffles, no LDS round trips.
+#include <cmath>
+#include <string>
+
+#include "common.h"
+#include "kern_common.h"
+
+namespace omg {
+
+// ---------------------------------------------------------------- decode
+
+// Four consecutive elements e..e+3 (e % 4 == 0) of a device weight, f32.
+template <int DT>
+__device__ inline void load4_f32(const DevWeight& w, int64_t e, float v[4]) {
+    if constexpr (DT == F16_DT) {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const half_t*>(w.data) + e);
+        const half2v a = as_half2(u.x), b = as_half2(u.y);
+        v[0] = float(a.x);
+        v[1] = float(a.y);
+        v[2] = float(b.x);
+        v[3] = float(b.y);
+    } else if constexpr (DT == Q8_DT) {
+        const float d = half_bits_to_f32(w.scales[e / 32]);
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(w.data) + e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = float(int8_t(u >> (8 * i))) * d;
+    } else {
+        const int64_t b = e / 32;
+        const int j = int(e % 32);
+        const float d = half_bits_to_f32(w.scales[b]);
+        const uint32_t word = static_cast<const uint32_t*>(w.data)[b * 4 + j / 8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = q4_elem_f32(word, (j % 8) + i, d);
+    }
+}
+
+// ------------------------------------------------------------ embedding
+
+// embed.wgsl:15-48 + the layer-0 input norm (rmsnorm.wgsl:41-61), one wave
+// per token.  The stored row is deq(E[id]) * sqrt(d) in f32: the decode is
+// exact, so the one product rounds exactly like reference.rs:186.
+template <int DT>
+__global__ __launch_bounds__(256) void embed_norm_kernel(DevWeight E, const uint32_t* __restrict__ ids,
+                                                         int64_t t, float escale,
+                                                         const float* __restrict__ w, float eps,
+                                                         float* __restrict__ x, half_t* __restrict__ hn) {
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int64_t row = int64_t(blockIdx.x) * 4 + wave;
+    if (row >= t) return;
+    const int64_t d = E.cols;
+    const int64_t id = ids[row];
+    float ss = 0.0f;
+    for (int64_t q = lane; q < d / 4; q += WAVE) {
+        float v[4];
+        load4_f32<DT>(E, id * d + 4 * q, v);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = v[i] * escale;
+            ss += v[i] * v[i];
+        }
+        *reinterpret_cast<float4*>(x + row * d + 4 * q) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / float(d) + eps);
+    for (int64_t q = lane; q < d / 4; q += WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(x + row * d + 4 * q);
+        const float4 g = *reinterpret_cast<const float4*>(w + 4 * q);
+        half4 o = {half_t(v.x * inv * g.x), half_t(v.y * inv * g.y), half_t(v.z * inv * g.z),
+                   half_t(v.w * inv * g.w)};
+        *reinterpret_cast<half4*>(hn + row * d + 4 * q) = o;
+    }
+}
+
+void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, int64_t t,
+                       float embed_scale, const float* w, float eps, float* x, half_t* hn) {
+    if (t <= 0) return;
+    if (E.cols % 32 != 0) fail(E_INVALID, "embed: width must be a multiple of 32");
+    const dim3 grid(unsigned((t + 3) / 4)), block(256);
+    switch (E.dtype) {
+        case F16_DT: embed_norm_kernel<F16_DT><<<grid, block, 0, s>>>(E, ids, t, embed_scale, w, eps, x, hn); break;
+        case Q8_DT: embed_norm_kernel<Q8_DT><<<grid, block, 0, s>>>(E, ids, t, embed_scale, w, eps, x, hn); break;
+        default: embed_norm_kernel<Q4_DT><<<grid, block, 0, s>>>(E, ids, t, embed_scale, w, eps, x, hn); break;
+    }
+    OMG_HIP(hipGetLastError());
+}
+
+// -------------------------------------------------------- residual norm
+
+// rmsnorm.wgsl:41-68 in residual mode with the fused second norm: the
+// post-attention / post-feedforward norm of `a` is added into the stream x,
+// then the norm that reads x next writes its f16 input hn.
+__global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ a,
+                                                            const float* __restrict__ w1,
+                                                            float* __restrict__ x,
+                                                            const float* __restrict__ w2,
+                                                            half_t* __restrict__ hn, int64_t t,
+                                                            int64_t d, float eps, float scale) {
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int64_t row = int64_t(blockIdx.x) * 4 + wave;
+    if (row >= t) return;
+    const float* ar = a + row * d;
+    float* xr = x + row * d;
+    float ss = 0.0f;
+    for (int64_t q = lane; q < d / 4; q += WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(ar + 4 * q);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / float(d) + eps);
+    float ss2 = 0.0f;
+    for (int64_t q = lane; q < d / 4; q += WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(ar + 4 * q);
+        const float4 g = *reinterpret_cast<const float4*>(w1 + 4 * q);
+        float4 o = *reinterpret_cast<const float4*>(xr + 4 * q);
+        o.x = (v.x * inv * g.x + o.x) * scale;
+        o.y = (v.y * inv * g.y + o.y) * scale;
+        o.z = (v.z * inv * g.z + o.z) * scale;
+        o.w = (v.w * inv * g.w + o.w) * scale;
+        *reinterpret_cast<float4*>(xr + 4 * q) = o;
+        ss2 += o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+    }
+    if (!w2) return;
+    const float inv2 = 1.0f / sqrtf(wave_sum(ss2) / float(d) + eps);
+    for (int64_t q = lane; q < d / 4; q += WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
+        const float4 g = *reinterpret_cast<const float4*>(w2 + 4 * q);
+        half4 o = {half_t(v.x * inv2 * g.x), half_t(v.y * inv2 * g.y), half_t(v.z * inv2 * g.z),
+                   half_t(v.w * inv2 * g.w)};
+        *reinterpret_cast<half4*>(hn + row * d + 4 * q) = o;
+    }
+}
+
+void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float* x, const float* w2,
+                          half_t* hn, int64_t t, int64_t d, float eps, float scale) {
+    if (t <= 0) return;
+    if (d % 4 != 0) fail(E_INVALID, "residual_norm: width must be a multiple of 4");
+    residual_norm_kernel<<<dim3(unsigned((t + 3) / 4)), dim3(256), 0, s>>>(a, w1, x, w2, hn, t, d, eps,
+                                                                          scale);
+    OMG_HIP(hipGetLastError());
+}
+
+// -------------------------------------------------------------- qk prep
+
+// qk_prep.wgsl:66-114: one wave per (token, head slot); slots are the q
+// heads, then (on layers with their own K/V) the k heads, then the v heads.
+// Head row element e = lane * EPL + i, so the RoPE partner e +- HD/2 sits
+// in lane ^ 32.
+template <int HD>
+__global__ void qk_prep_kernel(QkArgs a) {
+    constexpr int EPL = HD / WAVE;
+    constexpr int HALF = HD / 2;
+    const int slot = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int64_t tok = blockIdx.x;
+    const int64_t row = a.base + tok;
+    const int H = a.heads, KV = a.kv_heads;
+    int kind, head;
+    if (slot < H) {
+        kind = 0;
+        head = slot;
+    } else if (slot < H + KV) {
+        kind = 1;
+        head = slot - H;
+    } else {
+        kind = 2;
+        head = slot - H - KV;
+    }
+    const float* src = a.qkv + tok * a.qkv_stride + int64_t(slot) * HD;
+    float v[EPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        v[i] = src[lane * EPL + i];
+        ss += v[i] * v[i];
+    }
+    ss = wave_sum(ss);
+    if (kind == 2) {
+        const float inv = a.v_norm ? 1.0f / sqrtf(ss / float(HD) + a.eps) : 1.0f;
+        half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + row / 64) * HD) * 64 + row % 64;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) dst[int64_t(lane * EPL + i) * 64] = half_t(v[i] * inv);
+        return;
+    }
+    const float inv = 1.0f / sqrtf(ss / float(HD) + a.eps);
+    const float* nw = kind == 0 ? a.q_norm : a.k_norm;
+    const float pos = float(a.meta[4 * row]);
+    float y[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) y[i] = v[i] * inv * nw[lane * EPL + i];
+    float o[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const float partner = __shfl_xor(y[i], 32, WAVE);
+        const int e = lane * EPL + i;
+        const int dd = e < HALF ? e : e - HALF;
+        if (dd < a.rope_dims / 2) {
+            const float ang = pos * a.inv_freq[dd];
+            const float c = cosf(ang), sn = sinf(ang);
+            o[i] = e < HALF ? y[i] * c - partner * sn : y[i] * c + partner * sn;
+        } else {
+            o[i] = y[i];
+        }
+    }
+    if (kind == 0) {
+        half_t* dst = a.q16 + (tok * H + head) * HD + lane * EPL;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) dst[i] = half_t(o[i] * a.q_scale);
+    } else {
+        half_t* dst = a.kc + (int64_t(head) * a.cap_pad + row) * HD + lane * EPL;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) dst[i] = half_t(o[i]);
+    }
+}
+
+void launch_qk_prep(hipStream_t s, const QkArgs& a) {
+    if (a.t <= 0) return;
+    const int slots = a.heads + (a.has_kv ? 2 * a.kv_heads : 0);
+    if (slots * WAVE > 1024) fail(E_INVALID, "qk_prep: too many heads for one block");
+    if (a.base + a.t > a.cap_pad || a.cap_pad % 64) fail(E_INVALID, "qk_prep: cache rows out of range");
+    if (a.hd != 256) fail(E_INVALID, "qk_prep: head_dim must be 256");
+    qk_prep_kernel<256><<<dim3(unsigned(a.t)), dim3(unsigned(slots * WAVE)), 0, s>>>(a);
+    OMG_HIP(hipGetLastError());
+}
+
+// -------------------------------------------------------------- readout
+
+// The last layer's fused norm (engine.rs:1752-1758) applied at the wanted
+// rows only: rows[i] = rmsnorm(x[wanted[i]]) * w in f32.
+__global__ __launch_bounds__(256) void final_rows_kernel(const float* __restrict__ x,
+                                                         const int32_t* __restrict__ wanted, int64_t n,
+                                                         int64_t d, const float* __restrict__ w,
+                                                         float eps, float* __restrict__ rows) {
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int64_t i = int64_t(blockIdx.x) * 4 + wave;
+    if (i >= n) return;
+    const float* xr = x + int64_t(wanted[i]) * d;
+    float ss = 0.0f;
+    for (int64_t q = lane; q < d / 4; q += WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / float(d) + eps);
+    for (int64_t q = lane; q < d / 4; q += WAVE) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
+        const float4 g = *reinterpret_cast<const float4*>(w + 4 * q);
+        *reinterpret_cast<float4*>(rows + i * d + 4 * q) =
+            make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+    }
+}
+
+void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int64_t n, int64_t d,
+                       const float* w, float eps, float* rows) {
+    if (n <= 0) return;
+    final_rows_kernel<<<dim3(unsigned((n + 3) / 4)), dim3(256), 0, s>>>(x, wanted, n, d, w, eps, rows);
+    OMG_HIP(hipGetLastError());
+}
+
+// logits.wgsl:38-79: one thread per output column (a vocabulary row of E),
+// the wanted rows staged through LDS RM rows x KS columns at a time; E is
+// decoded to f32 (no f16 rounding on this path, as in the reference).
+constexpr int LG_RM = 16, LG_KS = 128, LG_THREADS = 64;
+
+template <int DT>
+__global__ __launch_bounds__(LG_THREADS) void logits_kernel(DevWeight E, const float* __restrict__ rows,
+                                                            int64_t nrows, const uint32_t* __restrict__ cols,
+                                                            int64_t ncols, float softcap,
+                                                            float* __restrict__ out) {
+    __shared__ float xs[LG_RM][LG_KS];
+    const int64_t j = int64_t(blockIdx.x) * LG_THREADS + threadIdx.x;
+    const bool ok = j < ncols;
+    const int64_t col = ok ? (cols ? int64_t(cols[j]) : j) : 0;
+    const int64_t K = E.cols;
+    for (int64_t r0 = 0; r0 < nrows; r0 += LG_RM) {
+        float acc[LG_RM];
+#pragma unroll
+        for (int r = 0; r < LG_RM; ++r) acc[r] = 0.0f;
+        for (int64_t k0 = 0; k0 < K; k0 += LG_KS) {
+            for (int i = int(threadIdx.x); i < LG_RM * LG_KS; i += LG_THREADS) {
+                const int r = i / LG_KS, c = i % LG_KS;
+                xs[r][c] = (r0 + r < nrows && k0 + c < K) ? rows[(r0 + r) * K + k0 + c] : 0.0f;
+            }
+            __syncthreads();
+            if (ok) {
+                const int64_t kn = K - k0 < LG_KS ? K - k0 : LG_KS;
+                for (int64_t kk = 0; kk < kn; kk += 4) {
+                    float wv[4];
+                    load4_f32<DT>(E, col * K + k0 + kk, wv);
+#pragma unroll
+                    for (int r = 0; r < LG_RM; ++r)
+                        acc[r] += xs[r][kk] * wv[0] + xs[r][kk + 1] * wv[1] + xs[r][kk + 2] * wv[2] +
+                                  xs[r][kk + 3] * wv[3];
+                }
+            }
+            __syncthreads();
+        }
+        if (ok) {
+            for (int r = 0; r < LG_RM; ++r) {
+                if (r0 + r >= nrows) break;
+                float z = acc[r];
+                if (softcap > 0.0f) z = softcap * tanhf(z / softcap);
+                out[(r0 + r) * ncols + j] = z;
+            }
+        }
+    }
+}
+
+void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows,
+                   const uint32_t* cols, int64_t ncols, float softcap, float* out) {
+    if (nrows <= 0 || ncols <= 0) return;
+    if (E.cols % 32 != 0) fail(E_INVALID, "logits: width must be a multiple of 32");
+    const dim3 grid(unsigned((ncols + LG_THREADS - 1) / LG_THREADS)), block(LG_THREADS);
+    switch (E.dtype) {
+        case F16_DT: logits_kernel<F16_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out); break;
+        case Q8_DT: logits_kernel<Q8_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out); break;
+        default: logits_kernel<Q4_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out); break;
+    }
+    OMG_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------- state rows
+
+// engine.rs:499-502: a state row is every K head then every V head of one
+// token, f16.  The cache keeps K row-major and V in 64-row transposed tiles.
+__global__ void kv_gather_kernel(const half_t* __restrict__ kc, const half_t* __restrict__ vt,
+                                 int64_t cap_pad, int kvh, int hd, int64_t row0, int64_t rows,
+                                 half_t* __restrict__ out) {
+    const int64_t width = int64_t(2) * kvh * hd;
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows * width) return;
+    const int64_t r = i / width, c = i % width, row = row0 + r;
+    const int64_t g = (c / hd) % kvh, e = c % hd;
+    if (c < int64_t(kvh) * hd)
+        out[i] = kc[(g * cap_pad + row) * hd + e];
+    else
+        out[i] = vt[((g * (cap_pad / 64) + row / 64) * hd + e) * 64 + row % 64];
+}
+
+__global__ void kv_scatter_kernel(half_t* __restrict__ kc, half_t* __restrict__ vt, int64_t cap_pad,
+                                  int kvh, int hd, int64_t row0, int64_t rows,
+                                  const half_t* __restrict__ in) {
+    const int64_t width = int64_t(2) * kvh * hd;
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows * width) return;
+    const int64_t r = i / width, c = i % width, row = row0 + r;
+    const int64_t g = (c / hd) % kvh, e = c % hd;
+    if (c < int64_t(kvh) * hd)
+        kc[(g * cap_pad + row) * hd + e] = in[i];
+    else
+        vt[((g * (cap_pad / 64) + row / 64) * hd + e) * 64 + row % 64] = in[i];
+}
+
+void launch_kv_gather(hipStream_t s, const half_t* kc, const half_t* vt, int64_t cap_pad, int kv_heads,
+                      int hd, int64_t row0, int64_t rows, half_t* out) {
+    if (rows <= 0) return;
+    if (row0 < 0 || row0 + rows > cap_pad) fail(E_INVALID, "kv_gather: rows out of range");
+    const int64_t n = rows * 2 * kv_heads * hd;
+    kv_gather_kernel<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(kc, vt, cap_pad, kv_heads, hd,
+                                                                          row0, rows, out);
+    OMG_HIP(hipGetLastError());
+}
+
+void launch_kv_scatter(hipStream_t s, half_t* kc, half_t* vt, int64_t cap_pad, int kv_heads, int hd,
+                       int64_t row0, int64_t rows, const half_t* in) {
+    if (rows <= 0) return;
+    if (row0 < 0 || row0 + rows > cap_pad) fail(E_INVALID, "kv_scatter: rows out of range");
+    const int64_t n = rows * 2 * kv_heads * hd;
+    kv_scatter_kernel<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(kc, vt, cap_pad, kv_heads, hd,
+                                                                           row0, rows, in);
+    OMG_HIP(hipGetLastError());
+}
+
+// --------------------------------------------------------------- repack
+
+void repack_q4(const uint8_t* src, uint8_t* dst, int64_t n) {
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const uint8_t* in = src + 16 * b;
+        uint8_t q[32];
+        for (int j = 0; j < 16; ++j) {
+            q[j] = in[j] & 0xf;
+            q[j + 16] = in[j] >> 4;
+        }
+        for (int w = 0; w < 4; ++w) {
+            uint32_t word = 0;
+            for (int p = 0; p < 8; ++p) {
+                const int sh = (p & 1) ? 16 + 4 * (p >> 1) : 4 * (p >> 1);
+                word |= uint32_t(q[8 * w + p]) << sh;
+            }
+            std::memcpy(dst + 16 * b + 4 * w, &word, 4);
+        }
+    }
+}
+
+}  // namespace omg

@@ -1,0 +1,299 @@
+"""Host-side mirror of the reference's engine surface over the C ABI.
+
+Names and meaning follow omg-core's backend contract
+(crates/omg-core/src/backend.rs:9-167: Token ids, Want, BranchTokens,
+BranchOutput, Group, GroupOutput, PrefixSource) and omg_wgpu's engine
+(crates/omg-wgpu/src/engine.rs: EngineBuilder::{new, push, missing,
+finish}, Engine::{evaluate, evaluate_groups, warmup, set_state_cache,
+save_state, restore_state, is_resident, prefix_source, evict_resident},
+SavedState::{to_bytes, from_bytes}).  Errors are OmgError with the
+library's message, where the reference returns anyhow errors.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib as L
+from .model import QTensor, Weights
+
+
+class Want(enum.IntEnum):
+    """backend.rs:14-20, plus LABELS: logits of given label ids only."""
+
+    LOGITS = L.WANT_LOGITS
+    HIDDEN = L.WANT_HIDDEN
+    LABELS = L.WANT_LABELS
+
+
+class PrefixSource(enum.IntEnum):
+    """backend.rs:92-104."""
+
+    NONE = L.SRC_NONE
+    RESIDENT = L.SRC_RESIDENT
+    RAM = L.SRC_RAM
+    DISK = L.SRC_DISK
+    DECODED = L.SRC_DECODED
+
+
+@dataclass
+class BranchTokens:
+    """backend.rs:22-30: branch tokens + ascending wanted indices."""
+
+    tokens: Sequence[int]
+    want: Sequence[int]
+
+
+@dataclass
+class BranchOutput:
+    """backend.rs:32-36: rows in `want` order."""
+
+    rows: list = field(default_factory=list)
+
+
+@dataclass
+class Group:
+    """backend.rs:38-45 / engine.rs:26-38."""
+
+    prefix: Sequence[int]
+    branches: Sequence[BranchTokens]
+
+
+@dataclass
+class GroupOutput:
+    """backend.rs:62-68."""
+
+    branches: list
+    prefix_source: PrefixSource
+
+
+def _u32(xs) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(xs, dtype=np.int64).astype(np.uint32))
+
+
+class _CGroups:
+    """C views of a list of Groups; keeps the backing arrays alive."""
+
+    def __init__(self, groups: Sequence[Group]):
+        self.keep = []
+        self.arr = (L.omg_group * max(1, len(groups)))()
+        self.n = len(groups)
+        for gi, g in enumerate(groups):
+            p = _u32(g.prefix)
+            br = (L.omg_branch * max(1, len(g.branches)))()
+            for bi, b in enumerate(g.branches):
+                t, w = _u32(b.tokens), _u32(b.want)
+                self.keep += [t, w]
+                br[bi].tokens = t.ctypes.data_as(C.POINTER(C.c_uint32))
+                br[bi].ntokens = t.size
+                br[bi].want = w.ctypes.data_as(C.POINTER(C.c_uint32))
+                br[bi].nwant = w.size
+            self.keep += [p, br]
+            self.arr[gi].prefix = p.ctypes.data_as(C.POINTER(C.c_uint32))
+            self.arr[gi].prefix_len = p.size
+            self.arr[gi].branches = br
+            self.arr[gi].nbranches = len(g.branches)
+
+
+class EngineBuilder:
+    """engine.rs:763-1335."""
+
+    def __init__(self, config: str):
+        self._h = L.handle(L.lib().omg_builder_new(config.encode()))
+        self.config = config
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            L.lib().omg_builder_free(self._h)
+            self._h = None
+
+    def push(self, t: QTensor) -> None:
+        shape = (C.c_int64 * len(t.shape))(*t.shape)
+        L.check(L.lib().omg_builder_push(self._h, t.name.encode(), t.dtype, shape, len(t.shape),
+                                         t.data.ctypes.data, t.data.size, t.scales.ctypes.data if t.scales.size else None,
+                                         t.scales.size))
+
+    def push_weights(self, w: Weights) -> None:
+        L.check(L.lib().omg_builder_push_weights(self._h, w._h))
+
+    def missing(self) -> list[str]:
+        buf = C.create_string_buffer(1 << 16)
+        L.lib().omg_builder_missing(self._h, buf, len(buf))
+        return [s for s in buf.value.decode().split("\n") if s]
+
+    def finish(self, capacity: int, max_rows: int) -> "Engine":
+        h, self._h = self._h, None
+        return Engine(L.handle(L.lib().omg_builder_finish(h, capacity, max_rows)))
+
+
+class Engine:
+    """engine.rs:449-2182 over libomg_hip.so."""
+
+    def __init__(self, handle):
+        self._h = handle
+        c = L.omg_config_t()
+        L.check(L.lib().omg_config(self._h, C.byref(c)))
+        self.vocab, self.d, self.layers = c.vocab, c.d, c.layers
+        self.capacity, self.max_rows, self.bos = c.capacity, c.max_rows, c.bos
+
+    @classmethod
+    def new(cls, weights: Weights, capacity: int, max_rows: int) -> "Engine":
+        """engine.rs:1341-1351."""
+        b = EngineBuilder(weights.config)
+        b.push_weights(weights)
+        return b.finish(capacity, max_rows)
+
+    @classmethod
+    def open_dir(cls, path: str | Path, capacity: int, max_rows: int) -> "Engine":
+        """backend.rs:28-71 (an exported directory)."""
+        return cls(L.handle(L.lib().omg_open_dir(str(path).encode(), capacity, max_rows)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            L.lib().omg_close(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def warmup(self) -> None:
+        L.check(L.lib().omg_warmup(self._h))
+
+    def evaluate_groups(self, groups: Sequence[Group], want: Want, labels: Sequence[int] | None = None
+                        ) -> list[GroupOutput]:
+        cg = _CGroups(groups)
+        lab = _u32(labels if labels is not None else [])
+        width = {Want.HIDDEN: self.d, Want.LOGITS: self.vocab, Want.LABELS: lab.size}[Want(want)]
+        rows = sum(len(b.want) for g in groups for b in g.branches)
+        out = np.zeros((max(rows, 1), max(width, 1)), np.float32)
+        src = (C.c_int * max(1, len(groups)))()
+        L.check(L.lib().omg_evaluate_groups(self._h, cg.arr, cg.n, int(want),
+                                            lab.ctypes.data_as(C.POINTER(C.c_uint32)), lab.size,
+                                            out.ctypes.data_as(C.POINTER(C.c_float)), out.size, src))
+        res, r = [], 0
+        for gi, g in enumerate(groups):
+            bo = []
+            for b in g.branches:
+                bo.append(BranchOutput(rows=[out[r + s, :width].copy() for s in range(len(b.want))]))
+                r += len(b.want)
+            res.append(GroupOutput(branches=bo, prefix_source=PrefixSource(src[gi])))
+        return res
+
+    def evaluate(self, prefix: Sequence[int], branches: Sequence[BranchTokens], want: Want,
+                 labels: Sequence[int] | None = None) -> list[BranchOutput]:
+        """engine.rs:1386-1396."""
+        return self.evaluate_groups([Group(prefix, branches)], want, labels)[0].branches
+
+    def prefix_source(self) -> PrefixSource:
+        return PrefixSource(L.lib().omg_prefix_source(self._h))
+
+    def is_resident(self, prefix: Sequence[int]) -> bool:
+        p = _u32(prefix)
+        return bool(L.lib().omg_is_resident(self._h, p.ctypes.data_as(C.POINTER(C.c_uint32)), p.size))
+
+    def evict_resident(self) -> None:
+        L.lib().omg_evict_resident(self._h)
+
+    def set_state_cache(self, nbytes: int, directory: str | Path | None, model_id: str) -> None:
+        L.check(L.lib().omg_set_state_cache(self._h, nbytes, str(directory).encode() if directory else None,
+                                            model_id.encode()))
+
+    def save_state(self, prefix: Sequence[int], model_id: str) -> bytes:
+        """Engine::save_state + SavedState::to_bytes: GRWS1 bytes."""
+        p = _u32(prefix)
+        ptr, n = C.POINTER(C.c_uint8)(), C.c_size_t()
+        L.check(L.lib().omg_save_state(self._h, p.ctypes.data_as(C.POINTER(C.c_uint32)), p.size, model_id.encode(),
+                                       C.byref(ptr), C.byref(n)))
+        try:
+            return C.string_at(ptr, n.value)
+        finally:
+            L.lib().omg_free_bytes(ptr)
+
+    def restore_state(self, data: bytes, model_id: str) -> None:
+        buf = (C.c_uint8 * len(data)).from_buffer_copy(data)
+        L.check(L.lib().omg_restore_state(self._h, buf, len(data), model_id.encode()))
+
+    # ---- measurement surface ----
+    def prepare(self, groups: Sequence[Group], want: Want, labels: Sequence[int] | None = None,
+                first_resident: bool = False) -> None:
+        cg = _CGroups(groups)
+        lab = _u32(labels if labels is not None else [])
+        L.check(L.lib().omg_pass_prepare(self._h, cg.arr, cg.n, int(want), lab.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                         lab.size, int(first_resident)))
+
+    def launch(self) -> None:
+        L.check(L.lib().omg_pass_launch(self._h))
+
+    def sync(self) -> None:
+        L.check(L.lib().omg_sync(self._h))
+
+    def profile(self, on: bool) -> None:
+        L.check(L.lib().omg_profile(self._h, int(on)))
+
+    def profile_report(self) -> dict[str, tuple[int, float]]:
+        """kernel name -> (launches, total ms) since profiling was switched on."""
+        buf = C.create_string_buffer(1 << 16)
+        L.lib().omg_profile_report(self._h, buf, len(buf))
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, n, ms = line.split()
+            out[name] = (int(n), float(ms))
+        return out
+
+
+def pack(groups: Sequence[Group], first: int = 0, resident: bool = False):
+    """engine.rs:1512-1571 through omg_pack: (ids, meta[n,4], wanted[r,4])."""
+    cg = _CGroups(groups)
+    total = sum(len(g.prefix) + sum(len(b.tokens) for b in g.branches) for g in groups)
+    rows = sum(len(b.want) for g in groups for b in g.branches)
+    ids = np.zeros(max(total, 1), np.uint32)
+    meta = np.zeros((max(total, 1), 4), np.int32)
+    wanted = np.zeros((max(rows, 1), 4), np.int64)
+    n_ids, n_w = C.c_size_t(ids.size), C.c_size_t(wanted.shape[0])
+    L.check(L.lib().omg_pack(cg.arr, cg.n, first, int(resident), ids.ctypes.data_as(C.POINTER(C.c_uint32)),
+                             meta.ctypes.data_as(C.POINTER(C.c_int32)), wanted.ctypes.data_as(C.POINTER(C.c_int64)),
+                             C.byref(n_ids), C.byref(n_w)))
+    return ids[:n_ids.value], meta[:n_ids.value], wanted[:n_w.value]
+
+
+def state_key(model_id: str, prefix: Sequence[int]) -> int:
+    p = _u32(prefix)
+    return int(L.lib().omg_state_key(model_id.encode(), p.ctypes.data_as(C.POINTER(C.c_uint32)), p.size))
+
+
+def state_check(data: bytes, model_id: str) -> tuple[int, int]:
+    """SavedState::from_bytes without an engine: (prefix length, layers)."""
+    buf = (C.c_uint8 * max(1, len(data))).from_buffer_copy(data if data else b"\0")
+    pl, nl = C.c_size_t(), C.c_size_t()
+    L.check(L.lib().omg_state_check(buf, len(data), model_id.encode(), C.byref(pl), C.byref(nl)))
+    return pl.value, nl.value
+
+
+class DeviceWeight:
+    """A weight uploaded in the device layout, for the kernel-level tests."""
+
+    def __init__(self, t: QTensor):
+        rows, cols = t.shape
+        self._h = L.handle(L.lib().omg_weight_upload(t.dtype, rows, cols, t.data.ctypes.data,
+                                                     t.scales.ctypes.data if t.scales.size else None))
+        self.rows, self.cols = rows, cols
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            L.lib().omg_weight_free(self._h)
+            self._h = None
+
+    def gemm(self, x_ptr: int, ldx: int, m: int, y_ptr: int, ldy: int, stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_gemm(self._h, x_ptr, ldx, m, y_ptr, ldy, stream))
+
+    def gemm_geglu(self, up: "DeviceWeight", x_ptr: int, ldx: int, m: int, act_ptr: int, ldact: int,
+                   stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_gemm_geglu(self._h, up._h, x_ptr, ldx, m, act_ptr, ldact, stream))
+
+    def embed_norm(self, ids_ptr: int, t: int, scale: float, w_ptr: int, eps: float, x_ptr: int, hn_ptr: int,
+                   stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_embed_norm(self._h, ids_ptr, t, scale, w_ptr, eps, x_ptr, hn_ptr, stream))

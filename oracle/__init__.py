@@ -1,0 +1,327 @@
+"""CPU oracle: a restatement of the reference's decision-path forward.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in grande_amd/ imports this package;
+only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg do,
+and only as the checker or the timed CPU baseline.  See oracle.h for the
+reference lines each function restates, and tests/test_oracle.py for how
+each one is pinned.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+BUILD = HERE / "_build"
+F16, Q8, Q4 = 0, 1, 2
+MAX_LAYERS = 64
+
+
+def build() -> None:
+    """Compile the oracle (oracle/Makefile) into oracle/_build."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def _has_avx512() -> bool:
+    try:
+        return "avx512f" in Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return False
+
+
+class orc_config(C.Structure):
+    _fields_ = [("vocab", C.c_int32), ("d", C.c_int32), ("layers", C.c_int32), ("heads", C.c_int32),
+                ("kv_heads", C.c_int32), ("head_dim", C.c_int32 * MAX_LAYERS), ("ff", C.c_int32 * MAX_LAYERS),
+                ("sliding", C.c_int32 * MAX_LAYERS), ("kv_source", C.c_int32 * MAX_LAYERS),
+                ("rope_dims", C.c_int32 * MAX_LAYERS), ("eps", C.c_float), ("window", C.c_int32),
+                ("theta_global", C.c_float), ("theta_local", C.c_float), ("query_scale", C.c_float),
+                ("norm_offset", C.c_float), ("v_norm", C.c_int32), ("softcap", C.c_float), ("bos", C.c_int32)]
+
+
+class orc_branch(C.Structure):
+    _fields_ = [("tokens", C.POINTER(C.c_uint32)), ("ntokens", C.c_int64), ("want", C.POINTER(C.c_int64)),
+                ("nwant", C.c_int64)]
+
+
+class orc_group(C.Structure):
+    _fields_ = [("prefix", C.POINTER(C.c_uint32)), ("prefix_len", C.c_int64), ("branches", C.POINTER(orc_branch)),
+                ("nbranches", C.c_int64)]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        path = BUILD / ("liboracle_v4.so" if _has_avx512() else "liboracle_v3.so")
+        if not path.exists():
+            build()
+        L = C.CDLL(str(path))
+        P = C.c_void_p
+        sig = {
+            "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "orc_rng_next": (C.c_float, [C.POINTER(C.c_uint64)]),
+            "orc_rng_values": (None, [C.POINTER(C.c_uint64), C.POINTER(C.c_float), C.c_size_t, C.c_float]),
+            "orc_quantize_q8": (C.c_int, [P, C.c_size_t, P, P]),
+            "orc_quantize_q4": (C.c_int, [P, C.c_size_t, P, P]),
+            "orc_get": (C.c_float, [C.c_int, P, P, C.c_size_t]),
+            "orc_model_new": (P, [C.POINTER(orc_config), C.c_int]),
+            "orc_model_free": (None, [P]),
+            "orc_model_set": (C.c_int, [P, C.c_char_p, C.c_int, C.c_int64, C.c_int64, P, P]),
+            "orc_model_missing": (C.c_int, [P, C.c_char_p, C.c_size_t]),
+            "orc_forward": (C.c_int, [P, P, P, P, C.c_int64, P]),
+            "orc_logits": (C.c_int, [P, P, C.c_int64, P]),
+            "orc_pack": (C.c_int, [C.POINTER(orc_group), C.c_int64, C.c_int64, C.c_int, P, P, P, P,
+                                   C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+            "orc_state_key": (C.c_uint64, [C.c_char_p, P, C.c_int64]),
+            "orc_state_rows": (None, [C.c_int, C.c_int64, C.c_int64, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+            "orc_softmax": (None, [P, C.c_int64, C.c_float, P]),
+            "orc_log_sum_exp": (C.c_double, [P, C.c_int64]),
+            "orc_confidence": (C.c_double, [P, C.c_int64]),
+            "orc_argmax": (C.c_int64, [P, C.c_int64]),
+            "orc_option_orders": (C.c_int64, [C.c_int64, C.c_int64, P]),
+            "orc_label_readout": (None, [P, C.c_int64, P, C.c_int64, C.c_float, P, P, C.POINTER(C.c_double)]),
+            "orc_pointer_logits": (None, [C.c_int64, C.c_int64, P, P, P, P, P, P, C.c_int64, P]),
+            "orc_fold_mean": (None, [C.c_int64, C.c_int64, P, P, C.c_float, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data
+
+
+# ------------------------------------------------------------- scalars
+
+def f32_to_f16(x: float) -> int:
+    return int(lib().orc_f32_to_f16(C.c_float(x)))
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().orc_f16_to_f32(h))
+
+
+def rng_values(seed: int, n: int, scale: float = 1.0) -> tuple[np.ndarray, int]:
+    """n values of the reference.rs:17-28 xorshift from state `seed`; returns
+    (values, next state)."""
+    s = C.c_uint64(seed)
+    out = np.zeros(n, np.float32)
+    lib().orc_rng_values(C.byref(s), out.ctypes.data_as(C.POINTER(C.c_float)), n, scale)
+    return out, s.value
+
+
+def quantize(dtype: int, values: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    v = np.ascontiguousarray(values, np.float32).ravel()
+    data = np.zeros(v.size if dtype == Q8 else v.size // 2, np.uint8)
+    scales = np.zeros(v.size // 32 * 2, np.uint8)
+    fn = lib().orc_quantize_q8 if dtype == Q8 else lib().orc_quantize_q4
+    if fn(_ptr(v), v.size, _ptr(data), _ptr(scales)) != 0:
+        raise ValueError("oracle quantize: length must be a multiple of 32")
+    return data, scales
+
+
+def get(dtype: int, data: np.ndarray, scales: np.ndarray, n: int) -> np.ndarray:
+    return np.array([lib().orc_get(dtype, _ptr(data), _ptr(scales) if scales.size else None, i) for i in range(n)],
+                    np.float32)
+
+
+# --------------------------------------------------------------- model
+
+def config_from_json(text: str) -> orc_config:
+    """The subset of model.rs:66-210 the oracle needs (Gemma 3 text)."""
+    v = json.loads(text)
+    v = v.get("text_config", v)
+    L = int(v["num_hidden_layers"])
+    if "layer_types" in v:
+        sliding = [t == "sliding_attention" for t in v["layer_types"]]
+    else:
+        k = int(v.get("_sliding_window_pattern", 6))
+        sliding = [(i + 1) % k != 0 for i in range(L)]
+    hd = int(v["head_dim"])
+    ff = v["intermediate_size"]
+    ff = list(ff) if isinstance(ff, list) else [int(ff)] * L
+    c = orc_config()
+    c.vocab, c.d, c.layers = int(v["vocab_size"]), int(v["hidden_size"]), L
+    c.heads, c.kv_heads = int(v["num_attention_heads"]), int(v["num_key_value_heads"])
+    for i in range(L):
+        c.head_dim[i], c.ff[i], c.sliding[i], c.kv_source[i], c.rope_dims[i] = hd, ff[i], int(sliding[i]), i, hd
+    c.eps = float(v.get("rms_norm_eps", 1e-6))
+    c.window = int(v.get("sliding_window", 512))
+    c.theta_global = float(v.get("rope_theta", 1e6))
+    c.theta_local = float(v.get("rope_local_base_freq", 1e4))
+    c.query_scale = float(np.float32(v.get("query_pre_attn_scalar", hd)) ** np.float32(-0.5))
+    c.norm_offset = float(v.get("omg_norm_offset", 1.0))
+    c.v_norm, c.softcap, c.bos = 0, float(v.get("final_logit_softcapping", 0.0)), int(v.get("bos_token_id", 2))
+    return c
+
+
+class Model:
+    """orc_model: dequantized weights + the reference CPU forward."""
+
+    def __init__(self, config_text: str, tensors, gpu_rounding: bool = False):
+        self.cfg = config_from_json(config_text)
+        self._h = lib().orc_model_new(C.byref(self.cfg), int(gpu_rounding))
+        if not self._h:
+            raise ValueError("oracle: bad config")
+        for t in tensors:
+            rows, cols = (t.shape[0], t.shape[1]) if len(t.shape) == 2 else (1, t.shape[0])
+            rc = lib().orc_model_set(self._h, t.name.encode(), t.dtype, rows, cols, _ptr(t.data),
+                                     _ptr(t.scales) if t.scales.size else None)
+            if rc != 0:
+                raise ValueError(f"oracle: cannot set {t.name}")
+        buf = C.create_string_buffer(1 << 16)
+        if lib().orc_model_missing(self._h, buf, len(buf)):
+            raise ValueError("oracle: missing " + buf.value.decode())
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_model_free(self._h)
+            self._h = None
+
+    def forward(self, ids, pos, seq) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.uint32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        seq = np.ascontiguousarray(seq, np.int32)
+        out = np.zeros((ids.size, self.cfg.d), np.float32)
+        rc = lib().orc_forward(self._h, _ptr(ids), _ptr(pos), _ptr(seq), ids.size, _ptr(out))
+        if rc != 0:
+            raise ValueError(f"oracle forward failed ({rc})")
+        return out
+
+    def logits(self, rows: np.ndarray) -> np.ndarray:
+        rows = np.ascontiguousarray(rows, np.float32)
+        out = np.zeros((rows.shape[0], self.cfg.vocab), np.float32)
+        lib().orc_logits(self._h, _ptr(rows), rows.shape[0], _ptr(out))
+        return out
+
+
+def pack_single(prefix, branches) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """tests/reference.rs:368-378 pack(): one group, seq 0 for the prefix and
+    b + 1 for branch b; returns (ids, pos, seq)."""
+    ids, pos, seq = list(prefix), list(range(len(prefix))), [0] * len(prefix)
+    for bi, b in enumerate(branches):
+        for j, t in enumerate(b.tokens):
+            ids.append(t)
+            pos.append(len(prefix) + j)
+            seq.append(bi + 1)
+    return np.array(ids, np.uint32), np.array(pos, np.int32), np.array(seq, np.int32)
+
+
+def pack(groups, first: int = 0, resident: bool = False):
+    """engine.rs:1512-1571 restated in C (orc_pack): (ids, meta[n,4], wanted[r,4])."""
+    keep = []
+    arr = (orc_group * len(groups))()
+    total = rows = 0
+    for gi, g in enumerate(groups):
+        p = np.ascontiguousarray(g.prefix, np.uint32)
+        br = (orc_branch * max(1, len(g.branches)))()
+        for bi, b in enumerate(g.branches):
+            t = np.ascontiguousarray(b.tokens, np.uint32)
+            w = np.ascontiguousarray(b.want, np.int64)
+            keep += [t, w]
+            br[bi].tokens = t.ctypes.data_as(C.POINTER(C.c_uint32))
+            br[bi].ntokens = t.size
+            br[bi].want = w.ctypes.data_as(C.POINTER(C.c_int64))
+            br[bi].nwant = w.size
+            total += t.size
+            rows += w.size
+        keep += [p, br]
+        total += p.size
+        arr[gi].prefix = p.ctypes.data_as(C.POINTER(C.c_uint32))
+        arr[gi].prefix_len = p.size
+        arr[gi].branches = br
+        arr[gi].nbranches = len(g.branches)
+    ids = np.zeros(max(total, 1), np.uint32)
+    meta = np.zeros((max(total, 1), 4), np.int32)
+    wanted = np.zeros((max(rows, 1), 4), np.int64)
+    decoded = np.zeros((max(len(groups), 1), 2), np.int64)
+    n_ids, n_w, n_d = C.c_int64(), C.c_int64(), C.c_int64()
+    rc = lib().orc_pack(arr, len(groups), first, int(resident), _ptr(ids), _ptr(meta), _ptr(wanted), _ptr(decoded),
+                        C.byref(n_ids), C.byref(n_w), C.byref(n_d))
+    if rc != 0:
+        raise ValueError(f"oracle pack failed ({rc})")
+    return ids[:n_ids.value], meta[:n_ids.value], wanted[:n_w.value], decoded[:n_d.value]
+
+
+# --------------------------------------------------------------- state
+
+def state_key(model_id: str, prefix) -> int:
+    p = np.ascontiguousarray(prefix, np.uint32)
+    return int(lib().orc_state_key(model_id.encode(), _ptr(p) if p.size else None, p.size))
+
+
+def state_rows(sliding: bool, window: int, p: int) -> tuple[int, int]:
+    r0, r1 = C.c_int64(), C.c_int64()
+    lib().orc_state_rows(int(sliding), window, p, C.byref(r0), C.byref(r1))
+    return r0.value, r1.value
+
+
+# ------------------------------------------------------------- readout
+
+def softmax(z, temperature: float = 1.0) -> np.ndarray:
+    z = np.ascontiguousarray(z, np.float32)
+    out = np.zeros(z.size, np.float64)
+    lib().orc_softmax(_ptr(z), z.size, temperature, _ptr(out))
+    return out
+
+
+def log_sum_exp(z) -> float:
+    z = np.ascontiguousarray(z, np.float32)
+    return float(lib().orc_log_sum_exp(_ptr(z), z.size))
+
+
+def confidence(p) -> float:
+    p = np.ascontiguousarray(p, np.float64)
+    return float(lib().orc_confidence(_ptr(p), p.size))
+
+
+def argmax(p) -> int:
+    p = np.ascontiguousarray(p, np.float64)
+    return int(lib().orc_argmax(_ptr(p), p.size))
+
+
+def option_orders(k: int, n: int) -> list[list[int]]:
+    out = np.zeros(max(1, 2 * k * k), np.int64)
+    cnt = lib().orc_option_orders(k, n, _ptr(out))
+    return [list(map(int, out[r * k:(r + 1) * k])) for r in range(cnt)]
+
+
+def label_readout(row, label_ids, temperature: float = 1.0):
+    """readout.rs:124-146: (label logits, probs, candidate mass)."""
+    row = np.ascontiguousarray(row, np.float32)
+    lab = np.ascontiguousarray(label_ids, np.uint32)
+    logits = np.zeros(lab.size, np.float32)
+    probs = np.zeros(lab.size, np.float64)
+    mass = C.c_double()
+    lib().orc_label_readout(_ptr(row), row.size, _ptr(lab), lab.size, temperature, _ptr(logits), _ptr(probs),
+                            C.byref(mass))
+    return logits, probs, mass.value
+
+
+def pointer_logits(w_q, b_q, w_k, b_k, decide, opts) -> np.ndarray:
+    w_q, b_q, w_k, b_k, decide, opts = (np.ascontiguousarray(a, np.float32) for a in (w_q, b_q, w_k, b_k, decide, opts))
+    dp, d = w_q.shape
+    out = np.zeros(opts.shape[0], np.float32)
+    lib().orc_pointer_logits(d, dp, _ptr(w_q), _ptr(b_q), _ptr(w_k), _ptr(b_k), _ptr(decide), _ptr(opts),
+                             opts.shape[0], _ptr(out))
+    return out
+
+
+def fold_mean(orders, logits, excluded: float = -1e4) -> np.ndarray:
+    orders = np.ascontiguousarray(orders, np.int64)
+    logits = np.ascontiguousarray(logits, np.float32)
+    nruns, k = orders.shape
+    out = np.zeros(k, np.float32)
+    lib().orc_fold_mean(k, nruns, _ptr(orders), _ptr(logits), excluded, _ptr(out))
+    return out

@@ -1,0 +1,249 @@
+"""The engine against the CPU oracle on identical seeded weights and token
+ids, and the reference's invariants, through the C ABI on the GPU.  Each
+test mirrors one of crates/omg-wgpu/tests/reference.rs:380-735."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import grande_amd as g
+import oracle
+from grande_amd import BranchTokens, Group, PrefixSource, Want
+from tests.common import assert_close, build, gemma3_tiny, gguf_tiny, oracle_rows, rel_diff
+
+pytestmark = pytest.mark.gpu
+
+PREFIX = [2, 5, 9, 14, 20, 31, 7, 8, 3, 22]
+BRANCHES = [BranchTokens([11, 12, 13, 14, 15], [1, 4]), BranchTokens([30, 31, 32, 33, 34, 35, 36, 37], [0, 7])]
+
+
+def check_hidden(cfg: str, seed: int, linear: int, embed: int, tol: float = 2e-2, tight: float = 4e-3,
+                 prefix=PREFIX, branches=BRANCHES):
+    """reference.rs:380-407: rows at the wanted positions within `tol`
+    (relative to the row's largest magnitude) of the plain f32 forward, and
+    within `tight` of the forward with the GPU path's f16 rounding points."""
+    eng, plain, gpu_r, _ = build(cfg, seed, linear, embed)
+    out = eng.evaluate(prefix, branches, Want.HIDDEN)
+    exp_plain = oracle_rows(plain, prefix, branches)
+    exp_gpu = oracle_rows(gpu_r, prefix, branches)
+    worst_p = worst_g = 0.0
+    for o, ep, eg in zip(out, exp_plain, exp_gpu):
+        for got, a, b in zip(o.rows, ep, eg):
+            worst_p = max(worst_p, rel_diff(got, a))
+            worst_g = max(worst_g, rel_diff(got, b))
+    print(f"rel diff vs f32 oracle {worst_p:.2e}, vs f16-rounding oracle {worst_g:.2e}")
+    assert worst_p < tol, f"relative diff {worst_p} vs the f32 oracle"
+    assert worst_g < tight, f"relative diff {worst_g} vs the f16-rounding oracle"
+
+
+def test_gemma3_matches_cpu_reference():
+    check_hidden(gemma3_tiny(), 7, g.F16, g.F16)
+
+
+def test_q8_matches_cpu_reference():
+    check_hidden(gguf_tiny(), 7, g.Q8, g.Q8)
+
+
+def test_q4_matches_cpu_reference():
+    check_hidden(gguf_tiny(), 9, g.Q4, g.Q8)
+
+
+@pytest.mark.parametrize("heads,kv", [(8, 2), (4, 2), (2, 2), (16, 1)])
+def test_gqa_q4_matches_cpu_reference(heads, kv):
+    """Every query-heads-per-KV-head grouping the attention kernel packs."""
+    check_hidden(gguf_tiny(heads, kv), 11, g.Q4, g.Q8)
+
+
+def test_long_prefix_sliding_window_matches_cpu_reference():
+    """Keys beyond one 64-row tile, windows cutting through tiles, branches
+    straddling tile boundaries."""
+    rng = np.random.default_rng(3)
+    cfg = gguf_tiny(4, 1, window=37, vocab=64)
+    prefix = rng.integers(0, 64, 150).tolist()
+    branches = [BranchTokens(rng.integers(0, 64, n).tolist(), [n - 1, n // 2]) for n in (23, 9, 41)]
+    eng, plain, gpu_r, _ = build(cfg, 21, g.Q4, g.Q8, capacity=256)
+    out = eng.evaluate(prefix, branches, Want.HIDDEN)
+    for o, ep, eg in zip(out, oracle_rows(plain, prefix, branches), oracle_rows(gpu_r, prefix, branches)):
+        for got, a, b in zip(o.rows, ep, eg):
+            assert rel_diff(got, a) < 2e-2
+            assert rel_diff(got, b) < 4e-3
+
+
+def test_resident_prefix_matches_full_pass():
+    """reference.rs:430-480: bit-equal rows over a resident prefix."""
+    for cfg, lin, emb in [(gemma3_tiny(), g.F16, g.F16), (gguf_tiny(), g.Q4, g.Q8), (gguf_tiny(8, 2), g.Q4, g.Q8)]:
+        eng, _, _, _ = build(cfg, 13, lin, emb, oracle_models=False)
+        prefix = [2, 5, 9, 14, 20, 31, 7]
+        branches = [BranchTokens([11, 12, 13, 14, 15], [1, 4]), BranchTokens([30, 31, 32], [0, 2])]
+        other = [BranchTokens([33, 34, 35, 36, 37, 38], [5])]
+        full = eng.evaluate(prefix, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.DECODED
+        cont = eng.evaluate(prefix, other, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.RESIDENT
+        eng.evict_resident()
+        cold = eng.evaluate(prefix, other, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.DECODED
+        assert all(np.array_equal(a, b) for a, b in zip(cont[0].rows, cold[0].rows))
+        again = eng.evaluate(prefix, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.RESIDENT
+        for a, b in zip(full, again):
+            assert all(np.array_equal(x, y) for x, y in zip(a.rows, b.rows))
+        prefix2 = [2, 3, 4]
+        p2 = eng.evaluate(prefix2, branches, Want.LOGITS)
+        assert eng.prefix_source() == PrefixSource.DECODED
+        p2r = eng.evaluate(prefix2, branches, Want.LOGITS)
+        assert eng.prefix_source() == PrefixSource.RESIDENT
+        for a, b in zip(p2, p2r):
+            assert all(np.array_equal(x, y) for x, y in zip(a.rows, b.rows))
+
+
+def test_state_cache_restores_exactly(tmp_path):
+    """reference.rs:482-522: RAM cache and GRWS1 bytes restore bit-equal rows;
+    a foreign model id is refused."""
+    for cfg, lin, emb in [(gemma3_tiny(), g.F16, g.F16), (gguf_tiny(), g.Q4, g.Q8), (gguf_tiny(8, 2), g.Q4, g.Q8)]:
+        eng, _, _, _ = build(cfg, 17, lin, emb, oracle_models=False)
+        eng.set_state_cache(64 << 20, None, "test")
+        a = [2, 5, 9, 14, 20, 31, 7, 8, 3, 22, 4, 6]
+        b = [2, 3, 4]
+        branches = [BranchTokens([11, 12, 13, 14, 15], [0, 2, 4])]
+        full_a = eng.evaluate(a, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.DECODED
+        saved = eng.save_state(a, "test")
+        eng.evaluate(b, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.DECODED
+        ram_a = eng.evaluate(a, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.RAM
+        assert all(np.array_equal(x, y) for x, y in zip(full_a[0].rows, ram_a[0].rows))
+        assert g.state_check(saved, "test")[0] == len(a)
+        with pytest.raises(g.OmgError):
+            g.state_check(saved, "other")
+        with pytest.raises(g.OmgError):
+            eng.restore_state(saved, "other")
+        eng.evaluate(b, branches, Want.HIDDEN)
+        eng.evict_resident()
+        eng.restore_state(saved, "test")
+        assert eng.is_resident(a)
+        file_a = eng.evaluate(a, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.RESIDENT
+        assert all(np.array_equal(x, y) for x, y in zip(full_a[0].rows, file_a[0].rows))
+        # The on-disk cache: a fresh RAM budget of 0, files only.
+        eng.set_state_cache(0, tmp_path / "states", "test")
+        eng.evict_resident()
+        eng.evaluate(a, branches, Want.HIDDEN)
+        eng.evaluate(b, branches, Want.HIDDEN)
+        disk_a = eng.evaluate(a, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.DISK
+        assert all(np.array_equal(x, y) for x, y in zip(full_a[0].rows, disk_a[0].rows))
+        name = f"{g.state_key('test', a):016x}.state"
+        assert (tmp_path / "states" / name).exists()
+
+
+def test_branches_do_not_see_each_other():
+    """reference.rs:533-562: a branch's rows are bit-equal whatever its
+    siblings are."""
+    for cfg, lin, emb in [(gemma3_tiny(), g.F16, g.F16), (gguf_tiny(), g.Q8, g.Q8), (gguf_tiny(8, 2), g.Q4, g.Q8)]:
+        eng, _, _, _ = build(cfg, 11, lin, emb, oracle_models=False)
+        prefix = [2, 4, 6, 8]
+        a = BranchTokens([10, 11, 12], [2])
+        b1 = BranchTokens([20, 21, 22, 23], [3])
+        b2 = BranchTokens([30, 31], [1])
+        with_b1 = eng.evaluate(prefix, [a, b1], Want.HIDDEN)
+        with_b2 = eng.evaluate(prefix, [a, b2], Want.HIDDEN)
+        alone = eng.evaluate(prefix, [a], Want.HIDDEN)
+        assert np.array_equal(with_b1[0].rows[0], with_b2[0].rows[0])
+        assert np.array_equal(with_b1[0].rows[0], alone[0].rows[0])
+
+
+def test_logits_are_hidden_times_embedding():
+    """reference.rs:564-598 (Gemma 3 has no softcap)."""
+    for cfg, lin, emb in [(gemma3_tiny(), g.F16, g.F16), (gguf_tiny(), g.Q8, g.Q8), (gguf_tiny(), g.Q4, g.Q4)]:
+        eng, plain, _, w = build(cfg, 3, lin, emb)
+        prefix = [2, 1, 3]
+        branches = [BranchTokens([4, 5], [1])]
+        hidden = eng.evaluate(prefix, branches, Want.HIDDEN)[0].rows[0]
+        logits = eng.evaluate(prefix, branches, Want.LOGITS)[0].rows[0]
+        expected = plain.logits(hidden[None, :])[0]
+        scale = max(float(np.max(np.abs(expected))), 1.0)
+        assert np.max(np.abs(logits - expected)) / scale < 1e-3
+        labels = [1, 7, 3, 30]
+        lab = eng.evaluate(prefix, branches, Want.LABELS, labels)[0].rows[0]
+        assert np.array_equal(lab, logits[labels])
+
+
+def test_groups_match_separate_passes():
+    """reference.rs:612-715: several requests in one pass give each the rows
+    it gets alone; the batch restores / decodes / remembers prefixes as the
+    reference's admit + run do."""
+    for cfg, lin, emb in [(gemma3_tiny(), g.F16, g.F16), (gguf_tiny(), g.Q4, g.Q8), (gguf_tiny(8, 2), g.Q4, g.Q8)]:
+        eng, _, _, _ = build(cfg, 19, lin, emb, oracle_models=False)
+        eng.set_state_cache(64 << 20, None, "test")
+        prefixes = [[2, 5, 9, 14, 20, 31, 7, 8, 3], [2, 3, 4], [2, 22, 4, 6, 9, 9, 14, 1, 30, 31, 5]]
+        branches = [
+            [BranchTokens([11, 12, 13, 14, 15], [1, 4]), BranchTokens([30, 31, 32], [0, 2])],
+            [BranchTokens([33, 34, 35, 36, 37, 38], [5])],
+            [BranchTokens([7, 8], [1]), BranchTokens([11, 12, 13, 14, 15, 16, 17], [3, 6]),
+             BranchTokens([1, 2, 3], [2])],
+        ]
+        groups = [Group(p, b) for p, b in zip(prefixes, branches)]
+        for want in (Want.HIDDEN, Want.LOGITS):
+            alone = []
+            for gr in groups:
+                eng.evict_resident()
+                alone.append(eng.evaluate(gr.prefix, gr.branches, want))
+            eng.evict_resident()
+            together = eng.evaluate_groups(groups, want)
+            for i, (a, t) in enumerate(zip(alone, together)):
+                assert len(t.branches) == len(a)
+                for x, y in zip(a, t.branches):
+                    assert_close(x.rows, y.rows, f"group {i} in the batch")
+            assert together[0].prefix_source == PrefixSource.RAM
+            assert together[1].prefix_source == PrefixSource.DECODED
+            assert together[2].prefix_source == PrefixSource.DECODED
+            assert eng.is_resident(prefixes[0])
+            eng.evaluate(prefixes[1], branches[1], want)
+            again = eng.evaluate_groups(groups, want)
+            assert again[1].prefix_source == PrefixSource.RESIDENT
+            for i, (a, t) in enumerate(zip(alone, again)):
+                for x, y in zip(a, t.branches):
+                    assert_close(x.rows, y.rows, f"group {i} with group 1 resident")
+            eng.evaluate(prefixes[1], branches[1], want)
+            from_cache = eng.evaluate(prefixes[2], branches[2], want)
+            assert eng.prefix_source() == PrefixSource.RAM
+            for x, y in zip(alone[2], from_cache):
+                assert_close(x.rows, y.rows, "group 2 from the state cache")
+
+
+def test_request_errors_are_reported_not_raised_on_device():
+    """engine.rs:1503-1581: every bad request fails with an error and leaves
+    the engine usable."""
+    eng, _, _, _ = build(gemma3_tiny(), 5, g.F16, g.F16, capacity=32, max_rows=4, oracle_models=False)
+    ok = eng.evaluate([2, 3], [BranchTokens([4, 5], [1])], Want.HIDDEN)
+    cases = [
+        ([2] * 30, [BranchTokens([4, 5, 6], [0])], "capacity"),
+        ([2, 3], [BranchTokens([4, 5], [0, 1])] * 3, "rows"),
+        ([2, 3], [BranchTokens([40], [0])], "vocabulary"),
+        ([2, 3], [BranchTokens([4, 5], [2])], "past"),
+    ]
+    for prefix, branches, what in cases:
+        with pytest.raises(g.OmgError) as e:
+            eng.evaluate(prefix, branches, Want.HIDDEN)
+        assert what in e.value.message, e.value.message
+    with pytest.raises(g.OmgError):
+        eng.evaluate([2], [BranchTokens([3], [0])] * 4096, Want.HIDDEN)
+    with pytest.raises(g.OmgError):
+        eng.evaluate_groups([], Want.HIDDEN)
+    again = eng.evaluate([2, 3], [BranchTokens([4, 5], [1])], Want.HIDDEN)
+    assert np.array_equal(ok[0].rows[0], again[0].rows[0])
+
+
+def test_open_dir_loads_an_exported_directory(tmp_path):
+    """backend.rs:28-71 over the tools/export_wgpu_gguf.py layout."""
+    cfg = gguf_tiny()
+    w = g.Weights.synth(cfg, 23, g.Q4, g.Q8)
+    g.export_dir(w, tmp_path / "model")
+    a = g.Engine.new(w, 64, 8)
+    b = g.Engine.open_dir(tmp_path / "model", 64, 8)
+    prefix, branches = [2, 5, 9], [BranchTokens([4, 6, 8], [2])]
+    ra = a.evaluate(prefix, branches, Want.HIDDEN)[0].rows[0]
+    rb = b.evaluate(prefix, branches, Want.HIDDEN)[0].rows[0]
+    assert np.array_equal(ra, rb)

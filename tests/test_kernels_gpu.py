@@ -1,0 +1,118 @@
+"""Kernel-level parity on the GPU through the C ABI: the MFMA GEMM and the
+gated GeGLU GEMM against a CPU GEMM with the same f16 rounding points, on
+the odd shapes of the reference's kernel tests
+(crates/omg-wgpu/tests/matmul.rs:201-290, relative tolerance 2e-3) and on
+the 270M configuration's shapes; the embedding gather bit-exact."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import grande_amd as g
+import oracle
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DTYPES = [g.F16, g.Q8, g.Q4]
+
+
+def weight(rng: np.random.Generator, n: int, k: int, dtype: int, name: str = "w") -> tuple[g.QTensor, np.ndarray]:
+    """[n, k] weight in `dtype` and its dequantized values rounded to f16 —
+    the kernel's rounding point (matmul.rs:178-199)."""
+    v = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    if dtype == g.F16:
+        t = g.QTensor(name, g.F16, (n, k), v.astype(np.float16).view(np.uint8).ravel().copy(), np.zeros(0, np.uint8))
+    else:
+        data, scales = oracle.quantize(dtype, v)
+        t = g.QTensor(name, dtype, (n, k), data, scales)
+    return t, t.to_f32().astype(np.float16).astype(np.float32)
+
+
+def gelu(x):
+    return 0.5 * x * (1.0 + np.tanh(0.7978845608 * (x + 0.044715 * x ** 3)))
+
+
+def dev(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,n,k", [(23, 96, 64), (130, 200, 96), (64, 128, 32), (1, 640, 2048),
+                                   (384, 1536, 640), (2384, 640, 2048), (257, 1152, 1152)])
+def test_gemm_matches_cpu(m, n, k, dtype):
+    rng = np.random.default_rng(m * n * k + dtype)
+    x = (rng.uniform(-1, 1, (m, k)) * 4).astype(np.float16)
+    t, wd = weight(rng, n, k, dtype)
+    w = g.DeviceWeight(t)
+    xd = dev(x)
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    w.gemm(xd.data_ptr(), k, m, y.data_ptr(), n)
+    torch.cuda.synchronize()
+    exp = x.astype(np.float32) @ wd.T
+    got = y.cpu().numpy()
+    worst = float(np.max(np.abs(got - exp) / np.maximum(np.abs(exp), 1.0)))
+    assert worst < 2e-3, f"gemm {dtype} {m}x{n}x{k}: max rel diff {worst}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,n,k", [(23, 96, 64), (70, 100, 160), (384, 2048, 640), (2384, 2048, 640)])
+def test_gated_matches_cpu(m, n, k, dtype):
+    rng = np.random.default_rng(7 * m * n * k + dtype)
+    x = rng.uniform(-1, 1, (m, k)).astype(np.float16)
+    tg, gd = weight(rng, n, k, dtype, "gate")
+    tu, ud = weight(rng, n, k, dtype, "up")
+    wg, wu = g.DeviceWeight(tg), g.DeviceWeight(tu)
+    xd = dev(x)
+    act = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+    wg.gemm_geglu(wu, xd.data_ptr(), k, m, act.data_ptr(), n)
+    torch.cuda.synchronize()
+    xf = x.astype(np.float32)
+    exp = gelu(xf @ gd.T) * (xf @ ud.T)
+    got = act.cpu().numpy().astype(np.float32)
+    worst = float(np.max(np.abs(got - exp) / np.maximum(np.abs(exp), 1.0)))
+    assert worst < 2e-3, f"gated {dtype} {m}x{n}x{k}: max rel diff {worst}"
+
+
+def test_gemm_rows_are_independent_of_m():
+    """A row's result does not depend on how many rows share the launch (no
+    split-K, fixed k order): the basis of the bit-equal resident-prefix and
+    isolation invariants."""
+    rng = np.random.default_rng(5)
+    n, k = 640, 2048
+    t, _ = weight(rng, n, k, g.Q4)
+    w = g.DeviceWeight(t)
+    x = rng.uniform(-2, 2, (2384, k)).astype(np.float16)
+    outs = []
+    for m in (2384, 384, 17, 1):
+        y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+        w.gemm(dev(x[:m]).data_ptr(), k, m, y.data_ptr(), n)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0][:o.shape[0]])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_embed_gather_bit_exact(dtype):
+    """embed.wgsl:15-48 = reference.rs:182-189: x = deq(E[id]) * sqrt(d),
+    bit-exact; the fused first norm within f16 rounding."""
+    rng = np.random.default_rng(11 + dtype)
+    vocab, d = 300, 640
+    t, _ = weight(rng, vocab, d, dtype, "embed")
+    w = g.DeviceWeight(t)
+    ids = rng.integers(0, vocab, 97).astype(np.uint32)
+    norm_w = (1.0 + rng.uniform(-0.5, 0.5, d)).astype(np.float32)
+    scale = np.float32(np.sqrt(np.float32(d)))
+    x = torch.zeros((ids.size, d), dtype=torch.float32, device="cuda")
+    hn = torch.zeros((ids.size, d), dtype=torch.float16, device="cuda")
+    idd, wd = dev(ids.view(np.int32)), dev(norm_w)
+    w.embed_norm(idd.data_ptr(), ids.size, float(scale), wd.data_ptr(), 1e-6, x.data_ptr(), hn.data_ptr())
+    torch.cuda.synchronize()
+    deq = t.to_f32()  # exact dequantization, f32
+    exp = (deq[ids] * scale).astype(np.float32)
+    got = x.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), "embedding gather is not bit-exact"
+    ms = (exp.astype(np.float64) ** 2).mean(axis=1, keepdims=True)
+    exp_h = exp / np.sqrt(ms + 1e-6) * norm_w
+    assert np.max(np.abs(hn.cpu().numpy().astype(np.float32) - exp_h)) < 1e-2 * np.max(np.abs(exp_h))
