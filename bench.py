@@ -1,0 +1,204 @@
+"""Benchmark of the decision-path pass on one MI355X.
+
+Workload (the metric's configuration): a
+Gemma-3-270M-shaped decoder with seeded Q4_0 weights and a 25,000-row
+vocabulary, one 2,000-token state plus 12 question branches of 32 tokens
+in one block-causal pass, label readout (26 label logits) at each branch's
+last position.  A step is one cold pass (state + branches, T = 2,384) with
+the token ids and metadata already in HBM; the warm pass (branches only on
+the resident state, T = 384) and the API wall times (host upload and
+readback included) are reported beside it.
+
+Prints one JSON line (see the repository's driver contract).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_F16_TFLOPS = 2500.0   # MI355X dense FP16/BF16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+SEED = 0x5EED
+
+
+def linear_macs_per_token(cfg) -> dict:
+    d, ff, H, KV, hd = cfg["d"], cfg["ff"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    return {"mm_qkv": (H + 2 * KV) * hd * d, "mm_o": d * H * hd, "mm_gate_up": 2 * ff * d, "mm_down": d * ff}
+
+
+def visible_pairs(prefix: int, nb: int, bt: int, window: int, layers: int, pattern: int = 6) -> int:
+    """Query-key pairs the block-causal mask admits over all layers (the
+    attention FLOP count is 4 * heads * head_dim per pair)."""
+    total = 0
+    for layer in range(layers):
+        w = window if (layer + 1) % pattern != 0 else 0
+        for q in range(prefix):
+            total += min(q + 1, w) if w else q + 1
+        for j in range(bt):
+            qp = prefix + j
+            vis_prefix = prefix if not w else max(0, min(prefix, prefix - (qp - w + 1)))
+            vis_own = j + 1 if not w else min(j + 1, w)
+            total += nb * (vis_prefix + vis_own)
+    return total
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this engine runs on one GPU (--gpus {args.gpus} requested); a state's branches would "
+              "shard across GPUs by broadcasting the prefix K/V, which is not built.", file=sys.stderr)
+        return 2
+
+    import grande_amd as g
+    from grande_amd import BranchTokens, Group, Want
+
+    spec = g.BASELINE_CONFIGS[args.config]
+    mc = spec["model"]
+    cfg = g.config_json(**mc)
+    P, NB, BT = spec["state"], spec["branches"], spec["branch_tokens"]
+    T = P + NB * BT
+    rng = np.random.default_rng(SEED)
+    prefix = rng.integers(0, mc["vocab"], P).tolist()
+    branches = [BranchTokens(rng.integers(0, mc["vocab"], BT).tolist(), [BT - 1]) for _ in range(NB)]
+    labels = g.LABEL_IDS
+
+    t0 = time.perf_counter()
+    weights = g.Weights.synth(cfg, SEED, spec["dtype"], spec["dtype"])
+    eng = g.Engine.new(weights, T + 64, 64)
+    load_s = time.perf_counter() - t0
+
+    # API passes (host ids in, label logits out): cold, then warm on the
+    # resident state, then a state save / evict / restore round trip.
+    eng.evict_resident()
+    t = time.perf_counter()
+    cold_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    api_cold_ms = (time.perf_counter() - t) * 1e3
+    t = time.perf_counter()
+    warm_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    api_warm_ms = (time.perf_counter() - t) * 1e3
+    assert eng.prefix_source() == g.PrefixSource.RESIDENT
+    t = time.perf_counter()
+    state = eng.save_state(prefix, "bench")
+    save_ms = (time.perf_counter() - t) * 1e3
+    eng.evict_resident()
+    t = time.perf_counter()
+    eng.restore_state(state, "bench")
+    restore_ms = (time.perf_counter() - t) * 1e3
+    restored_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    restored_equal = all(np.array_equal(a.rows[0], b.rows[0]) for a, b in zip(warm_rows, restored_rows))
+    warm_equal_cold = max(float(np.max(np.abs(a.rows[0] - b.rows[0]))) for a, b in zip(cold_rows, warm_rows))
+
+    def timed(first_resident: bool, steps: int, warmup: int) -> float:
+        eng.prepare([Group(prefix, branches)], Want.LABELS, labels, first_resident=first_resident)
+        for _ in range(warmup):
+            eng.launch()
+        eng.sync()
+        t = time.perf_counter()
+        for _ in range(steps):
+            eng.launch()
+        eng.sync()
+        return (time.perf_counter() - t) / steps
+
+    eng.evict_resident()
+    cold_s = timed(False, args.steps, args.warmup)
+    eng.evaluate(prefix, branches, Want.LABELS, labels)  # leaves the state resident
+    warm_s = timed(True, args.steps, args.warmup)
+
+    # Per-kernel HIP-event times over a second timed region of cold steps.
+    eng.profile(True)
+    timed(False, args.steps, 0)
+    prof = eng.profile_report()
+    eng.profile(False)
+
+    macs = linear_macs_per_token(mc)
+    pairs = visible_pairs(P, NB, BT, mc["window"], mc["layers"])
+    flops = {k: 2.0 * T * v for k, v in macs.items()}
+    flops["attention"] = 4.0 * mc["heads"] * mc["head_dim"] * pairs / mc["layers"]
+    kernels = {}
+    for name, (n, ms) in prof.items():
+        avg_us = ms / n * 1e3
+        entry = {"launches_per_step": n // args.steps, "avg_us": round(avg_us, 2),
+                 "share": round(ms / sum(v[1] for v in prof.values()), 4)}
+        if name in flops:
+            tf = flops[name] / (avg_us * 1e-6) / 1e12
+            entry.update(tflops=round(tf, 1), mfma_frac=round(tf / PEAK_F16_TFLOPS, 4))
+        kernels[name] = entry
+    dom = max((k for k in kernels if k in flops), key=lambda k: prof[k][1])
+    dom_tf = kernels[dom]["tflops"]
+    total_flop = sum(flops.values()) * mc["layers"]
+
+    out = {
+        "metric": "questions/sec + state prefill tok/s (Gemma-3-270M Q4_0, 2k state, 12 Qs), 1 GPU",
+        "value": round(NB / cold_s, 2),
+        "unit": "questions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(cold_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights, f16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded random-init weights and token ids)",
+        "config": {"workload": f"{args.config}: Gemma-3-270M-shaped Q4_0, vocab 25k, state {P} + {NB}x{BT} branches, "
+                               "26-label readout", "tokens": T, "state_tokens": P, "branches": NB,
+                   "branch_tokens": BT},
+        "cold_tok_per_s": round(T / cold_s, 1),
+        "warm_ms": round(warm_s * 1e3, 4),
+        "warm_questions_per_s": round(NB / warm_s, 2),
+        "warm_tok_per_s": round(NB * BT / warm_s, 1),
+        "api_ms": {"cold": round(api_cold_ms, 3), "warm": round(api_warm_ms, 3), "state_save": round(save_ms, 3),
+                   "state_restore": round(restore_ms, 3), "state_bytes": len(state)},
+        "restored_bit_equal": bool(restored_equal),
+        "warm_vs_cold_max_abs_logit": warm_equal_cold,
+        "pass_tflops": round(total_flop / cold_s / 1e12, 2),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": dom_tf, "peak": PEAK_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_F16_TFLOPS, 4), "traffic": None},
+        "kernels": kernels,
+        "load_s": round(load_s, 2),
+    }
+
+    if not args.no_cpu:
+        import oracle
+
+        model = oracle.Model(cfg, list(weights.tensors()))
+        ids, pos, seq = oracle.pack_single(prefix, branches)
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        t = time.perf_counter()
+        hidden = model.forward(ids, pos, seq)
+        rows = np.stack([hidden[P + i * BT + BT - 1] for i in range(NB)])
+        cpu_logits = model.logits(rows)[:, labels]
+        cpu_s = time.perf_counter() - t
+        dp, argmax_same = 0.0, True
+        for i in range(NB):
+            pg = oracle.softmax(cold_rows[i].rows[0])
+            pc = oracle.softmax(cpu_logits[i])
+            dp = max(dp, float(np.max(np.abs(pg - pc))))
+            argmax_same &= int(np.argmax(pg)) == int(np.argmax(pc))
+        out["cpu_baseline"] = {"value": round(NB / cpu_s, 4), "unit": "questions/s", "cores": threads,
+                               "kind": "port", "sample": f"one full cold pass of the same workload ({T} tokens, "
+                               f"{mc['layers']} layers) + label readout, f32 C restatement of the reference CPU "
+                               f"forward, OpenMP", "seconds": round(cpu_s, 3),
+                               "gpu_speedup": round(cpu_s / cold_s, 1)}
+        out["parity"] = {"max_abs_dprob_after_softmax": dp, "argmax_identical": bool(argmax_same), "tol": 2e-2}
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -143,15 +143,17 @@ void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float*
 
 // -------------------------------------------------------------- qk prep
 
-// qk_prep.wgsl:66-114: one wave per (token, head slot); slots are the q
-// heads, then (on layers with their own K/V) the k heads, then the v heads.
+// qk_prep.wgsl:66-114: one wave per (token, head slot), four slots per
+// block; slots are the q heads, then (on layers with their own K/V) the k
+// heads, then the v heads.
 // Head row element e = lane * EPL + i, so the RoPE partner e +- HD/2 sits
 // in lane ^ 32.
 template <int HD>
-__global__ void qk_prep_kernel(QkArgs a) {
+__global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int slots) {
     constexpr int EPL = HD / WAVE;
     constexpr int HALF = HD / 2;
-    const int slot = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int slot = int(blockIdx.y) * 4 + int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    if (slot >= slots) return;
     const int64_t tok = blockIdx.x;
     const int64_t row = a.base + tok;
     const int H = a.heads, KV = a.kv_heads;
@@ -216,10 +218,9 @@ __global__ void qk_prep_kernel(QkArgs a) {
 void launch_qk_prep(hipStream_t s, const QkArgs& a) {
     if (a.t <= 0) return;
     const int slots = a.heads + (a.has_kv ? 2 * a.kv_heads : 0);
-    if (slots * WAVE > 1024) fail(E_INVALID, "qk_prep: too many heads for one block");
     if (a.base + a.t > a.cap_pad || a.cap_pad % 64) fail(E_INVALID, "qk_prep: cache rows out of range");
     if (a.hd != 256) fail(E_INVALID, "qk_prep: head_dim must be 256");
-    qk_prep_kernel<256><<<dim3(unsigned(a.t)), dim3(unsigned(slots * WAVE)), 0, s>>>(a);
+    qk_prep_kernel<256><<<dim3(unsigned(a.t), unsigned((slots + 3) / 4)), dim3(256), 0, s>>>(a, slots);
     OMG_HIP(hipGetLastError());
 }
 

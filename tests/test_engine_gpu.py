@@ -170,6 +170,15 @@ def test_logits_are_hidden_times_embedding():
         assert np.array_equal(lab, logits[labels])
 
 
+# Rows of one request at another cache offset meet their keys in other
+# 64-key tiles.  The attention kernel rounds each probability to f16 for the
+# P.V MFMA relative to the running maximum at that tile, so those rows move
+# by f16 rounding (about 5e-4 relative per probability, ~2e-4 on a row)
+# where the reference's f32 probabilities move by ~1e-5; a layout bug moves
+# them by O(1).
+GROUPS_TOL = 1e-3
+
+
 def test_groups_match_separate_passes():
     """reference.rs:612-715: several requests in one pass give each the rows
     it gets alone; the batch restores / decodes / remembers prefixes as the
@@ -195,7 +204,7 @@ def test_groups_match_separate_passes():
             for i, (a, t) in enumerate(zip(alone, together)):
                 assert len(t.branches) == len(a)
                 for x, y in zip(a, t.branches):
-                    assert_close(x.rows, y.rows, f"group {i} in the batch")
+                    assert_close(x.rows, y.rows, f"group {i} in the batch", GROUPS_TOL)
             assert together[0].prefix_source == PrefixSource.RAM
             assert together[1].prefix_source == PrefixSource.DECODED
             assert together[2].prefix_source == PrefixSource.DECODED
@@ -205,12 +214,12 @@ def test_groups_match_separate_passes():
             assert again[1].prefix_source == PrefixSource.RESIDENT
             for i, (a, t) in enumerate(zip(alone, again)):
                 for x, y in zip(a, t.branches):
-                    assert_close(x.rows, y.rows, f"group {i} with group 1 resident")
+                    assert_close(x.rows, y.rows, f"group {i} with group 1 resident", GROUPS_TOL)
             eng.evaluate(prefixes[1], branches[1], want)
             from_cache = eng.evaluate(prefixes[2], branches[2], want)
             assert eng.prefix_source() == PrefixSource.RAM
             for x, y in zip(alone[2], from_cache):
-                assert_close(x.rows, y.rows, "group 2 from the state cache")
+                assert_close(x.rows, y.rows, "group 2 from the state cache", GROUPS_TOL)
 
 
 def test_request_errors_are_reported_not_raised_on_device():
