@@ -310,6 +310,23 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.wanted_ = DevBuf(size_t(max_rows) * 4);
     E.labels_ = DevBuf(size_t(c.vocab) * 4);
     E.kv_stage_ = DevBuf(size_t(E.cap_pad_ * 2 * c.kv_heads * hd) * 2);
+    // Attention work: sliding layers never split a query tile's key range
+    // (it is at most window + branch long); global layers split it at fixed
+    // multiples of `chunk` key tiles, at most ~8 chunks per tile.
+    {
+        const int64_t key_tiles = E.cap_pad_ / 64;
+        const int64_t tpb = 4 * (16 / (c.heads / c.kv_heads));
+        const int64_t qtiles = (capacity + tpb - 1) / tpb;
+        E.attn_chunk_[0] = 0;
+        E.attn_chunk_[1] = int(std::max<int64_t>(8, (key_tiles + 7) / 8));
+        const int64_t per_tile = (key_tiles + E.attn_chunk_[1] - 1) / E.attn_chunk_[1] + 1;
+        E.attn_items_[0] = DevBuf(size_t(qtiles) * 16);
+        E.attn_merges_[0] = DevBuf(16);
+        E.attn_items_[1] = DevBuf(size_t(qtiles * per_tile) * 16);
+        E.attn_merges_[1] = DevBuf(size_t(qtiles) * 16);
+        E.part_o_ = DevBuf(size_t(qtiles * per_tile) * 64 * size_t(hd) * 4);
+        E.part_ml_ = DevBuf(size_t(qtiles * per_tile) * 64 * 2 * 4);
+    }
     // The K/V cache starts zeroed: a masked key's probability is exactly 0
     // and its V row must be finite for the 0 * V product to vanish.
     for (int64_t l = 0; l < c.layers; ++l) {
@@ -456,6 +473,20 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     for (int64_t r = 0; r < nr; ++r) w[r] = int32_t(pk.wanted[size_t(r)][3]);
     if (nr) OMG_HIP(hipMemcpyAsync(wanted_.p, w, size_t(nr) * 4, hipMemcpyHostToDevice, stream_));
     off += size_t(max_rows_) * 4;
+    // Attention work lists for both layer types.
+    for (int kind = 0; kind < 2; ++kind) {
+        AttnWork w;
+        attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), kind == 0 ? int(cfg_.window) : 0,
+                       attn_chunk_[kind], w);
+        if (w.items.size() * 16 > attn_items_[kind].bytes || w.merges.size() * 16 > std::max<size_t>(16, attn_merges_[kind].bytes))
+            fail(E_CAPACITY, "attention work list larger than its buffer");
+        n_items_[kind] = int64_t(w.items.size());
+        n_merges_[kind] = int64_t(w.merges.size());
+        if (!w.items.empty())
+            OMG_HIP(hipMemcpy(attn_items_[kind].p, w.items.data(), w.items.size() * 16, hipMemcpyHostToDevice));
+        if (!w.merges.empty())
+            OMG_HIP(hipMemcpy(attn_merges_[kind].p, w.merges.data(), w.merges.size() * 16, hipMemcpyHostToDevice));
+    }
     if (nlabels > 0) {
         if (nlabels > cfg_.vocab) fail(E_INVALID, "more labels than vocabulary rows");
         for (int64_t i = 0; i < nlabels; ++i)
@@ -515,7 +546,11 @@ void Engine::forward(int64_t t, int64_t base) {
             a.kv_heads = int(c.kv_heads);
             a.hd = int(hd);
             a.window = c.sliding[size_t(l)] ? int(c.window) : 0;
-            launch_attention(stream_, a);
+            a.part_o = part_o_.as<float>();
+            a.part_ml = part_ml_.as<float>();
+            const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
+            launch_attention(stream_, a, attn_items_[kind].as<int4>(), n_items_[kind], attn_merges_[kind].as<int4>(),
+                             n_merges_[kind]);
         });
         step("mm_o", [&] {
             launch_gemm(stream_, attn_.as<half_t>(), c.heads * hd, L.o.w, a_.as<float>(), d, t);

@@ -184,6 +184,10 @@ class Engine {
     DevBuf inv_freq_local_, inv_freq_global_;
     // workspace
     DevBuf ids_, meta_, x_, hn_, qkv_, q16_, attn_, a_, act_, rows_, logits_, wanted_, labels_, kv_stage_;
+    // attention work lists of the current pass: [0] sliding layers, [1] global
+    int attn_chunk_[2] = {0, 0};
+    DevBuf attn_items_[2], attn_merges_[2], part_o_, part_ml_;
+    int64_t n_items_[2] = {0, 0}, n_merges_[2] = {0, 0};
     std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
     // pinned host staging
     void* h_in_ = nullptr;

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <vector>
 
 namespace omg {
 
@@ -85,10 +86,25 @@ struct AttnArgs {
     const half_t* vt;    // [kv_heads][cap_pad/64][hd][64]
     const int32_t* meta; // per cache row
     half_t* out;         // [t][heads][hd]
+    float* part_o;       // chunk partials: [slot][64 rows][hd] unnormalised O
+    float* part_ml;      // [slot][64 rows][2]: running max (log2 units), sum
     int64_t t, base, cap_pad;
     int heads, kv_heads, hd;
     int window;          // 0 = global layer
 };
-void launch_attention(hipStream_t s, const AttnArgs& a);
+// The pass's attention work: items (query tile, first key tile, end key
+// tile, partial slot or -1) and, for split tiles, merges (query tile, first
+// slot, slot count, 0).
+struct AttnWork {
+    std::vector<int4> items, merges;
+    int slots = 0;
+};
+// Build the work of one layer type from the pass's per-token metadata
+// (4 ints per token of this pass, in workspace order).  chunk = key tiles
+// per split (0 = never split).
+void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk,
+                    AttnWork& w);
+void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, const int4* merges,
+                      int64_t nmerges);
 
 }  // namespace omg

@@ -257,51 +257,46 @@ void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int
     OMG_HIP(hipGetLastError());
 }
 
-// logits.wgsl:38-79: one thread per output column (a vocabulary row of E),
-// the wanted rows staged through LDS RM rows x KS columns at a time; E is
-// decoded to f32 (no f16 rounding on this path, as in the reference).
-constexpr int LG_RM = 16, LG_KS = 128, LG_THREADS = 64;
+// logits.wgsl:38-79's product, rows . deq(E[col])^T in f32 (no f16
+// rounding on this path, as in the reference): one wave per output column
+// (a vocabulary row of E) and block of up to 16 wanted rows.  Lanes split
+// the width, so each wave streams its E row once, coalesced, and finishes
+// with one wave reduction per row.  For the label readout the columns are
+// the label ids only.
+constexpr int LG_R = 16;
 
 template <int DT>
-__global__ __launch_bounds__(LG_THREADS) void logits_kernel(DevWeight E, const float* __restrict__ rows,
-                                                            int64_t nrows, const uint32_t* __restrict__ cols,
-                                                            int64_t ncols, float softcap,
-                                                            float* __restrict__ out) {
-    __shared__ float xs[LG_RM][LG_KS];
-    const int64_t j = int64_t(blockIdx.x) * LG_THREADS + threadIdx.x;
-    const bool ok = j < ncols;
-    const int64_t col = ok ? (cols ? int64_t(cols[j]) : j) : 0;
+__global__ __launch_bounds__(256) void logits_kernel(DevWeight E, const float* __restrict__ rows, int64_t nrows,
+                                                     const uint32_t* __restrict__ cols, int64_t ncols,
+                                                     float softcap, float* __restrict__ out) {
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int64_t j = int64_t(blockIdx.x) * 4 + wave;
+    if (j >= ncols) return;
+    const int64_t col = cols ? int64_t(cols[j]) : j;
+    const int64_t r0 = int64_t(blockIdx.y) * LG_R;
+    const int nr = int(nrows - r0 < LG_R ? nrows - r0 : LG_R);
     const int64_t K = E.cols;
-    for (int64_t r0 = 0; r0 < nrows; r0 += LG_RM) {
-        float acc[LG_RM];
+    float acc[LG_R];
 #pragma unroll
-        for (int r = 0; r < LG_RM; ++r) acc[r] = 0.0f;
-        for (int64_t k0 = 0; k0 < K; k0 += LG_KS) {
-            for (int i = int(threadIdx.x); i < LG_RM * LG_KS; i += LG_THREADS) {
-                const int r = i / LG_KS, c = i % LG_KS;
-                xs[r][c] = (r0 + r < nrows && k0 + c < K) ? rows[(r0 + r) * K + k0 + c] : 0.0f;
-            }
-            __syncthreads();
-            if (ok) {
-                const int64_t kn = K - k0 < LG_KS ? K - k0 : LG_KS;
-                for (int64_t kk = 0; kk < kn; kk += 4) {
-                    float wv[4];
-                    load4_f32<DT>(E, col * K + k0 + kk, wv);
+    for (int r = 0; r < LG_R; ++r) acc[r] = 0.0f;
+    for (int64_t q = lane; q < K / 4; q += WAVE) {
+        float wv[4];
+        load4_f32<DT>(E, col * K + 4 * q, wv);
 #pragma unroll
-                    for (int r = 0; r < LG_RM; ++r)
-                        acc[r] += xs[r][kk] * wv[0] + xs[r][kk + 1] * wv[1] + xs[r][kk + 2] * wv[2] +
-                                  xs[r][kk + 3] * wv[3];
-                }
+        for (int r = 0; r < LG_R; ++r) {
+            if (r < nr) {
+                const float4 x = *reinterpret_cast<const float4*>(rows + (r0 + r) * K + 4 * q);
+                acc[r] += x.x * wv[0] + x.y * wv[1] + x.z * wv[2] + x.w * wv[3];
             }
-            __syncthreads();
         }
-        if (ok) {
-            for (int r = 0; r < LG_RM; ++r) {
-                if (r0 + r >= nrows) break;
-                float z = acc[r];
-                if (softcap > 0.0f) z = softcap * tanhf(z / softcap);
-                out[(r0 + r) * ncols + j] = z;
-            }
+    }
+#pragma unroll
+    for (int r = 0; r < LG_R; ++r) {
+        if (r >= nr) break;
+        float z = wave_sum(acc[r]);
+        if (lane == 0) {
+            if (softcap > 0.0f) z = softcap * tanhf(z / softcap);
+            out[(r0 + r) * ncols + j] = z;
         }
     }
 }
@@ -310,7 +305,7 @@ void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t
                    const uint32_t* cols, int64_t ncols, float softcap, float* out) {
     if (nrows <= 0 || ncols <= 0) return;
     if (E.cols % 32 != 0) fail(E_INVALID, "logits: width must be a multiple of 32");
-    const dim3 grid(unsigned((ncols + LG_THREADS - 1) / LG_THREADS)), block(LG_THREADS);
+    const dim3 grid(unsigned((ncols + 3) / 4), unsigned((nrows + LG_R - 1) / LG_R)), block(256);
     switch (E.dtype) {
         case F16_DT: logits_kernel<F16_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out); break;
         case Q8_DT: logits_kernel<Q8_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out); break;
