@@ -12,7 +12,14 @@
 //
 // MFMA operand layout used throughout (16x16x32 f16): lane l supplies
 // A[l % 16][8*(l/16) .. +8) and B[8*(l/16) .. +8)[l % 16]; the f32 result
-// D[4*(l/16) + r][l % 16] lands in element r of the lane's float4.
+// D[4*(l/16) + r][l % 16] lands in element r of the lane's float4.  The
+// weight tile is the A operand and the activation tile the B operand, so
+// D = (X W^T)^T and a lane ends up with four consecutive output columns of
+// one row: the epilogue stores them as one vector.
+//
+// Global loads are buffer loads on per-tile resources: rows past M or N
+// read as zero in hardware, and the K tail is sent out of range the same
+// way, so the loads carry no branches.
 #include <string>
 
 #include "common.h"
@@ -24,18 +31,18 @@ constexpr int G_BK = 64;         // k per LDS stage
 constexpr int G_LDS = G_BK + 8;  // halfs per LDS row: a 16 B pad
 constexpr int G_THREADS = 256;
 
-template <int QUANT>
-struct BWords {
-    static constexpr int N = QUANT == Q4_DT ? 1 : (QUANT == Q8_DT ? 2 : 4);  // uint4 per 32-element block
-};
-
 // One thread's share of a stage between the global loads and the LDS stores.
+// The weight tile is decoded in tasks of one quant block (32 elements), or
+// of half a block when whole blocks would leave threads idle, so that every
+// thread decodes the same amount.
 template <int QUANT, int BM, int BNW>
 struct Stage {
     static constexpr int A_CHUNKS = BM * (G_BK / 8) / G_THREADS;
-    static constexpr int B_TASKS = (BNW * 2 + G_THREADS - 1) / G_THREADS;
+    static constexpr int SPLIT = BNW * 2 < G_THREADS ? 2 : 1;                // tasks per block
+    static constexpr int B_TASKS = (BNW * 2 * SPLIT + G_THREADS - 1) / G_THREADS;
+    static constexpr int B_WORDS = (QUANT == Q4_DT ? 4 : (QUANT == Q8_DT ? 8 : 16)) / SPLIT;  // u32 per task
     uint4 a[A_CHUNKS];
-    uint4 b[B_TASKS][BWords<QUANT>::N];
+    uint32_t b[B_TASKS][B_WORDS];
     uint16_t sc[B_TASKS];
 };
 
@@ -47,46 +54,82 @@ struct GemmArgs {
     int64_t ldy;
 };
 
+// Buffer resources of one workgroup's tiles.
+struct TileRes {
+    __amdgpu_buffer_rsrc_t x, w0, w1, s0, s1;
+};
+
+constexpr int RSRC_FLAGS = 0x00020000;  // raw (untyped) 32-bit buffer
+
+__device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+    const int64_t n = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, int(n), RSRC_FLAGS);
+}
+
 template <int QUANT, int BM, int BN, bool GATED>
-__device__ inline void load_stage(Stage<QUANT, BM, (GATED ? 2 * BN : BN)>& st, const GemmArgs& g,
-                                  int64_t m0, int64_t n0, int64_t k0, int tid) {
+__device__ inline TileRes tile_res(const GemmArgs& g, int64_t m0, int64_t n0) {
+    const int64_t M = g.m, K = g.w0.cols, N = g.w0.rows, KB = K / 32;
+    const int64_t rows_m = M - m0 < BM ? M - m0 : BM;
+    const int64_t rows_n = N - n0 < BN ? N - n0 : BN;
+    TileRes r;
+    r.x = rsrc(g.x + m0 * g.ldx, rows_m * g.ldx * 2);
+    const int64_t wrow = QUANT == Q4_DT ? KB * 16 : (QUANT == Q8_DT ? K : 2 * K);  // bytes per weight row
+    r.w0 = rsrc(static_cast<const uint8_t*>(g.w0.data) + n0 * wrow, rows_n * wrow);
+    r.w1 = rsrc(static_cast<const uint8_t*>(g.w1.data) + n0 * wrow, rows_n * wrow);
+    r.s0 = rsrc(g.w0.scales ? g.w0.scales + n0 * KB : nullptr, g.w0.scales ? rows_n * KB * 2 : 0);
+    r.s1 = rsrc(g.w1.scales ? g.w1.scales + n0 * KB : nullptr, g.w1.scales ? rows_n * KB * 2 : 0);
+    return r;
+}
+
+__device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+constexpr int OOB = 0x7ffffff0;  // an offset past every resource
+
+template <int QUANT, int BM, int BN, bool GATED>
+__device__ inline void load_stage(Stage<QUANT, BM, (GATED ? 2 * BN : BN)>& st, const TileRes& tr,
+                                  const GemmArgs& g, int64_t k0, int tid) {
     constexpr int BNW = GATED ? 2 * BN : BN;
     using S = Stage<QUANT, BM, BNW>;
-    const int64_t M = g.m, K = g.w0.cols, N = g.w0.rows;
+    const int64_t K = g.w0.cols, KB = K / 32;
 #pragma unroll
     for (int c = 0; c < S::A_CHUNKS; ++c) {
         const int idx = tid + c * G_THREADS;
         const int r = idx / (G_BK / 8), cc = idx % (G_BK / 8);
-        const int64_t m = m0 + r, k = k0 + cc * 8;
-        st.a[c] = (m < M && k < K) ? *reinterpret_cast<const uint4*>(g.x + m * g.ldx + k) : make_uint4(0, 0, 0, 0);
+        const int64_t k = k0 + cc * 8;
+        st.a[c] = bload16(tr.x, k < K ? int((r * g.ldx + k) * 2) : OOB);
     }
-    const int64_t KB = K / 32;
 #pragma unroll
     for (int t = 0; t < S::B_TASKS; ++t) {
+        constexpr int SP = S::SPLIT, W = S::B_WORDS;
         const int idx = tid + t * G_THREADS;
-        const int nl = idx / 2, blk = idx % 2;
+        const int nl = idx / (2 * SP), blk = (idx / SP) % 2, part = idx % SP;
         const bool up = GATED && nl >= BN;
-        const DevWeight& w = up ? g.w1 : g.w0;
-        const int64_t n = n0 + (GATED ? nl % BN : nl);
+        const __amdgpu_buffer_rsrc_t wr = up ? tr.w1 : tr.w0;
+        const __amdgpu_buffer_rsrc_t sr = up ? tr.s1 : tr.s0;
+        const int64_t n = GATED ? nl % BN : nl;  // row within the tile
         const int64_t kb = k0 / 32 + blk;
-        const bool ok = idx < BNW * 2 && n < N && kb < KB;
+        const bool ok = idx < BNW * 2 * SP && kb < KB;
+        // Byte offset of this task's payload within the tile's weight rows.
+        const int64_t base = QUANT == Q4_DT ? (n * KB + kb) * 16 : (QUANT == Q8_DT ? n * K + kb * 32 : (n * K + kb * 32) * 2);
+        const int off = ok ? int(base + part * W * 4) : OOB;
+        if constexpr (W == 2) {
+            const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, off, 0, 0));
+            st.b[t][0] = u.x;
+            st.b[t][1] = u.y;
+        } else {
 #pragma unroll
-        for (int q = 0; q < BWords<QUANT>::N; ++q) st.b[t][q] = make_uint4(0, 0, 0, 0);
-        st.sc[t] = 0;
-        if (ok) {
-            if constexpr (QUANT == Q4_DT) {
-                st.b[t][0] = reinterpret_cast<const uint4*>(w.data)[n * KB + kb];
-            } else if constexpr (QUANT == Q8_DT) {
-                const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(w.data) + n * K + kb * 32);
-                st.b[t][0] = p[0];
-                st.b[t][1] = p[1];
-            } else {
-                const uint4* p = reinterpret_cast<const uint4*>(static_cast<const half_t*>(w.data) + n * K + kb * 32);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) st.b[t][q] = p[q];
+            for (int q = 0; q < W / 4; ++q) {
+                const uint4 u = bload16(wr, ok ? off + 16 * q : OOB);
+                st.b[t][4 * q] = u.x;
+                st.b[t][4 * q + 1] = u.y;
+                st.b[t][4 * q + 2] = u.z;
+                st.b[t][4 * q + 3] = u.w;
             }
-            if constexpr (QUANT != F16_DT) st.sc[t] = w.scales[n * KB + kb];
         }
+        if constexpr (QUANT != F16_DT)
+            st.sc[t] = uint16_t(__builtin_amdgcn_raw_buffer_load_b16(sr, ok ? int((n * KB + kb) * 2) : OOB, 0, 0));
     }
 }
 
@@ -101,36 +144,37 @@ __device__ inline void store_stage(const Stage<QUANT, BM, BNW>& st, half_t* As, 
     }
 #pragma unroll
     for (int t = 0; t < S::B_TASKS; ++t) {
+        constexpr int SP = S::SPLIT, W = S::B_WORDS;
         const int idx = tid + t * G_THREADS;
-        if (idx >= BNW * 2) break;
-        const int nl = idx / 2, blk = idx % 2;
-        half8* dst = reinterpret_cast<half8*>(Bs + nl * G_LDS + blk * 32);
+        if (idx >= BNW * 2 * SP) break;
+        const int nl = idx / (2 * SP), blk = (idx / SP) % 2, part = idx % SP;
+        half8* dst = reinterpret_cast<half8*>(Bs + nl * G_LDS + blk * 32 + part * (32 / SP));
         if constexpr (QUANT == Q4_DT) {
             const half_t d = __builtin_bit_cast(half_t, st.sc[t]);
             const half2v dd = {d, d};
-            const uint4 u = st.b[t][0];
-            dst[0] = dq4_word(u.x, dd);
-            dst[1] = dq4_word(u.y, dd);
-            dst[2] = dq4_word(u.z, dd);
-            dst[3] = dq4_word(u.w, dd);
+#pragma unroll
+            for (int q = 0; q < W; ++q) dst[q] = dq4_word(st.b[t][q], dd);
         } else if constexpr (QUANT == Q8_DT) {
             const half_t d = __builtin_bit_cast(half_t, st.sc[t]);
-            dst[0] = dq8_words(st.b[t][0].x, st.b[t][0].y, d);
-            dst[1] = dq8_words(st.b[t][0].z, st.b[t][0].w, d);
-            dst[2] = dq8_words(st.b[t][1].x, st.b[t][1].y, d);
-            dst[3] = dq8_words(st.b[t][1].z, st.b[t][1].w, d);
+#pragma unroll
+            for (int q = 0; q < W / 2; ++q) dst[q] = dq8_words(st.b[t][2 * q], st.b[t][2 * q + 1], d);
         } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) reinterpret_cast<uint4*>(dst)[q] = st.b[t][q];
+            for (int q = 0; q < W / 4; ++q)
+                reinterpret_cast<uint4*>(dst)[q] =
+                    make_uint4(st.b[t][4 * q], st.b[t][4 * q + 1], st.b[t][4 * q + 2], st.b[t][4 * q + 3]);
         }
     }
 }
 
-// matmul_gated.wgsl:126-134: tanh GELU with the argument clamped to +-15.
+// matmul_gated.wgsl:126-134: tanh GELU with the argument clamped to +-15,
+// through the identity 0.5 (1 + tanh z) = 1 / (1 + e^(-2z)) evaluated with
+// the hardware exp2 and reciprocal.
 __device__ inline float gelu_tanh(float x) {
     float z = 0.7978845608028654f * (x + 0.044715f * x * x * x);
     z = fminf(15.0f, fmaxf(-15.0f, z));
-    return 0.5f * x * (1.0f + tanhf(z));
+    const float e = __builtin_amdgcn_exp2f(z * -2.8853900817779268f);  // e^(-2z)
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 template <int QUANT, int BM, int BN, bool GATED>
@@ -147,7 +191,16 @@ __global__ __launch_bounds__(G_THREADS) void gemm_kernel(GemmArgs g) {
     const int tid = int(threadIdx.x);
     const int wave = tid / WAVE, lane = tid % WAVE;
     const int wm = wave / 2, wn = wave % 2;
-    const int64_t n0 = int64_t(blockIdx.x) * BN, m0 = int64_t(blockIdx.y) * BM;
+    // Workgroups are dispatched round-robin over the 8 XCDs (each with its
+    // own L2): workgroup b runs on XCD b % 8.  Give each XCD a contiguous run
+    // of tiles, row-tile major, so the activation rows it reads stay in its
+    // L2 while it sweeps the (small) weight matrix.
+    const int ntn = int((g.w0.rows + BN - 1) / BN);
+    const int ntiles = ntn * int((g.m + BM - 1) / BM);
+    const int per_xcd = int(gridDim.x) / 8;
+    const int tile = (int(blockIdx.x) % 8) * per_xcd + int(blockIdx.x) / 8;
+    if (tile >= ntiles) return;
+    const int64_t n0 = int64_t(tile % ntn) * BN, m0 = int64_t(tile / ntn) * BM;
     const int64_t K = g.w0.cols;
     const int nk = int((K + G_BK - 1) / G_BK);
 
@@ -157,15 +210,16 @@ __global__ __launch_bounds__(G_THREADS) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    const TileRes tr = tile_res<QUANT, BM, BN, GATED>(g, m0, n0);
     Stage<QUANT, BM, BNW> st;
-    load_stage<QUANT, BM, BN, GATED>(st, g, m0, n0, 0, tid);
+    load_stage<QUANT, BM, BN, GATED>(st, tr, g, 0, tid);
     store_stage<QUANT, BM, BNW>(st, a_tile(0), b_tile(0), tid);
     __syncthreads();
 
     const int lr = lane % 16, lk = (lane / 16) * 8;
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
-        if (kt + 1 < nk) load_stage<QUANT, BM, BN, GATED>(st, g, m0, n0, int64_t(kt + 1) * G_BK, tid);
+        if (kt + 1 < nk) load_stage<QUANT, BM, BN, GATED>(st, tr, g, int64_t(kt + 1) * G_BK, tid);
         const half_t* A = a_tile(cur);
         const half_t* B = b_tile(cur);
 #pragma unroll
@@ -183,27 +237,41 @@ __global__ __launch_bounds__(G_THREADS) void gemm_kernel(GemmArgs g) {
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < NJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) store_stage<QUANT, BM, BNW>(st, a_tile(cur ^ 1), b_tile(cur ^ 1), tid);
         __syncthreads();
     }
 
+    // Lane (lr, G) holds columns 4G..4G+3 of row lr of each 16 x 16 tile.
     const int64_t N = g.w0.rows;
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
+        const int64_t m = m0 + wm * WM + i * 16 + lr;
+        if (m >= g.m) continue;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
-            const int64_t n = n0 + wn * WN + j * 16 + lr;
+            const int64_t n = n0 + wn * WN + j * 16 + (lane / 16) * 4;
+            float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + wm * WM + i * 16 + (lane / 16) * 4 + r;
-                if (m >= g.m || n >= N) continue;
+            for (int r = 0; r < 4; ++r)
+                v[r] = GATED ? gelu_tanh(acc[i][j][r]) * acc[i][j + (GATED ? NI : 0)][r] : acc[i][j][r];
+            if (n + 3 < N) {
                 if constexpr (GATED) {
-                    const float v = gelu_tanh(acc[i][j][r]) * acc[i][j + NI][r];
-                    static_cast<half_t*>(g.y)[m * g.ldy + n] = half_t(v);
+                    *reinterpret_cast<half4*>(static_cast<half_t*>(g.y) + m * g.ldy + n) =
+                        half4{half_t(v[0]), half_t(v[1]), half_t(v[2]), half_t(v[3])};
                 } else {
-                    static_cast<float*>(g.y)[m * g.ldy + n] = acc[i][j][r];
+                    *reinterpret_cast<float4*>(static_cast<float*>(g.y) + m * g.ldy + n) =
+                        make_float4(v[0], v[1], v[2], v[3]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (n + r >= N) break;
+                    if constexpr (GATED)
+                        static_cast<half_t*>(g.y)[m * g.ldy + n + r] = half_t(v[r]);
+                    else
+                        static_cast<float*>(g.y)[m * g.ldy + n + r] = v[r];
                 }
             }
         }
@@ -213,7 +281,8 @@ __global__ __launch_bounds__(G_THREADS) void gemm_kernel(GemmArgs g) {
 template <int QUANT, int BM, int BN, bool GATED>
 static void run(hipStream_t s, const GemmArgs& g) {
     const int64_t N = g.w0.rows;
-    const dim3 grid(unsigned((N + BN - 1) / BN), unsigned((g.m + BM - 1) / BM));
+    const int64_t tiles = ((N + BN - 1) / BN) * ((g.m + BM - 1) / BM);
+    const dim3 grid(unsigned((tiles + 7) / 8 * 8));
     gemm_kernel<QUANT, BM, BN, GATED><<<grid, dim3(G_THREADS), 0, s>>>(g);
     OMG_HIP(hipGetLastError());
 }
@@ -241,6 +310,7 @@ static void check(const half_t* x, int64_t ldx, const DevWeight& w, int64_t ldy,
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w.data) % 16 != 0)
         fail(E_INVALID, "gemm: operands must be 16-byte aligned");
     if (ldy < w.rows) fail(E_INVALID, "gemm: Y row stride must be >= N");
+    if (ldy % 4 != 0) fail(E_INVALID, "gemm: Y row stride must be a multiple of 4");
     if (w.dtype != F16_DT && !w.scales) fail(E_INVALID, "gemm: quantized weight without scales");
 }
 

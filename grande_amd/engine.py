@@ -108,8 +108,9 @@ class EngineBuilder:
         self.config = config
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            L.lib().omg_builder_free(self._h)
+        lib = getattr(L, "_lib", None)
+        if lib is not None and getattr(self, "_h", None):
+            lib.omg_builder_free(self._h)
             self._h = None
 
     def push(self, t: QTensor) -> None:
@@ -154,8 +155,9 @@ class Engine:
         return cls(L.handle(L.lib().omg_open_dir(str(path).encode(), capacity, max_rows)))
 
     def close(self) -> None:
-        if getattr(self, "_h", None):
-            L.lib().omg_close(self._h)
+        lib = getattr(L, "_lib", None)
+        if lib is not None and getattr(self, "_h", None):
+            lib.omg_close(self._h)
             self._h = None
 
     __del__ = close
@@ -283,8 +285,9 @@ class DeviceWeight:
         self.rows, self.cols = rows, cols
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            L.lib().omg_weight_free(self._h)
+        lib = getattr(L, "_lib", None)
+        if lib is not None and getattr(self, "_h", None):
+            lib.omg_weight_free(self._h)
             self._h = None
 
     def gemm(self, x_ptr: int, ldx: int, m: int, y_ptr: int, ldy: int, stream: int | None = None) -> None:

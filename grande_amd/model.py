@@ -129,8 +129,9 @@ class Weights:
         return cls(h, (Path(path) / "config.json").read_text())
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            L.lib().omg_weights_free(self._h)
+        lib = getattr(L, "_lib", None)
+        if lib is not None and getattr(self, "_h", None):
+            lib.omg_weights_free(self._h)
             self._h = None
 
     def __len__(self) -> int:
