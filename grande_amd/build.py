@@ -26,6 +26,10 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", f"-I{INCL
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 SOURCES = ["gemm.hip", "attention.hip", "norm.hip", "model.cpp", "engine.cpp", "capi.cpp"]
+# Per-file device flags.  The GEMM keeps its MFMA accumulators in ordinary
+# VGPRs: with the AGPR form the register allocator shuffles them between
+# loop iterations (v_accvgpr moves in the main loop).
+EXTRA = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HEADERS = sorted(CSRC.glob("*.h")) + [INCLUDE / "omg_hip.h"]
 
 
@@ -34,7 +38,7 @@ def _compile(src: Path, force: bool) -> Path:
     newest_dep = max([src.stat().st_mtime] + [h.stat().st_mtime for h in HEADERS])
     if not force and obj.exists() and obj.stat().st_mtime >= newest_dep:
         return obj
-    flags = COMMON + (DEVICE if src.suffix == ".hip" else [f"--offload-arch={ARCH}"])
+    flags = COMMON + (DEVICE if src.suffix == ".hip" else [f"--offload-arch={ARCH}"]) + EXTRA.get(src.name, [])
     cmd = [HIPCC, *flags, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

@@ -378,24 +378,7 @@ omg_weight* omg_weight_upload(int dtype, int64_t rows, int64_t cols, const void*
         const size_t nbytes = size_t(omg::payload_bytes(omg::Dtype(dtype), n));
         omg::QTensor t = make_tensor(dtype, shape, 2, data, nbytes, scales, dtype == OMG_DTYPE_F16 ? 0 : size_t(n / 32 * 2));
         auto w = std::make_unique<omg_weight>();
-        w->t.w.dtype = dtype;
-        w->t.w.rows = rows;
-        w->t.w.cols = cols;
-        if (dtype == OMG_DTYPE_Q4) {
-            std::vector<uint8_t> rep(t.data.size());
-            omg::repack_q4(t.data.data(), rep.data(), n);
-            w->t.data = omg::DevBuf(rep.size());
-            OMG_HIP(hipMemcpy(w->t.data.p, rep.data(), rep.size(), hipMemcpyHostToDevice));
-        } else {
-            w->t.data = omg::DevBuf(t.data.size());
-            OMG_HIP(hipMemcpy(w->t.data.p, t.data.data(), t.data.size(), hipMemcpyHostToDevice));
-        }
-        if (dtype != OMG_DTYPE_F16) {
-            w->t.scales = omg::DevBuf(t.scales.size());
-            OMG_HIP(hipMemcpy(w->t.scales.p, t.scales.data(), t.scales.size(), hipMemcpyHostToDevice));
-        }
-        w->t.w.data = w->t.data.p;
-        w->t.w.scales = w->t.scales.as<uint16_t>();
+        w->t = omg::upload_weight(t);
         out = w.release();
     });
     return out;

@@ -3,6 +3,8 @@
 // (crates/omg-wgpu/src/engine.rs).
 #include "engine.h"
 
+#include <cstring>
+
 #include <sys/stat.h>
 
 #include <algorithm>
@@ -196,6 +198,33 @@ static DevBuf upload_bytes(const void* src, size_t n) {
     return b;
 }
 
+DevTensor upload_weight(const QTensor& t) {
+    if (t.shape.size() != 2 || t.shape[1] % 32 != 0) fail(E_INVALID, "weight: expected [rows, cols % 32 == 0]");
+    DevTensor d;
+    d.w.dtype = int(t.dtype);
+    d.w.rows = t.shape[0];
+    d.w.cols = t.shape[1];
+    const int64_t n = d.w.rows * d.w.cols, kb = d.w.cols / BLOCK;
+    if (t.dtype == Q4) {
+        std::vector<uint8_t> rep(t.data.size());
+        repack_q4(t.data.data(), rep.data(), n);
+        d.data = upload_bytes(rep.data(), rep.size());
+    } else {
+        d.data = upload_bytes(t.data.data(), t.data.size());
+    }
+    if (t.dtype != F16) {
+        // Scale rows padded to an even count of blocks (zeros in the pad).
+        d.w.sld = (kb + 1) / 2 * 2;
+        std::vector<uint8_t> sc(size_t(d.w.rows * d.w.sld) * 2, 0);
+        for (int64_t r = 0; r < d.w.rows; ++r)
+            std::memcpy(sc.data() + r * d.w.sld * 2, t.scales.data() + r * kb * 2, size_t(kb) * 2);
+        d.scales = upload_bytes(sc.data(), sc.size());
+    }
+    d.w.data = d.data.p;
+    d.w.scales = d.scales.as<uint16_t>();
+    return d;
+}
+
 // --------------------------------------------------------------- builder
 
 Builder::Builder(Config cfg) : cfg_(std::move(cfg)) {
@@ -220,21 +249,7 @@ void Builder::push(const std::string& name, const QTensor& t) {
         return;
     }
     if (t.shape[1] % 32 != 0) fail(E_INVALID, name + ": inner dimension is not a multiple of 32");
-    DevTensor d;
-    d.w.dtype = int(t.dtype);
-    d.w.rows = t.shape[0];
-    d.w.cols = t.shape[1];
-    if (t.dtype == Q4) {
-        std::vector<uint8_t> rep(t.data.size());
-        repack_q4(t.data.data(), rep.data(), n);
-        d.data = upload_bytes(rep.data(), rep.size());
-    } else {
-        d.data = upload_bytes(t.data.data(), t.data.size());
-    }
-    if (t.dtype != F16) d.scales = upload_bytes(t.scales.data(), t.scales.size());
-    d.w.data = d.data.p;
-    d.w.scales = d.scales.as<uint16_t>();
-    linears_[name] = std::move(d);
+    linears_[name] = upload_weight(t);
     norms_.erase(name);
 }
 

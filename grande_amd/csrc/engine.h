@@ -99,6 +99,9 @@ struct DevTensor {
     DevWeight w;
     DevBuf data, scales;
 };
+// Upload a linear weight in the device layout (Q4 repacked, scale rows
+// padded to an even block count).
+DevTensor upload_weight(const QTensor& t);
 
 class Engine;
 

@@ -57,14 +57,20 @@ __device__ inline float q4_elem_f32(uint32_t w, int p, float d) {
 }
 
 // Eight Q8 codes (two little-endian words) times the block scale, f16.
-__device__ inline half8 dq8_words(uint32_t w0, uint32_t w1, half_t d) {
-    half8 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        r[i] = half_t(float(int8_t(w0 >> (8 * i)))) * d;
-        r[4 + i] = half_t(float(int8_t(w1 >> (8 * i)))) * d;
-    }
-    return r;
+// Each signed byte b is flipped to b + 128, placed under the exponent byte
+// of 1024.0 (0x64) with a byte permute, and 1152 is subtracted: b exactly,
+// so the only rounding is the product with d, as in shaders/weight.wgsl.
+__device__ inline half2v q8_pair(uint32_t flipped, uint32_t sel) {
+    return as_half2(__builtin_amdgcn_perm(0x64646464u, flipped, sel));
+}
+__device__ inline half8 dq8_words(uint32_t w0, uint32_t w1, half2v dd) {
+    const half2v off = {half_t(1152.0f), half_t(1152.0f)};
+    const uint32_t a = w0 ^ 0x80808080u, b = w1 ^ 0x80808080u;
+    const half2v h0 = (q8_pair(a, 0x04010400u) - off) * dd;
+    const half2v h1 = (q8_pair(a, 0x04030402u) - off) * dd;
+    const half2v h2 = (q8_pair(b, 0x04010400u) - off) * dd;
+    const half2v h3 = (q8_pair(b, 0x04030402u) - off) * dd;
+    return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
 }
 
 }  // namespace omg

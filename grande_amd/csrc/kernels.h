@@ -17,7 +17,7 @@ constexpr int F16_DT = 0, Q8_DT = 1, Q4_DT = 2;
 
 // A linear weight on the device, row-major [rows, cols] = [out, in].
 //   F16: data = half_t[rows*cols].
-//   Q8:  data = int8[rows*cols] (natural order), scales = f16[rows*cols/32].
+//   Q8:  data = int8[rows*cols] (natural order), scales as below.
 //   Q4:  data = 16 B per 32-element block, [rows][cols/32][16 B]; inside a
 //        block, 32-bit word w holds elements 8w..8w+7 with element 8w+p at
 //        bit 4*(p/2) (p even) or 16+4*(p/2) (p odd), so two shifts and a
@@ -26,7 +26,8 @@ struct DevWeight {
     int dtype = 0;
     int64_t rows = 0, cols = 0;
     const void* data = nullptr;
-    const uint16_t* scales = nullptr;
+    const uint16_t* scales = nullptr;  // [rows][sld] f16, block b of row r at r * sld + b
+    int64_t sld = 0;                   // cols / 32 rounded up to even (the pad holds zeros)
 };
 
 // Repack one Q4_0 tensor (model.rs layout: byte j = element j | element

@@ -13,9 +13,10 @@ namespace omg {
 
 // ---------------------------------------------------------------- decode
 
-// Four consecutive elements e..e+3 (e % 4 == 0) of a device weight, f32.
+// Elements (row, c..c+3) (c % 4 == 0) of a device weight, f32.
 template <int DT>
-__device__ inline void load4_f32(const DevWeight& w, int64_t e, float v[4]) {
+__device__ inline void load4_f32(const DevWeight& w, int64_t row, int64_t c, float v[4]) {
+    const int64_t e = row * w.cols + c;
     if constexpr (DT == F16_DT) {
         const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const half_t*>(w.data) + e);
         const half2v a = as_half2(u.x), b = as_half2(u.y);
@@ -24,15 +25,14 @@ __device__ inline void load4_f32(const DevWeight& w, int64_t e, float v[4]) {
         v[2] = float(b.x);
         v[3] = float(b.y);
     } else if constexpr (DT == Q8_DT) {
-        const float d = half_bits_to_f32(w.scales[e / 32]);
+        const float d = half_bits_to_f32(w.scales[row * w.sld + c / 32]);
         const uint32_t u = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(w.data) + e);
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = float(int8_t(u >> (8 * i))) * d;
     } else {
-        const int64_t b = e / 32;
-        const int j = int(e % 32);
-        const float d = half_bits_to_f32(w.scales[b]);
-        const uint32_t word = static_cast<const uint32_t*>(w.data)[b * 4 + j / 8];
+        const int j = int(c % 32);
+        const float d = half_bits_to_f32(w.scales[row * w.sld + c / 32]);
+        const uint32_t word = static_cast<const uint32_t*>(w.data)[(e / 32) * 4 + j / 8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = q4_elem_f32(word, (j % 8) + i, d);
     }
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(DevWeight E, const uint
     float ss = 0.0f;
     for (int64_t q = lane; q < d / 4; q += WAVE) {
         float v[4];
-        load4_f32<DT>(E, id * d + 4 * q, v);
+        load4_f32<DT>(E, id, 4 * q, v);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             v[i] = v[i] * escale;
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256) void logits_kernel(DevWeight E, const float* _
     for (int r = 0; r < LG_R; ++r) acc[r] = 0.0f;
     for (int64_t q = lane; q < K / 4; q += WAVE) {
         float wv[4];
-        load4_f32<DT>(E, col * K + 4 * q, wv);
+        load4_f32<DT>(E, col, 4 * q, wv);
 #pragma unroll
         for (int r = 0; r < LG_R; ++r) {
             if (r < nr) {
