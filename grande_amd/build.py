@@ -26,10 +26,10 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", f"-I{INCL
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 SOURCES = ["gemm.hip", "attention.hip", "norm.hip", "model.cpp", "engine.cpp", "capi.cpp"]
-# Per-file device flags.  The GEMM keeps its MFMA accumulators in ordinary
-# VGPRs: with the AGPR form the register allocator shuffles them between
-# loop iterations (v_accvgpr moves in the main loop).
-EXTRA = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-file device flags.  The GEMM and attention kernels keep their MFMA
+# accumulators in ordinary VGPRs: with the AGPR form the register allocator
+# shuffles them between loop iterations (v_accvgpr moves in the main loop).
+EXTRA = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HEADERS = sorted(CSRC.glob("*.h")) + [INCLUDE / "omg_hip.h"]
 
 

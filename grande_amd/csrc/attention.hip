@@ -15,10 +15,10 @@
 // is the same whichever tokens share its tile: rows over a resident prefix
 // are bit-equal to a full pass.
 //
-// Per item: K and V tiles are double-buffered in LDS; the next tile's
-// global loads are issued into registers before the current tile's MFMAs
-// and stored after them, one barrier per tile.  A wave that sees no key of
-// a tile skips it; a wave that sees every key of it skips the masking.
+// Per item: K and V^T tiles are double-buffered in LDS, loaded by LDS DMA
+// one tile ahead; one barrier per tile.  A wave that sees no key of a tile
+// skips it; a wave that sees every key of it skips the masking.  Masks are
+// per-token 64-bit ballots over the tile's keys.
 //
 // Both products run on v_mfma_f32_16x16x32_f16 arranged so that no operand
 // needs a register transpose:
@@ -26,8 +26,10 @@
 //                 registers): lane l holds S[q = l%16][keys 16j + 4(l/16) + r];
 //   O^T[c][q]  += V^T[c][key] . P^T[key][q]  (A = V^T from the cache's
 //                 transposed tiles, B = the lane's own probabilities).
-// A lane owns one query row for the softmax statistics and the output, so
-// the running max and sum need only the 4 lanes of that row.
+// The cache stores V^T tile columns in the order of vt_col, so the eight
+// keys a lane holds probabilities for are one contiguous 16-byte read.  A
+// lane owns one query row for the softmax statistics and the output, so the
+// running max and sum need only the 4 lanes of that row.
 #include <climits>
 #include <string>
 
@@ -48,18 +50,15 @@ __device__ inline bool visible(int qp, int qs, int kp, int ks, int window) {
 
 // LDS of one work item.  K and V^T tiles are stored without padding; the
 // 16-byte chunks of each row are XOR-swizzled so that the MFMA operand reads
-// (16 lanes on 16 consecutive rows at one logical chunk) hit 16 distinct
-// bank groups:
+// (16 lanes on 16 consecutive rows at one logical chunk) hit distinct banks:
 //   K   [64 keys][HD]:  physical chunk = logical ^ (row & 15)  (32-chunk rows)
 //   V^T [HD][64 keys]:  physical chunk = logical ^ ((row >> 1) & 7)  (8-chunk rows)
+// The key metadata (cache rows' int4 meta) of each tile comes along.
 template <int HD>
 struct AttnSmem {
     half_t k[2][A_KT * HD];
     half_t v[2][HD * A_KT];
-    int kpos[2][A_KT];
-    int kseq[2][A_KT];
-    int qpos[A_ROWS];
-    int qseq[A_ROWS];
+    int4 kmeta[2][A_KT];
 };
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
@@ -68,10 +67,12 @@ typedef __attribute__((address_space(1))) void* global_void_ptr;
 // Issue this wave's share of one K/V tile as direct global -> LDS loads
 // (global_load_lds_dwordx4: lane i of an instruction writes 16 bytes at LDS
 // base + 16 i).  Every lane picks the global chunk that belongs at its LDS
-// slot, which is how the swizzle is applied.
+// slot, which is how the swizzle is applied.  Wave 0 also brings the keys'
+// metadata (rows past the cache's valid range read as never visible).
 template <int HD>
 __device__ __attribute__((always_inline)) inline void dma_tile(AttnSmem<HD>& sm, int buf, const half_t* kt,
-                                                               const half_t* vt, int wave, int lane) {
+                                                               const half_t* vt, const int4* meta, int wave,
+                                                               int lane) {
     constexpr int KROW = HD / 8;                     // 16 B chunks per K row
     constexpr int KINS = A_KT * HD / 8 / WAVE / 4;   // instructions per wave for K
     constexpr int VINS = HD * A_KT / 8 / WAVE / 4;
@@ -93,45 +94,44 @@ __device__ __attribute__((always_inline)) inline void dma_tile(AttnSmem<HD>& sm,
         __builtin_amdgcn_global_load_lds((global_void_ptr)(vt + row * A_KT + lc * 8),
                                          (lds_void_ptr)(sm.v[buf] + blk * WAVE * 8), 16, 0, 0);
     }
+    if (wave == 0)
+        __builtin_amdgcn_global_load_lds((global_void_ptr)(meta + lane), (lds_void_ptr)(sm.kmeta[buf]), 16, 0, 0);
 }
 
-template <int HD>
+// One work item per workgroup: 64 query rows (TPW tokens x HPG heads per
+// wave, four waves) against key tiles [tb, te) of the KV head blockIdx.y.
+template <int HD, int HPG>
 __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const int4* __restrict__ items) {
     using SM = AttnSmem<HD>;
     constexpr int DS = HD / 32;  // MFMA steps over the head dim
     constexpr int CT = HD / 16;  // 16-wide output column tiles
+    constexpr int TPW = 16 / HPG, TPB = 4 * TPW;
     constexpr float LOG2E = 1.4426950408889634f;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     SM& sm = *reinterpret_cast<SM*>(smem_raw);
 
     const int4 item = items[blockIdx.x];
     const int qtile = item.x, tb = item.y, te = item.z, slot = item.w;
-    const int tid = int(threadIdx.x), wave = tid / WAVE, lane = tid % WAVE;
-    const int H = a.heads, hpg = a.heads / a.kv_heads, tpw = 16 / hpg, tpb = 4 * tpw;
+    const int tid = int(threadIdx.x), lane = tid % WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int H = a.heads;
     const int g = int(blockIdx.y);
-    const int64_t tok0 = int64_t(qtile) * tpb;
+    const int64_t tok0 = int64_t(qtile) * TPB + wave * TPW;
     const int lr = lane % 16, G = lane / 16;
-    const int64_t tq = tok0 + wave * tpw + lr / hpg;
-    const int head = g * hpg + lr % hpg;
+    const int u_lane = lr / HPG;  // the lane's token within the wave
+    const int64_t tq = tok0 + u_lane;
+    const int head = g * HPG + lr % HPG;
     const bool valid = tq < a.t;
-    const int64_t kend = a.base + a.t;  // cache rows holding keys
+    const int4* meta = reinterpret_cast<const int4*>(a.meta);
 
-    if (tid < tpb) {
-        const int64_t tk = tok0 + tid;
-        if (tk < a.t) {
-            const int4 m = reinterpret_cast<const int4*>(a.meta)[a.base + tk];
-            sm.qpos[tid] = m.x;
-            sm.qseq[tid] = m.y;
-        } else {
-            sm.qpos[tid] = -1;  // sees nothing: every key position is >= 0
-            sm.qseq[tid] = -2;
-        }
-    }
-    int qp = -1, qsq = -2;
-    if (valid) {
-        const int4 m = reinterpret_cast<const int4*>(a.meta)[a.base + tq];
-        qp = m.x;
-        qsq = m.y;
+    // Positions and sequence ids of the wave's tokens, wave-uniform.
+    int qpos[TPW], qseq[TPW];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+        int4 m = make_int4(-1, -2, 0, 0);  // past the pass: sees nothing (positions are >= 0)
+        if (tok0 + u < a.t) m = meta[a.base + tok0 + u];
+        qpos[u] = __builtin_amdgcn_readfirstlane(m.x);
+        qseq[u] = __builtin_amdgcn_readfirstlane(m.y);
     }
 
     half8 qf[DS];
@@ -145,123 +145,111 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 
     const half_t* kbase = a.kc + int64_t(g) * a.cap_pad * HD;
     const half_t* vbase = a.vt + int64_t(g) * (a.cap_pad / 64) * HD * 64;
-    // Key metadata of the next tile travels in registers (threads < 64).
-    int2 km = make_int2(INT_MAX, -3);
-    auto key_meta = [&](int tile) {
-        const int64_t row = int64_t(tile) * A_KT + tid;
-        km = make_int2(INT_MAX, -3);
-        if (tid < A_KT && row < kend) {
-            const int4 m = reinterpret_cast<const int4*>(a.meta)[row];
-            km = make_int2(m.x, m.y);
-        }
+    auto issue = [&](int tile, int buf) {
+        dma_tile<HD>(sm, buf, kbase + int64_t(tile) * A_KT * HD, vbase + int64_t(tile) * HD * A_KT,
+                     meta + int64_t(tile) * A_KT, wave, lane);
     };
-    if (tb < te) {
-        dma_tile<HD>(sm, 0, kbase + int64_t(tb) * A_KT * HD, vbase + int64_t(tb) * HD * A_KT, wave, lane);
-        key_meta(tb);
-    }
+    if (tb < te) issue(tb, 0);
     for (int tile = tb; tile < te; ++tile) {
         const int cur = (tile - tb) & 1;
         // This wave's loads of `tile` are the only ones outstanding.
         __builtin_amdgcn_s_waitcnt(0);
-        if (tid < A_KT) {
-            sm.kpos[cur][tid] = km.x;
-            sm.kseq[cur][tid] = km.y;
-        }
         // Every wave's part of `tile` has landed, and every wave is done
         // with the other buffer (tile - 1), which the next loads overwrite.
         __syncthreads();
-        if (tile + 1 < te) {
-            dma_tile<HD>(sm, cur ^ 1, kbase + int64_t(tile + 1) * A_KT * HD, vbase + int64_t(tile + 1) * HD * A_KT,
-                         wave, lane);
-            key_meta(tile + 1);
+        if (tile + 1 < te) issue(tile + 1, cur ^ 1);
+
+        // Which keys of the tile each of the wave's tokens sees: lane = key.
+        // Rows at or past the pass's end are never visible (their stale
+        // metadata may look valid).
+        const int4 km = sm.kmeta[cur][lane];
+        const bool key_ok = int64_t(tile) * A_KT + lane < a.base + a.t;
+        uint64_t vis[TPW];
+        uint64_t any = 0, all = ~0ull;
+#pragma unroll
+        for (int u = 0; u < TPW; ++u) {
+            vis[u] = __ballot(key_ok && visible(qpos[u], qseq[u], km.x, km.y, a.window));
+            any |= vis[u];
+            all &= vis[u];
         }
-        // Which of this tile's keys the wave's queries see.
-        bool any = false, all = true;
-        {
-            const int kp = sm.kpos[cur][lane], ks = sm.kseq[cur][lane];
-            for (int u = 0; u < tpw; ++u) {
-                const bool v = visible(sm.qpos[wave * tpw + u], sm.qseq[wave * tpw + u], kp, ks, a.window);
-                any |= v;
-                all &= v;
+        if (any == 0ull) continue;
+        const bool full = all == ~0ull;
+
+        const half_t* K = sm.k[cur];
+        floatx4 sacc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sacc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < DS; ++s) {
+                const int pc = (s * 4 + G) ^ lr;  // row & 15 == lr
+                const half8 kf = *reinterpret_cast<const half8*>(K + (j * 16 + lr) * HD + pc * 8);
+                sacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sacc[j], 0, 0, 0);
             }
         }
-        if (__ballot(any) != 0ull) {
-            const bool full = __ballot(!all) == 0ull;
-            const half_t* K = sm.k[cur];
-            floatx4 sacc[4];
+        float mt = -INFINITY;
+        if (full) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sacc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int s = 0; s < DS; ++s) {
-                    const int pc = (s * 4 + G) ^ lr;  // row & 15 == lr
-                    const half8 kf = *reinterpret_cast<const half8*>(K + (j * 16 + lr) * HD + pc * 8);
-                    sacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sacc[j], 0, 0, 0);
+                for (int r = 0; r < 4; ++r) {
+                    sacc[j][r] *= LOG2E;
+                    mt = fmaxf(mt, sacc[j][r]);
                 }
-            }
-            float mt = -INFINITY;
-            if (full) {
+        } else {
+            // The lane's 16 keys are bits 16j + 4G + r of its token's mask.
+            uint64_t mk = vis[0];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+            for (int u = 1; u < TPW; ++u) mk = u_lane == u ? vis[u] : mk;
+            const uint32_t lo = uint32_t(mk), hi = uint32_t(mk >> 32);
+            const uint32_t bits = ((lo >> (4 * G)) & 0xfu) | (((lo >> (16 + 4 * G)) & 0xfu) << 4) |
+                                  (((hi >> (4 * G)) & 0xfu) << 8) | (((hi >> (16 + 4 * G)) & 0xfu) << 12);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        sacc[j][r] *= LOG2E;
-                        mt = fmaxf(mt, sacc[j][r]);
-                    }
-            } else {
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int4 kp4 = *reinterpret_cast<const int4*>(sm.kpos[cur] + j * 16 + G * 4);
-                    const int4 ks4 = *reinterpret_cast<const int4*>(sm.kseq[cur] + j * 16 + G * 4);
-                    const int kpv[4] = {kp4.x, kp4.y, kp4.z, kp4.w};
-                    const int ksv[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float sv =
-                            visible(qp, qsq, kpv[r], ksv[r], a.window) ? sacc[j][r] * LOG2E : -INFINITY;
-                        sacc[j][r] = sv;
-                        mt = fmaxf(mt, sv);
-                    }
+                for (int r = 0; r < 4; ++r) {
+                    const float sv = (bits >> (4 * j + r)) & 1u ? sacc[j][r] * LOG2E : -INFINITY;
+                    sacc[j][r] = sv;
+                    mt = fmaxf(mt, sv);
                 }
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+        const float m_new = fmaxf(m_run, mt);
+        // A row that has seen nothing yet keeps m = -inf; exponents are
+        // taken against 0 then, which gives exactly 0 for every -inf score.
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        half8 pb[2];
+        float psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            half2v pr[2];
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+                pr[r / 2] = half2v{half_t(__builtin_amdgcn_exp2f(sacc[j][r] - m_use)),
+                                   half_t(__builtin_amdgcn_exp2f(sacc[j][r + 1] - m_use))};
+                psum = __builtin_amdgcn_fdot2(pr[r / 2], half2v{half_t(1.0f), half_t(1.0f)}, psum, false);
             }
-            mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
-            mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-            const float m_new = fmaxf(m_run, mt);
-            float alpha = 1.0f;
-            half8 pb[2];
-            float psum = 0.0f;
-            if (m_new == -INFINITY) {
-                pb[0] = half8{};
-                pb[1] = half8{};
-            } else {
-                alpha = exp2f(m_run - m_new);
+            pb[j / 2][(j % 2) * 4 + 0] = pr[0].x;
+            pb[j / 2][(j % 2) * 4 + 1] = pr[0].y;
+            pb[j / 2][(j % 2) * 4 + 2] = pr[1].x;
+            pb[j / 2][(j % 2) * 4 + 3] = pr[1].y;
+        }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__ballot(alpha != 1.0f) != 0ull) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+            for (int c = 0; c < CT; ++c) o[c] *= alpha;
+        }
+        const half_t* V = sm.v[cur];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const half_t p = half_t(exp2f(sacc[j][r] - m_new));
-                        psum += float(p);
-                        pb[j / 2][(j % 2) * 4 + r] = p;
-                    }
-            }
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
-            if (__ballot(alpha != 1.0f) != 0ull) {
+        for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
-                for (int c = 0; c < CT; ++c) o[c] *= alpha;
-            }
-            const half_t* V = sm.v[cur];
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int c = 0; c < CT; ++c) {
-                    const int row = c * 16 + lr, sw = (row >> 1) & 7;
-                    const half_t* vr = V + row * A_KT + (G & 1) * 4;
-                    const half4 lo = *reinterpret_cast<const half4*>(vr + (((tt * 4 + (G >> 1)) ^ sw) * 8));
-                    const half4 hi = *reinterpret_cast<const half4*>(vr + (((tt * 4 + 2 + (G >> 1)) ^ sw) * 8));
-                    const half8 vf = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-                    o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[tt], o[c], 0, 0, 0);
-                }
+            for (int c = 0; c < CT; ++c) {
+                const int row = c * 16 + lr;
+                const half8 vf = *reinterpret_cast<const half8*>(V + row * A_KT + (((tt * 4 + G) ^ ((row >> 1) & 7)) * 8));
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[tt], o[c], 0, 0, 0);
             }
         }
     }
@@ -317,7 +305,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
         const int64_t base = int64_t(slot0 + c) * A_ROWS + row;
         const float m = a.part_ml[base * 2];
         if (m == -INFINITY) continue;
-        const float w = exp2f(m - M);
+        const float w = __builtin_amdgcn_exp2f(m - M);
         L += a.part_ml[base * 2 + 1] * w;
         const float* op = a.part_o + base * HD + quarter * W;
 #pragma unroll
@@ -367,6 +355,18 @@ void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int
     w.slots = slot;
 }
 
+template <int HD, int HPG>
+static void run_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, size_t smem) {
+    static bool attr_set = false;  // once per instantiation (per process)
+    if (!attr_set) {
+        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<HD, HPG>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));
+        attr_set = true;
+    }
+    attention_kernel<HD, HPG><<<dim3(unsigned(nitems), unsigned(a.kv_heads)), dim3(A_THREADS), smem, s>>>(a, items);
+    OMG_HIP(hipGetLastError());
+}
+
 void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, const int4* merges,
                       int64_t nmerges) {
     if (a.t <= 0 || nitems <= 0) return;
@@ -377,14 +377,13 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
     if (a.cap_pad % A_KT || a.base + a.t > a.cap_pad) fail(E_INVALID, "attention: cache rows out of range");
     if (a.window < 0) fail(E_INVALID, "attention: negative window");
     const size_t smem = sizeof(AttnSmem<256>);
-    static bool attr_set = false;
-    if (!attr_set) {
-        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<256>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));
-        attr_set = true;
+    switch (hpg) {
+        case 1: run_attention<256, 1>(s, a, items, nitems, smem); break;
+        case 2: run_attention<256, 2>(s, a, items, nitems, smem); break;
+        case 4: run_attention<256, 4>(s, a, items, nitems, smem); break;
+        case 8: run_attention<256, 8>(s, a, items, nitems, smem); break;
+        default: run_attention<256, 16>(s, a, items, nitems, smem); break;
     }
-    attention_kernel<256><<<dim3(unsigned(nitems), unsigned(a.kv_heads)), dim3(A_THREADS), smem, s>>>(a, items);
-    OMG_HIP(hipGetLastError());
     if (nmerges > 0) {
         attention_merge_kernel<256><<<dim3(unsigned(nmerges), unsigned(a.kv_heads)), dim3(256), 0, s>>>(a, merges);
         OMG_HIP(hipGetLastError());

@@ -57,7 +57,7 @@ struct QkArgs {
     int64_t t, base, cap_pad;
     half_t* q16;  // [t][heads][hd]
     half_t* kc;   // [kv_heads][cap_pad][hd]
-    half_t* vt;   // [kv_heads][cap_pad/64][hd][64]
+    half_t* vt;   // [kv_heads][cap_pad/64][hd][64], key columns ordered by vt_col
 };
 void launch_qk_prep(hipStream_t s, const QkArgs& a);
 // rows[i] = rmsnorm(x[wanted[i]]) * w, f32.
@@ -79,6 +79,15 @@ void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w
 // act[M][F] (f16) = gelu_tanh(X . Wg^T) * (X . Wu^T).
 void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,
                        const DevWeight& wu, half_t* act, int64_t ldact, int64_t m);
+
+// Column of cache row `row` inside its 64-row V^T tile.  Within each half
+// of 32 keys, key k sits at 8 * ((k % 16) / 4) + 4 * (k / 16) + k % 4: the
+// eight keys one MFMA lane holds probabilities for (4g..4g+3 and
+// 16+4g..16+4g+3) are then adjacent, so a V^T fragment is one 16-byte read.
+__host__ __device__ inline int64_t vt_col(int64_t row) {
+    const int64_t k = row % 64, h = k / 32, kk = k % 32;
+    return 32 * h + 8 * ((kk % 16) / 4) + 4 * (kk / 16) + kk % 4;
+}
 
 // ---- block-causal attention (attention.hip) ----
 struct AttnArgs {

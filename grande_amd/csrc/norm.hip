@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int slots) {
     ss = wave_sum(ss);
     if (kind == 2) {
         const float inv = a.v_norm ? 1.0f / sqrtf(ss / float(HD) + a.eps) : 1.0f;
-        half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + row / 64) * HD) * 64 + row % 64;
+        half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + row / 64) * HD) * 64 + vt_col(row);
 #pragma unroll
         for (int i = 0; i < EPL; ++i) dst[int64_t(lane * EPL + i) * 64] = half_t(v[i] * inv);
         return;
@@ -329,7 +329,7 @@ __global__ void kv_gather_kernel(const half_t* __restrict__ kc, const half_t* __
     if (c < int64_t(kvh) * hd)
         out[i] = kc[(g * cap_pad + row) * hd + e];
     else
-        out[i] = vt[((g * (cap_pad / 64) + row / 64) * hd + e) * 64 + row % 64];
+        out[i] = vt[((g * (cap_pad / 64) + row / 64) * hd + e) * 64 + vt_col(row)];
 }
 
 __global__ void kv_scatter_kernel(half_t* __restrict__ kc, half_t* __restrict__ vt, int64_t cap_pad,
@@ -343,7 +343,7 @@ __global__ void kv_scatter_kernel(half_t* __restrict__ kc, half_t* __restrict__ 
     if (c < int64_t(kvh) * hd)
         kc[(g * cap_pad + row) * hd + e] = in[i];
     else
-        vt[((g * (cap_pad / 64) + row / 64) * hd + e) * 64 + row % 64] = in[i];
+        vt[((g * (cap_pad / 64) + row / 64) * hd + e) * 64 + vt_col(row)] = in[i];
 }
 
 void launch_kv_gather(hipStream_t s, const half_t* kc, const half_t* vt, int64_t cap_pad, int kv_heads,
