@@ -51,6 +51,20 @@ def visible_pairs(prefix: int, nb: int, bt: int, window: int, layers: int, patte
     return total
 
 
+def profiled_traffic(config: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/<config>_<kernel>_traffic.md, a line "traffic_bytes_per_launch:
+    N"), or None where there is none."""
+    path = ROOT / "profiles" / f"{config}_{kernel}_traffic.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -58,11 +72,24 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 256 MiB device to device three times (calibrates the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU (--gpus {args.gpus} requested); a state's branches would "
               "shard across GPUs by broadcasting the prefix K/V, which is not built.", file=sys.stderr)
         return 2
+
+    if args.copy_probe:
+        import torch
+
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4, "copies": 3}))
+        return 0
 
     import grande_amd as g
     from grande_amd import BranchTokens, Group, Want
@@ -168,7 +195,8 @@ def main() -> int:
         "warm_vs_cold_max_abs_logit": warm_equal_cold,
         "pass_tflops": round(total_flop / cold_s / 1e12, 2),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": dom_tf, "peak": PEAK_F16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_F16_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_F16_TFLOPS, 4),
+                     "traffic": profiled_traffic(args.config, dom)},
         "kernels": kernels,
         "load_s": round(load_s, 2),
     }

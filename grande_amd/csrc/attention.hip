@@ -367,8 +367,7 @@ static void run_attention(hipStream_t s, const AttnArgs& a, const int4* items, i
     OMG_HIP(hipGetLastError());
 }
 
-void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, const int4* merges,
-                      int64_t nmerges) {
+void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems) {
     if (a.t <= 0 || nitems <= 0) return;
     if (a.hd != 256) fail(E_INVALID, "attention: head_dim must be 256");
     if (a.kv_heads <= 0 || a.heads % a.kv_heads) fail(E_INVALID, "attention: heads / kv_heads");
@@ -384,10 +383,13 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
         case 8: run_attention<256, 8>(s, a, items, nitems, smem); break;
         default: run_attention<256, 16>(s, a, items, nitems, smem); break;
     }
-    if (nmerges > 0) {
-        attention_merge_kernel<256><<<dim3(unsigned(nmerges), unsigned(a.kv_heads)), dim3(256), 0, s>>>(a, merges);
-        OMG_HIP(hipGetLastError());
-    }
+}
+
+void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges) {
+    if (a.t <= 0 || nmerges <= 0) return;
+    if (a.hd != 256) fail(E_INVALID, "attention_merge: head_dim must be 256");
+    attention_merge_kernel<256><<<dim3(unsigned(nmerges), unsigned(a.kv_heads)), dim3(256), 0, s>>>(a, merges);
+    OMG_HIP(hipGetLastError());
 }
 
 }  // namespace omg

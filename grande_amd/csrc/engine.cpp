@@ -365,10 +365,8 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
 // ---------------------------------------------------------------- engine
 
 Engine::~Engine() {
-    for (Timed& t : pending_) {
-        (void)hipEventDestroy(t.a);
-        (void)hipEventDestroy(t.b);
-    }
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (Timed& t : pending_) (void)hipEventDestroy(t.e);
     for (hipEvent_t ev : event_pool_) (void)hipEventDestroy(ev);
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (h_in_) (void)hipHostFree(h_in_);
@@ -376,6 +374,9 @@ Engine::~Engine() {
     if (stream_) (void)hipStreamDestroy(stream_);
 }
 
+// Measurement mode: one event after each launch; a launch's time is the
+// interval since the previous event of the same sequence, so back-to-back
+// launches pay for one event each rather than two.
 template <class F>
 void Engine::step(const char* name, F&& f) {
     if (!profile_) {
@@ -385,30 +386,35 @@ void Engine::step(const char* name, F&& f) {
     auto ev = [&]() {
         if (event_pool_.empty()) {
             hipEvent_t e;
-            OMG_HIP(hipEventCreate(&e));
+            // No system-scope release at the timestamp: it would write back L2
+            // between the launches being timed.
+            OMG_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
             return e;
         }
         hipEvent_t e = event_pool_.back();
         event_pool_.pop_back();
         return e;
     };
-    Timed t{name, ev(), ev()};
-    OMG_HIP(hipEventRecord(t.a, stream_));
+    if (pending_.empty()) {
+        const hipEvent_t start = ev();
+        OMG_HIP(hipEventRecord(start, stream_));
+        pending_.push_back(Timed{nullptr, start});
+    }
     f();
-    OMG_HIP(hipEventRecord(t.b, stream_));
-    pending_.push_back(t);
+    const hipEvent_t end = ev();
+    OMG_HIP(hipEventRecord(end, stream_));
+    pending_.push_back(Timed{name, end});
 }
 
 void Engine::collect_profile() {
-    for (Timed& t : pending_) {
+    for (size_t i = 1; i < pending_.size(); ++i) {
         float ms = 0.0f;
-        OMG_HIP(hipEventElapsedTime(&ms, t.a, t.b));
-        auto& tot = totals_[t.name];
+        OMG_HIP(hipEventElapsedTime(&ms, pending_[i - 1].e, pending_[i].e));
+        auto& tot = totals_[pending_[i].name];
         tot.first += 1;
         tot.second += double(ms);
-        event_pool_.push_back(t.a);
-        event_pool_.push_back(t.b);
     }
+    for (Timed& t : pending_) event_pool_.push_back(t.e);
     pending_.clear();
 }
 
@@ -547,26 +553,26 @@ void Engine::forward(int64_t t, int64_t base) {
             q.vt = vt_[size_t(src)].as<half_t>();
             launch_qk_prep(stream_, q);
         });
-        step("attention", [&] {
-            AttnArgs a{};
-            a.q16 = q16_.as<half_t>();
-            a.kc = kc_[size_t(src)].as<half_t>();
-            a.vt = vt_[size_t(src)].as<half_t>();
-            a.meta = meta_.as<int32_t>();
-            a.out = attn_.as<half_t>();
-            a.t = t;
-            a.base = base;
-            a.cap_pad = cap_pad_;
-            a.heads = int(c.heads);
-            a.kv_heads = int(c.kv_heads);
-            a.hd = int(hd);
-            a.window = c.sliding[size_t(l)] ? int(c.window) : 0;
-            a.part_o = part_o_.as<float>();
-            a.part_ml = part_ml_.as<float>();
-            const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
-            launch_attention(stream_, a, attn_items_[kind].as<int4>(), n_items_[kind], attn_merges_[kind].as<int4>(),
-                             n_merges_[kind]);
-        });
+        AttnArgs att{};
+        att.q16 = q16_.as<half_t>();
+        att.kc = kc_[size_t(src)].as<half_t>();
+        att.vt = vt_[size_t(src)].as<half_t>();
+        att.meta = meta_.as<int32_t>();
+        att.out = attn_.as<half_t>();
+        att.t = t;
+        att.base = base;
+        att.cap_pad = cap_pad_;
+        att.heads = int(c.heads);
+        att.kv_heads = int(c.kv_heads);
+        att.hd = int(hd);
+        att.window = c.sliding[size_t(l)] ? int(c.window) : 0;
+        att.part_o = part_o_.as<float>();
+        att.part_ml = part_ml_.as<float>();
+        const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
+        step("attention", [&] { launch_attention(stream_, att, attn_items_[kind].as<int4>(), n_items_[kind]); });
+        if (n_merges_[kind] > 0)
+            step("attention_merge",
+                 [&] { launch_attention_merge(stream_, att, attn_merges_[kind].as<int4>(), n_merges_[kind]); });
         step("mm_o", [&] {
             launch_gemm(stream_, attn_.as<half_t>(), c.heads * hd, L.o.w, a_.as<float>(), d, t);
         });

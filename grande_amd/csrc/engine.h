@@ -207,8 +207,8 @@ class Engine {
     PassPlan prepared_;
     bool profile_ = false;
     struct Timed {
-        const char* name;
-        hipEvent_t a, b;
+        const char* name;  // null for the sequence's start event
+        hipEvent_t e;
     };
     std::vector<Timed> pending_;
     std::vector<hipEvent_t> event_pool_;

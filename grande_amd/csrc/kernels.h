@@ -114,7 +114,8 @@ struct AttnWork {
 // per split (0 = never split).
 void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk,
                     AttnWork& w);
-void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, const int4* merges,
-                      int64_t nmerges);
+void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems);
+// The chunk merges of the split query tiles (after launch_attention).
+void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges);
 
 }  // namespace omg
