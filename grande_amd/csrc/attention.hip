@@ -259,12 +259,13 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     const int row = wave * 16 + lr;
     if (slot >= 0) {
         // Partial result of this chunk: unnormalised O (f32), max and sum.
-        float* op = a.part_o + (int64_t(slot) * A_ROWS + row) * HD + G * 4;
+        const int64_t prow = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row;
+        float* op = a.part_o + prow * HD + G * 4;
 #pragma unroll
         for (int c = 0; c < CT; ++c) *reinterpret_cast<floatx4*>(op + c * 16) = o[c];
         if (G == 0) {
-            a.part_ml[(int64_t(slot) * A_ROWS + row) * 2] = m_run;
-            a.part_ml[(int64_t(slot) * A_ROWS + row) * 2 + 1] = l;
+            a.part_ml[prow * 2] = m_run;
+            a.part_ml[prow * 2 + 1] = l;
         }
         return;
     }
@@ -295,14 +296,15 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
     const int head = int(blockIdx.y) * hpg + lr % hpg;
     if (tq >= a.t) return;
     float M = -INFINITY;
-    for (int c = 0; c < n; ++c) M = fmaxf(M, a.part_ml[(int64_t(slot0 + c) * A_ROWS + row) * 2]);
+    const int g = int(blockIdx.y);
+    for (int c = 0; c < n; ++c) M = fmaxf(M, a.part_ml[((int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row) * 2]);
     constexpr int W = HD / 4;
     float acc[W];
 #pragma unroll
     for (int i = 0; i < W; ++i) acc[i] = 0.0f;
     float L = 0.0f;
     for (int c = 0; c < n; ++c) {
-        const int64_t base = int64_t(slot0 + c) * A_ROWS + row;
+        const int64_t base = (int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row;
         const float m = a.part_ml[base * 2];
         if (m == -INFINITY) continue;
         const float w = __builtin_amdgcn_exp2f(m - M);

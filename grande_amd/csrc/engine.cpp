@@ -339,8 +339,8 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
         E.attn_merges_[0] = DevBuf(16);
         E.attn_items_[1] = DevBuf(size_t(qtiles * per_tile) * 16);
         E.attn_merges_[1] = DevBuf(size_t(qtiles) * 16);
-        E.part_o_ = DevBuf(size_t(qtiles * per_tile) * 64 * size_t(hd) * 4);
-        E.part_ml_ = DevBuf(size_t(qtiles * per_tile) * 64 * 2 * 4);
+        E.part_o_ = DevBuf(size_t(qtiles * per_tile * c.kv_heads) * 64 * size_t(hd) * 4);
+        E.part_ml_ = DevBuf(size_t(qtiles * per_tile * c.kv_heads) * 64 * 2 * 4);
     }
     // The K/V cache starts zeroed: a masked key's probability is exactly 0
     // and its V row must be finite for the 0 * V product to vanish.

@@ -69,6 +69,29 @@ def test_long_prefix_sliding_window_matches_cpu_reference():
             assert rel_diff(got, b) < 4e-3
 
 
+@pytest.mark.parametrize("heads,kv", [(8, 2), (4, 4)])
+def test_split_key_ranges_with_several_kv_heads(heads, kv):
+    """A prefix long enough that global layers cut query tiles' key ranges
+    into chunks (partials merged afterwards), with more than one KV head;
+    a branch's rows must not change when its siblings' tokens do
+    (reference.rs:533-562, same layout)."""
+    rng = np.random.default_rng(5)
+    cfg = gguf_tiny(heads, kv, window=37, vocab=64)
+    prefix = rng.integers(0, 64, 1400).tolist()
+    branches = [BranchTokens(rng.integers(0, 64, n).tolist(), [n - 1, 0]) for n in (20, 7, 33)]
+    eng, plain, gpu_r, _ = build(cfg, 23, g.Q4, g.Q8, capacity=1536)
+    out = eng.evaluate(prefix, branches, Want.HIDDEN)
+    for o, ep, eg in zip(out, oracle_rows(plain, prefix, branches), oracle_rows(gpu_r, prefix, branches)):
+        for got, a, b in zip(o.rows, ep, eg):
+            assert rel_diff(got, a) < 2e-2
+            assert rel_diff(got, b) < 4e-3
+    eng.evict_resident()
+    changed = [BranchTokens(rng.integers(0, 64, len(b.tokens)).tolist(), b.want) for b in branches]
+    changed[1] = branches[1]
+    again = eng.evaluate(prefix, changed, Want.HIDDEN)
+    assert all(np.array_equal(x, y) for x, y in zip(again[1].rows, out[1].rows))
+
+
 def test_resident_prefix_matches_full_pass():
     """reference.rs:430-480: bit-equal rows over a resident prefix."""
     for cfg, lin, emb in [(gemma3_tiny(), g.F16, g.F16), (gguf_tiny(), g.Q4, g.Q8), (gguf_tiny(8, 2), g.Q4, g.Q8)]:
