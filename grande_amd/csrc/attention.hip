@@ -6,10 +6,10 @@
 //
 // Work split: a work item is one query tile (64 rows = (64 / hpg) tokens x
 // the hpg query heads sharing one KV head, 16 rows per wave) and a range of
-// 64-key tiles; the host builds the item lists from the pass's metadata
-// (AttnWork).  On global layers the key range is cut at fixed multiples of
-// `chunk` tiles and the per-chunk partial results are merged in key order
-// by attention_merge; on sliding layers one item covers the whole range.
+// 32-key tiles; the host builds the item lists from the pass's metadata
+// (AttnWork).  A tile's key range is cut at fixed multiples of `chunk`
+// tiles (sliding layers: 256 keys; global layers: 512 keys or more) and the
+// per-chunk partial results are merged in key order by attention_merge.
 // Because chunk boundaries are absolute cache rows and a tile that a query
 // cannot see leaves its state exactly unchanged, each query's arithmetic
 // is the same whichever tokens share its tile: rows over a resident prefix
@@ -38,9 +38,22 @@
 
 namespace omg {
 
-constexpr int A_KT = 64;  // keys per tile
-constexpr int A_THREADS = 256;
-constexpr int A_ROWS = 64;  // query rows per tile
+// Geometry: A_KT keys per K/V tile, A_NW waves of 16 query rows per work
+// item.
+constexpr int A_KT = 32;
+constexpr int A_NW = 4;
+constexpr int A_THREADS = A_NW * 64;
+constexpr int A_ROWS = A_NW * 16;  // query rows per tile
+constexpr int A_KB = A_KT / 16;    // 16-key MFMA blocks per tile
+constexpr int A_TT = A_KT / 32;    // 32-key MFMA steps of the O product per tile
+static_assert(A_KT == 32 || A_KT == 64, "key tile");
+
+int attention_key_tile() { return A_KT; }
+int attention_rows() { return A_ROWS; }
+
+// V^T tile rows hold A_KT keys (A_KT / 8 chunks of 16 B); the chunk swizzle
+// spreads 16 consecutive rows over distinct banks.
+__device__ inline int vt_swz(int row) { return A_KT == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
 
 __device__ inline bool visible(int qp, int qs, int kp, int ks, int window) {
     const bool same_group = ((ks ^ qs) >> 12) == 0;
@@ -52,13 +65,13 @@ __device__ inline bool visible(int qp, int qs, int kp, int ks, int window) {
 // 16-byte chunks of each row are XOR-swizzled so that the MFMA operand reads
 // (16 lanes on 16 consecutive rows at one logical chunk) hit distinct banks:
 //   K   [64 keys][HD]:  physical chunk = logical ^ (row & 15)  (32-chunk rows)
-//   V^T [HD][64 keys]:  physical chunk = logical ^ ((row >> 1) & 7)  (8-chunk rows)
+//   V^T [HD][A_KT keys]:  physical chunk = logical ^ vt_swz(row)
 // The key metadata (cache rows' int4 meta) of each tile comes along.
 template <int HD>
 struct AttnSmem {
     half_t k[2][A_KT * HD];
     half_t v[2][HD * A_KT];
-    int4 kmeta[2][A_KT];
+    int4 kmeta[2][64];  // A_KT keys (repeated to 64 rows)
 };
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
@@ -74,8 +87,8 @@ __device__ __attribute__((always_inline)) inline void dma_tile(AttnSmem<HD>& sm,
                                                                const half_t* vt, const int4* meta, int wave,
                                                                int lane) {
     constexpr int KROW = HD / 8;                     // 16 B chunks per K row
-    constexpr int KINS = A_KT * HD / 8 / WAVE / 4;   // instructions per wave for K
-    constexpr int VINS = HD * A_KT / 8 / WAVE / 4;
+    constexpr int KINS = A_KT * HD / 8 / WAVE / A_NW;   // instructions per wave for K
+    constexpr int VINS = HD * A_KT / 8 / WAVE / A_NW;
 #pragma unroll
     for (int i = 0; i < KINS; ++i) {
         const int blk = wave * KINS + i;            // 1 KB block of the tile
@@ -90,22 +103,24 @@ __device__ __attribute__((always_inline)) inline void dma_tile(AttnSmem<HD>& sm,
         const int blk = wave * VINS + i;
         const int slot = blk * WAVE + lane;
         const int row = slot / (A_KT / 8), pc = slot % (A_KT / 8);
-        const int lc = pc ^ ((row >> 1) & 7);
-        __builtin_amdgcn_global_load_lds((global_void_ptr)(vt + row * A_KT + lc * 8),
+        const int lc = pc ^ vt_swz(row);
+        __builtin_amdgcn_global_load_lds((global_void_ptr)(vt + row * 64 + lc * 8),
                                          (lds_void_ptr)(sm.v[buf] + blk * WAVE * 8), 16, 0, 0);
     }
     if (wave == 0)
-        __builtin_amdgcn_global_load_lds((global_void_ptr)(meta + lane), (lds_void_ptr)(sm.kmeta[buf]), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((global_void_ptr)(meta + (lane % A_KT)), (lds_void_ptr)(sm.kmeta[buf]), 16, 0,
+                                         0);
 }
 
-// One work item per workgroup: 64 query rows (TPW tokens x HPG heads per
-// wave, four waves) against key tiles [tb, te) of the KV head blockIdx.y.
+// One work item per workgroup: A_ROWS query rows (TPW tokens x HPG heads
+// per wave, A_NW waves) against key tiles [tb, te) of the KV head
+// blockIdx.y.
 template <int HD, int HPG>
 __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const int4* __restrict__ items) {
     using SM = AttnSmem<HD>;
     constexpr int DS = HD / 32;  // MFMA steps over the head dim
     constexpr int CT = HD / 16;  // 16-wide output column tiles
-    constexpr int TPW = 16 / HPG, TPB = 4 * TPW;
+    constexpr int TPW = 16 / HPG, TPB = A_NW * TPW;
     constexpr float LOG2E = 1.4426950408889634f;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     SM& sm = *reinterpret_cast<SM*>(smem_raw);
@@ -146,8 +161,8 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     const half_t* kbase = a.kc + int64_t(g) * a.cap_pad * HD;
     const half_t* vbase = a.vt + int64_t(g) * (a.cap_pad / 64) * HD * 64;
     auto issue = [&](int tile, int buf) {
-        dma_tile<HD>(sm, buf, kbase + int64_t(tile) * A_KT * HD, vbase + int64_t(tile) * HD * A_KT,
-                     meta + int64_t(tile) * A_KT, wave, lane);
+        const int64_t k0 = int64_t(tile) * A_KT;  // first key (cache row) of the tile
+        dma_tile<HD>(sm, buf, kbase + k0 * HD, vbase + (k0 / 64) * HD * 64 + k0 % 64, meta + k0, wave, lane);
     };
     if (tb < te) issue(tb, 0);
     for (int tile = tb; tile < te; ++tile) {
@@ -163,22 +178,23 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         // Rows at or past the pass's end are never visible (their stale
         // metadata may look valid).
         const int4 km = sm.kmeta[cur][lane];
-        const bool key_ok = int64_t(tile) * A_KT + lane < a.base + a.t;
+        const bool key_ok = int64_t(tile) * A_KT + (lane % A_KT) < a.base + a.t;
+        constexpr uint64_t KEYS = A_KT == 64 ? ~0ull : 0xffffffffull;
         uint64_t vis[TPW];
-        uint64_t any = 0, all = ~0ull;
+        uint64_t any = 0, all = KEYS;
 #pragma unroll
         for (int u = 0; u < TPW; ++u) {
-            vis[u] = __ballot(key_ok && visible(qpos[u], qseq[u], km.x, km.y, a.window));
+            vis[u] = __ballot(key_ok && visible(qpos[u], qseq[u], km.x, km.y, a.window)) & KEYS;
             any |= vis[u];
             all &= vis[u];
         }
         if (any == 0ull) continue;
-        const bool full = all == ~0ull;
+        const bool full = all == KEYS;
 
         const half_t* K = sm.k[cur];
-        floatx4 sacc[4];
+        floatx4 sacc[A_KB];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < A_KB; ++j) {
             sacc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < DS; ++s) {
@@ -190,7 +206,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         float mt = -INFINITY;
         if (full) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < A_KB; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     sacc[j][r] *= LOG2E;
@@ -201,11 +217,11 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             uint64_t mk = vis[0];
 #pragma unroll
             for (int u = 1; u < TPW; ++u) mk = u_lane == u ? vis[u] : mk;
-            const uint32_t lo = uint32_t(mk), hi = uint32_t(mk >> 32);
-            const uint32_t bits = ((lo >> (4 * G)) & 0xfu) | (((lo >> (16 + 4 * G)) & 0xfu) << 4) |
-                                  (((hi >> (4 * G)) & 0xfu) << 8) | (((hi >> (16 + 4 * G)) & 0xfu) << 12);
+            uint32_t bits = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < A_KB; ++j) bits |= uint32_t((mk >> (16 * j + 4 * G)) & 0xfu) << (4 * j);
+#pragma unroll
+            for (int j = 0; j < A_KB; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float sv = (bits >> (4 * j + r)) & 1u ? sacc[j][r] * LOG2E : -INFINITY;
@@ -220,10 +236,10 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         // taken against 0 then, which gives exactly 0 for every -inf score.
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        half8 pb[2];
+        half8 pb[A_TT];
         float psum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < A_KB; ++j) {
             half2v pr[2];
 #pragma unroll
             for (int r = 0; r < 4; r += 2) {
@@ -244,11 +260,11 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         }
         const half_t* V = sm.v[cur];
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
+        for (int tt = 0; tt < A_TT; ++tt) {
 #pragma unroll
             for (int c = 0; c < CT; ++c) {
                 const int row = c * 16 + lr;
-                const half8 vf = *reinterpret_cast<const half8*>(V + row * A_KT + (((tt * 4 + G) ^ ((row >> 1) & 7)) * 8));
+                const half8 vf = *reinterpret_cast<const half8*>(V + row * A_KT + (((tt * 4 + G) ^ vt_swz(row)) * 8));
                 o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[tt], o[c], 0, 0, 0);
             }
         }
@@ -284,56 +300,59 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 // Merge the chunk partials of one query tile in key order:
 // out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), M = max_c m_c, over
 // the chunks the row saw anything in.  A row with one such chunk gets
-// exactly O / l, as if its tile had not been split.
+// exactly O / l, as if its tile had not been split.  One wave per row (four
+// rows per workgroup); lane l owns columns 4l .. 4l + 3, so every partial
+// row is one contiguous 1 KB wave load, and the loads of all chunks are in
+// flight together.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const int4* __restrict__ merges) {
-    const int4 mg = merges[blockIdx.x];
+    static_assert(HD == 4 * WAVE, "one float4 column per lane");
+    constexpr int MAXC = 16;  // chunks merged per pass over the partials
+    const int4 mg = merges[blockIdx.x / (A_ROWS / 4)];
     const int qtile = mg.x, slot0 = mg.y, n = mg.z;
-    const int row = int(threadIdx.x) / 4, quarter = int(threadIdx.x) % 4;
-    const int hpg = a.heads / a.kv_heads, tpw = 16 / hpg, tpb = 4 * tpw;
-    const int wave = row / 16, lr = row % 16;
-    const int64_t tq = int64_t(qtile) * tpb + wave * tpw + lr / hpg;
-    const int head = int(blockIdx.y) * hpg + lr % hpg;
-    if (tq >= a.t) return;
-    float M = -INFINITY;
     const int g = int(blockIdx.y);
-    for (int c = 0; c < n; ++c) M = fmaxf(M, a.part_ml[((int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row) * 2]);
-    constexpr int W = HD / 4;
-    float acc[W];
-#pragma unroll
-    for (int i = 0; i < W; ++i) acc[i] = 0.0f;
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int row = int(blockIdx.x % (A_ROWS / 4)) * 4 + wave;
+    const int hpg = a.heads / a.kv_heads, tpw = 16 / hpg, tpb = A_NW * tpw;
+    const int64_t tq = int64_t(qtile) * tpb + (row / 16) * tpw + (row % 16) / hpg;
+    if (tq >= a.t) return;
+    const int head = g * hpg + (row % 16) % hpg;
+    auto base = [&](int c) { return (int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row; };
+    float M = -INFINITY;
+    for (int c = 0; c < n; ++c) M = fmaxf(M, a.part_ml[base(c) * 2]);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float L = 0.0f;
-    for (int c = 0; c < n; ++c) {
-        const int64_t base = (int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row;
-        const float m = a.part_ml[base * 2];
-        if (m == -INFINITY) continue;
-        const float w = __builtin_amdgcn_exp2f(m - M);
-        L += a.part_ml[base * 2 + 1] * w;
-        const float* op = a.part_o + base * HD + quarter * W;
+    for (int c0 = 0; c0 < n; c0 += MAXC) {
+        float4 v[MAXC];
+        float2 ml[MAXC];
 #pragma unroll
-        for (int i = 0; i < W; i += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(op + i);
-            acc[i] += v.x * w;
-            acc[i + 1] += v.y * w;
-            acc[i + 2] += v.z * w;
-            acc[i + 3] += v.w * w;
+        for (int c = 0; c < MAXC; ++c) {
+            if (c0 + c < n) {
+                ml[c] = *reinterpret_cast<const float2*>(a.part_ml + base(c0 + c) * 2);
+                v[c] = *reinterpret_cast<const float4*>(a.part_o + base(c0 + c) * HD + lane * 4);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            if (c0 + c >= n || ml[c].x == -INFINITY) continue;
+            const float w = __builtin_amdgcn_exp2f(ml[c].x - M);
+            L += ml[c].y * w;
+            acc.x += v[c].x * w;
+            acc.y += v[c].y * w;
+            acc.z += v[c].z * w;
+            acc.w += v[c].w * w;
         }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    half_t* dst = a.out + (tq * a.heads + head) * HD + quarter * W;
-#pragma unroll
-    for (int i = 0; i < W; i += 4) {
-        const half4 v = {half_t(acc[i] * inv), half_t(acc[i + 1] * inv), half_t(acc[i + 2] * inv),
-                         half_t(acc[i + 3] * inv)};
-        *reinterpret_cast<half4*>(dst + i) = v;
-    }
+    const half4 o = {half_t(acc.x * inv), half_t(acc.y * inv), half_t(acc.z * inv), half_t(acc.w * inv)};
+    *reinterpret_cast<half4*>(a.out + (tq * a.heads + head) * HD + lane * 4) = o;
 }
 
 void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk,
                     AttnWork& w) {
     w.items.clear();
     w.merges.clear();
-    const int hpg = heads / kv_heads, tpb = 4 * (16 / hpg);
+    const int hpg = heads / kv_heads, tpb = A_NW * (16 / hpg);
     int slot = 0;
     for (int64_t q0 = 0, qt = 0; q0 < t; q0 += tpb, ++qt) {
         int64_t lo = INT64_MAX, hi = 0;
@@ -375,7 +394,7 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
     if (a.kv_heads <= 0 || a.heads % a.kv_heads) fail(E_INVALID, "attention: heads / kv_heads");
     const int hpg = a.heads / a.kv_heads;
     if (16 % hpg) fail(E_INVALID, "attention: query heads per KV head must divide 16");
-    if (a.cap_pad % A_KT || a.base + a.t > a.cap_pad) fail(E_INVALID, "attention: cache rows out of range");
+    if (a.cap_pad % 64 || a.base + a.t > a.cap_pad) fail(E_INVALID, "attention: cache rows out of range");
     if (a.window < 0) fail(E_INVALID, "attention: negative window");
     const size_t smem = sizeof(AttnSmem<256>);
     switch (hpg) {
@@ -390,7 +409,8 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
 void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges) {
     if (a.t <= 0 || nmerges <= 0) return;
     if (a.hd != 256) fail(E_INVALID, "attention_merge: head_dim must be 256");
-    attention_merge_kernel<256><<<dim3(unsigned(nmerges), unsigned(a.kv_heads)), dim3(256), 0, s>>>(a, merges);
+    attention_merge_kernel<256><<<dim3(unsigned(nmerges * (A_ROWS / 4)), unsigned(a.kv_heads)), dim3(256), 0, s>>>(
+        a, merges);
     OMG_HIP(hipGetLastError());
 }
 

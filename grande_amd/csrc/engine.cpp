@@ -325,22 +325,27 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.wanted_ = DevBuf(size_t(max_rows) * 4);
     E.labels_ = DevBuf(size_t(c.vocab) * 4);
     E.kv_stage_ = DevBuf(size_t(E.cap_pad_ * 2 * c.kv_heads * hd) * 2);
-    // Attention work: sliding layers never split a query tile's key range
-    // (it is at most window + branch long); global layers split it at fixed
-    // multiples of `chunk` key tiles, at most ~8 chunks per tile.
+    // Attention work: query tiles' key ranges are split at fixed multiples
+    // of `chunk` key tiles: 256 keys on sliding layers (a range is at most
+    // window + branch long), at least 512 keys and at most ~8 chunks over
+    // the cache on global layers.
     {
-        const int64_t key_tiles = E.cap_pad_ / 64;
-        const int64_t tpb = 4 * (16 / (c.heads / c.kv_heads));
+        const int64_t kt = attention_key_tile();
+        const int64_t key_tiles = E.cap_pad_ / kt;
+        const int64_t tpb = attention_rows() / (c.heads / c.kv_heads);
         const int64_t qtiles = (capacity + tpb - 1) / tpb;
-        E.attn_chunk_[0] = 0;
-        E.attn_chunk_[1] = int(std::max<int64_t>(8, (key_tiles + 7) / 8));
-        const int64_t per_tile = (key_tiles + E.attn_chunk_[1] - 1) / E.attn_chunk_[1] + 1;
-        E.attn_items_[0] = DevBuf(size_t(qtiles) * 16);
-        E.attn_merges_[0] = DevBuf(16);
-        E.attn_items_[1] = DevBuf(size_t(qtiles * per_tile) * 16);
-        E.attn_merges_[1] = DevBuf(size_t(qtiles) * 16);
-        E.part_o_ = DevBuf(size_t(qtiles * per_tile * c.kv_heads) * 64 * size_t(hd) * 4);
-        E.part_ml_ = DevBuf(size_t(qtiles * per_tile * c.kv_heads) * 64 * 2 * 4);
+        E.attn_chunk_[0] = int(256 / kt);
+        E.attn_chunk_[1] = int(std::max<int64_t>(512 / kt, (key_tiles + 7) / 8));
+        // Work lists and chunk partials start sized for a few chunks per
+        // query tile and grow with the passes that need more (upload).
+        for (int k = 0; k < 2; ++k) {
+            E.attn_items_[k] = DevBuf(size_t(qtiles * 4) * 16);
+            E.attn_merges_[k] = DevBuf(size_t(qtiles) * 16);
+        }
+        E.part_slots_ = qtiles * 4;
+        E.part_o_ = DevBuf(size_t(E.part_slots_ * c.kv_heads * attention_rows()) * size_t(hd) * 4);
+        E.part_ml_ = DevBuf(size_t(E.part_slots_ * c.kv_heads * attention_rows()) * 2 * 4);
+        (void)key_tiles;
     }
     // The K/V cache starts zeroed: a masked key's probability is exactly 0
     // and its V row must be finite for the 0 * V product to vanish.
@@ -499,8 +504,15 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         AttnWork w;
         attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), kind == 0 ? int(cfg_.window) : 0,
                        attn_chunk_[kind], w);
-        if (w.items.size() * 16 > attn_items_[kind].bytes || w.merges.size() * 16 > std::max<size_t>(16, attn_merges_[kind].bytes))
-            fail(E_CAPACITY, "attention work list larger than its buffer");
+        // The stream is idle here (synchronised above): buffers can grow.
+        if (w.items.size() * 16 > attn_items_[kind].bytes) attn_items_[kind] = DevBuf(w.items.size() * 16);
+        if (w.merges.size() * 16 > attn_merges_[kind].bytes) attn_merges_[kind] = DevBuf(w.merges.size() * 16);
+        if (w.slots > part_slots_) {
+            part_slots_ = w.slots;
+            const size_t rows = size_t(part_slots_ * cfg_.kv_heads * attention_rows());
+            part_o_ = DevBuf(rows * size_t(cfg_.head_dim[0]) * 4);
+            part_ml_ = DevBuf(rows * 2 * 4);
+        }
         n_items_[kind] = int64_t(w.items.size());
         n_merges_[kind] = int64_t(w.merges.size());
         if (!w.items.empty())

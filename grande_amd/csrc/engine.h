@@ -191,6 +191,7 @@ class Engine {
     int attn_chunk_[2] = {0, 0};
     DevBuf attn_items_[2], attn_merges_[2], part_o_, part_ml_;
     int64_t n_items_[2] = {0, 0}, n_merges_[2] = {0, 0};
+    int64_t part_slots_ = 0;  // chunk partial slots part_o_ / part_ml_ hold
     std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
     // pinned host staging
     void* h_in_ = nullptr;

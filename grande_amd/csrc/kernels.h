@@ -109,6 +109,10 @@ struct AttnWork {
     std::vector<int4> items, merges;
     int slots = 0;
 };
+// Geometry of the attention work: keys per K/V tile (the unit of chunk and
+// of the items' key tile ranges) and query rows per work item.
+int attention_key_tile();
+int attention_rows();
 // Build the work of one layer type from the pass's per-token metadata
 // (4 ints per token of this pass, in workspace order).  chunk = key tiles
 // per split (0 = never split).
