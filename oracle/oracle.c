@@ -241,10 +241,12 @@ int orc_model_set(orc_model *m, const char *name, int dtype, int64_t rows, int64
     tensor_free(t);
     t->w = (float *)malloc((size_t)n * sizeof(float));
     if (!t->w) return -2;
+    const int round16 = m->gpu && lin;
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; i++) {
         float v = orc_get(dtype, data, scales, (size_t)i);
         /* matmul.wgsl decodes linear weights to f16 pairs. */
-        t->w[i] = (m->gpu && lin) ? r16(v) : v;
+        t->w[i] = round16 ? r16(v) : v;
     }
     t->rows = rows;
     t->cols = cols;
