@@ -309,7 +309,15 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     }
     E.inv_freq_local_ = upload_bytes(fl.data(), fl.size() * 4);
     E.inv_freq_global_ = upload_bytes(fg.data(), fg.size() * 4);
+    // Rotation (cos, sin) per position: positions stay below the capacity
+    // (every token of a pass has its own cache row).
     const int64_t cap = capacity, d = c.d;
+    E.rope_rows_ = cap;
+    E.rope_local_ = DevBuf(size_t(cap * (hd / 2)) * 8);
+    E.rope_global_ = DevBuf(size_t(cap * (hd / 2)) * 8);
+    launch_rope_table(E.stream_, E.inv_freq_local_.as<float>(), cap, hd / 2, E.rope_local_.as<float2>());
+    launch_rope_table(E.stream_, E.inv_freq_global_.as<float>(), cap, hd / 2, E.rope_global_.as<float2>());
+    OMG_HIP(hipStreamSynchronize(E.stream_));
     E.ids_ = DevBuf(size_t(cap) * 4);
     E.meta_ = DevBuf(size_t(E.cap_pad_) * 16, true);
     E.x_ = DevBuf(size_t(cap * d) * 4);
@@ -548,7 +556,8 @@ void Engine::forward(int64_t t, int64_t base) {
             q.meta = meta_.as<int32_t>();
             q.q_norm = L.q_norm.as<float>();
             q.k_norm = c.has_kv(l) ? L.k_norm.as<float>() : nullptr;
-            q.inv_freq = (c.sliding[size_t(l)] ? inv_freq_local_ : inv_freq_global_).as<float>();
+            q.rope = (c.sliding[size_t(l)] ? rope_local_ : rope_global_).as<float2>();
+            q.rope_rows = rope_rows_;
             q.rope_dims = c.rope_dims[size_t(l)];
             q.eps = c.eps;
             q.q_scale = c.query_scale;

@@ -184,7 +184,8 @@ class Engine {
         DevBuf attn_norm, q_norm, k_norm, post_attn_norm, ffn_norm, post_ffn_norm;
     };
     std::vector<Layer> layers_;
-    DevBuf inv_freq_local_, inv_freq_global_;
+    DevBuf inv_freq_local_, inv_freq_global_, rope_local_, rope_global_;
+    int64_t rope_rows_ = 0;
     // workspace
     DevBuf ids_, meta_, x_, hn_, qkv_, q16_, attn_, a_, act_, rows_, logits_, wanted_, labels_, kv_stage_;
     // attention work lists of the current pass: [0] sliding layers, [1] global

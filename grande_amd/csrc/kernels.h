@@ -49,8 +49,8 @@ struct QkArgs {
     const int32_t* meta;  // 4 ints per cache row: pos, seq, first key row, own row + 1
     const float* q_norm;
     const float* k_norm;
-    const float* inv_freq;  // rope_dims/2 entries
-    int64_t rope_dims;
+    const float2* rope;  // [rope_rows][hd/2]: (cos, sin) of pos * inv_freq[i]
+    int64_t rope_rows, rope_dims;
     float eps, q_scale;
     int heads, kv_heads, hd;
     bool has_kv, v_norm;
@@ -60,6 +60,8 @@ struct QkArgs {
     half_t* vt;   // [kv_heads][cap_pad/64][hd][64], key columns ordered by vt_col
 };
 void launch_qk_prep(hipStream_t s, const QkArgs& a);
+// out[p][i] = (cos, sin)(float(p) * inv_freq[i]) for p < rows, i < half.
+void launch_rope_table(hipStream_t s, const float* inv_freq, int64_t rows, int64_t half, float2* out);
 // rows[i] = rmsnorm(x[wanted[i]]) * w, f32.
 void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int64_t n, int64_t d,
                        const float* w, float eps, float* rows);

@@ -91,7 +91,10 @@ void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, i
 
 // rmsnorm.wgsl:41-68 in residual mode with the fused second norm: the
 // post-attention / post-feedforward norm of `a` is added into the stream x,
-// then the norm that reads x next writes its f16 input hn.
+// then the norm that reads x next writes its f16 input hn.  One wave per
+// row holding the row in registers (NV float4 per lane, element
+// 4 * (lane + 64 j)): every load is issued before the first reduction.
+template <int NV>
 __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ a,
                                                             const float* __restrict__ w1,
                                                             float* __restrict__ x,
@@ -101,34 +104,55 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
     const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
     const int64_t row = int64_t(blockIdx.x) * 4 + wave;
     if (row >= t) return;
+    const int64_t nq = d / 4;
     const float* ar = a + row * d;
     float* xr = x + row * d;
-    float ss = 0.0f;
-    for (int64_t q = lane; q < d / 4; q += WAVE) {
-        const float4 v = *reinterpret_cast<const float4*>(ar + 4 * q);
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    float4 av[NV], xv[NV], g1[NV], g2[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t q = lane + j * WAVE;
+        if (q < nq) {
+            av[j] = *reinterpret_cast<const float4*>(ar + 4 * q);
+            xv[j] = *reinterpret_cast<const float4*>(xr + 4 * q);
+            g1[j] = *reinterpret_cast<const float4*>(w1 + 4 * q);
+            if (w2) g2[j] = *reinterpret_cast<const float4*>(w2 + 4 * q);
+        }
     }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (lane + j * WAVE < nq) {
+            const float4 v = av[j];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
     const float inv = 1.0f / sqrtf(wave_sum(ss) / float(d) + eps);
     float ss2 = 0.0f;
-    for (int64_t q = lane; q < d / 4; q += WAVE) {
-        const float4 v = *reinterpret_cast<const float4*>(ar + 4 * q);
-        const float4 g = *reinterpret_cast<const float4*>(w1 + 4 * q);
-        float4 o = *reinterpret_cast<const float4*>(xr + 4 * q);
-        o.x = (v.x * inv * g.x + o.x) * scale;
-        o.y = (v.y * inv * g.y + o.y) * scale;
-        o.z = (v.z * inv * g.z + o.z) * scale;
-        o.w = (v.w * inv * g.w + o.w) * scale;
-        *reinterpret_cast<float4*>(xr + 4 * q) = o;
-        ss2 += o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t q = lane + j * WAVE;
+        if (q < nq) {
+            const float4 v = av[j], g = g1[j];
+            float4 o = xv[j];
+            o.x = (v.x * inv * g.x + o.x) * scale;
+            o.y = (v.y * inv * g.y + o.y) * scale;
+            o.z = (v.z * inv * g.z + o.z) * scale;
+            o.w = (v.w * inv * g.w + o.w) * scale;
+            *reinterpret_cast<float4*>(xr + 4 * q) = o;
+            ss2 += o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+            xv[j] = o;
+        }
     }
     if (!w2) return;
     const float inv2 = 1.0f / sqrtf(wave_sum(ss2) / float(d) + eps);
-    for (int64_t q = lane; q < d / 4; q += WAVE) {
-        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
-        const float4 g = *reinterpret_cast<const float4*>(w2 + 4 * q);
-        half4 o = {half_t(v.x * inv2 * g.x), half_t(v.y * inv2 * g.y), half_t(v.z * inv2 * g.z),
-                   half_t(v.w * inv2 * g.w)};
-        *reinterpret_cast<half4*>(hn + row * d + 4 * q) = o;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t q = lane + j * WAVE;
+        if (q < nq) {
+            const float4 v = xv[j], g = g2[j];
+            half4 o = {half_t(v.x * inv2 * g.x), half_t(v.y * inv2 * g.y), half_t(v.z * inv2 * g.z),
+                       half_t(v.w * inv2 * g.w)};
+            *reinterpret_cast<half4*>(hn + row * d + 4 * q) = o;
+        }
     }
 }
 
@@ -136,91 +160,163 @@ void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float*
                           half_t* hn, int64_t t, int64_t d, float eps, float scale) {
     if (t <= 0) return;
     if (d % 4 != 0) fail(E_INVALID, "residual_norm: width must be a multiple of 4");
-    residual_norm_kernel<<<dim3(unsigned((t + 3) / 4)), dim3(256), 0, s>>>(a, w1, x, w2, hn, t, d, eps,
-                                                                          scale);
+    const int nv = int((d / 4 + WAVE - 1) / WAVE);
+    const dim3 grid(unsigned((t + 3) / 4)), block(256);
+#define OMG_RN(N) \
+    case N: residual_norm_kernel<N><<<grid, block, 0, s>>>(a, w1, x, w2, hn, t, d, eps, scale); break;
+    switch (nv) {
+        OMG_RN(1) OMG_RN(2) OMG_RN(3) OMG_RN(4) OMG_RN(5) OMG_RN(6) OMG_RN(7) OMG_RN(8)
+        OMG_RN(9) OMG_RN(10) OMG_RN(11) OMG_RN(12) OMG_RN(13) OMG_RN(14) OMG_RN(15) OMG_RN(16)
+        default: fail(E_INVALID, "residual_norm: width above 4096");
+    }
+#undef OMG_RN
     OMG_HIP(hipGetLastError());
 }
 
 // -------------------------------------------------------------- qk prep
 
-// qk_prep.wgsl:66-114: one wave per (token, head slot), four slots per
-// block; slots are the q heads, then (on layers with their own K/V) the k
-// heads, then the v heads.
-// Head row element e = lane * EPL + i, so the RoPE partner e +- HD/2 sits
-// in lane ^ 32.
+// qk_prep.wgsl:66-114 in two kinds of blocks of one launch.
+//
+// The first vblocks blocks own one (64-row V^T cache tile, kv head) each:
+// wave w normalises the tile's rows 16w..16w+15 (when v_norm) and stores
+// them as f16 rows in LDS; then thread c owns head dimension c and writes
+// that dimension's 64 key columns (vt_col order) as eight 16-byte chunks,
+// so every 128-byte row of the tile is written whole from one block.  A
+// tile only partly inside this pass's rows is read first and its other
+// keys' columns are written back unchanged (no other block of the launch
+// touches them).
+//
+// The remaining blocks hold one wave per (token, q or k head slot): the
+// head row is normed, rotated with the position's (cos, sin) and stored
+// f16.  Head row element e = lane * EPL + i, so the RoPE partner e +- HD/2
+// sits in lane ^ 32.
 template <int HD>
-__global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int slots) {
+__global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int64_t vblocks, int qk_slots) {
     constexpr int EPL = HD / WAVE;
     constexpr int HALF = HD / 2;
-    const int slot = int(blockIdx.y) * 4 + int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
-    if (slot >= slots) return;
-    const int64_t tok = blockIdx.x;
-    const int64_t row = a.base + tok;
+    static_assert(EPL == 4 && HD == 256, "qk_prep: one float4 per lane, one dimension per thread");
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int e0 = lane * EPL;
     const int H = a.heads, KV = a.kv_heads;
-    int kind, head;
-    if (slot < H) {
-        kind = 0;
-        head = slot;
-    } else if (slot < H + KV) {
-        kind = 1;
-        head = slot - H;
-    } else {
-        kind = 2;
-        head = slot - H - KV;
-    }
-    const float* src = a.qkv + tok * a.qkv_stride + int64_t(slot) * HD;
-    float v[EPL];
-    float ss = 0.0f;
+    if (int64_t(blockIdx.x) < vblocks) {
+        __shared__ half_t tile_rows[64][HD];
+        const int64_t tile = a.base / 64 + int64_t(blockIdx.x) / KV;
+        const int head = int(int64_t(blockIdx.x) % KV);
+        const int64_t r0 = tile * 64;
+        const int64_t lo = r0 > a.base ? r0 : a.base;
+        const int64_t hi = r0 + 64 < a.base + a.t ? r0 + 64 : a.base + a.t;
+        const bool whole = lo == r0 && hi == r0 + 64;
+        const int dim = int(threadIdx.x);
+        half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + tile) * HD + dim) * 64;
+        uint4 kept[8];
+        if (!whole) {
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        v[i] = src[lane * EPL + i];
-        ss += v[i] * v[i];
-    }
-    ss = wave_sum(ss);
-    if (kind == 2) {
-        const float inv = a.v_norm ? 1.0f / sqrtf(ss / float(HD) + a.eps) : 1.0f;
-        half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + row / 64) * HD) * 64 + vt_col(row);
+            for (int c = 0; c < 8; ++c) kept[c] = reinterpret_cast<const uint4*>(dst)[c];
+        }
+        const float* src = a.qkv + int64_t(H + KV + head) * HD + e0;
+        float4 v[16];
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) dst[int64_t(lane * EPL + i) * 64] = half_t(v[i] * inv);
+        for (int k = 0; k < 16; ++k) {
+            const int64_t row = r0 + 16 * wave + k;
+            v[k] = row >= lo && row < hi ? *reinterpret_cast<const float4*>(src + (row - a.base) * a.qkv_stride)
+                                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            float inv = 1.0f;
+            if (a.v_norm) {
+                const float ss = v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+                inv = 1.0f / sqrtf(wave_sum(ss) / float(HD) + a.eps);
+            }
+            half4 h = {half_t(v[k].x * inv), half_t(v[k].y * inv), half_t(v[k].z * inv), half_t(v[k].w * inv)};
+            *reinterpret_cast<half4*>(&tile_rows[16 * wave + k][e0]) = h;
+        }
+        __syncthreads();
+        // Chunk (half hf, group m) holds keys 32hf + 4m + 0..3, then 32hf + 16 + 4m + 0..3.
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int hf = c / 4, m = c % 4;
+            uint32_t h[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = 32 * hf + 16 * (j / 4) + 4 * m + j % 4;
+                h[j] = __builtin_bit_cast(uint16_t, tile_rows[key][dim]);
+                if (!whole && (r0 + key < lo || r0 + key >= hi)) {
+                    const uint32_t w = j / 2 == 0 ? kept[c].x : j / 2 == 1 ? kept[c].y : j / 2 == 2 ? kept[c].z : kept[c].w;
+                    h[j] = (w >> (16 * (j % 2))) & 0xffffu;
+                }
+            }
+            const uint4 u = {h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
+            reinterpret_cast<uint4*>(dst)[c] = u;
+        }
         return;
     }
-    const float inv = 1.0f / sqrtf(ss / float(HD) + a.eps);
-    const float* nw = kind == 0 ? a.q_norm : a.k_norm;
-    const float pos = float(a.meta[4 * row]);
-    float y[EPL];
+    const int64_t id = (int64_t(blockIdx.x) - vblocks) * 4 + wave;
+    if (id >= a.t * qk_slots) return;
+    const int64_t tok = id / qk_slots;
+    const int slot = int(id - tok * qk_slots);
+    const int64_t row = a.base + tok;
+    const bool is_q = slot < H;
+    const int head = is_q ? slot : slot - H;
+    int pos = a.meta[4 * row];
+    pos = pos < 0 ? 0 : (pos >= a.rope_rows ? int(a.rope_rows - 1) : pos);
+    const float4 v4 = *reinterpret_cast<const float4*>(a.qkv + tok * a.qkv_stride + int64_t(slot) * HD + e0);
+    const float4 w4 = *reinterpret_cast<const float4*>((is_q ? a.q_norm : a.k_norm) + e0);
+    const int d0 = e0 % HALF;
+    const float4* rt = reinterpret_cast<const float4*>(a.rope + int64_t(pos) * HALF + d0);
+    const float4 r01 = rt[0], r23 = rt[1];
+    const float cs[EPL] = {r01.x, r01.z, r23.x, r23.z}, sn[EPL] = {r01.y, r01.w, r23.y, r23.w};
+    const float v[EPL] = {v4.x, v4.y, v4.z, v4.w};
+    float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) y[i] = v[i] * inv * nw[lane * EPL + i];
+    for (int i = 0; i < EPL; ++i) ss += v[i] * v[i];
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / float(HD) + a.eps);
+    const float y[EPL] = {v[0] * inv * w4.x, v[1] * inv * w4.y, v[2] * inv * w4.z, v[3] * inv * w4.w};
     float o[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
         const float partner = __shfl_xor(y[i], 32, WAVE);
-        const int e = lane * EPL + i;
-        const int dd = e < HALF ? e : e - HALF;
-        if (dd < a.rope_dims / 2) {
-            const float ang = pos * a.inv_freq[dd];
-            const float c = cosf(ang), sn = sinf(ang);
-            o[i] = e < HALF ? y[i] * c - partner * sn : y[i] * c + partner * sn;
-        } else {
+        if (d0 + i < a.rope_dims / 2)
+            o[i] = e0 < HALF ? y[i] * cs[i] - partner * sn[i] : y[i] * cs[i] + partner * sn[i];
+        else
             o[i] = y[i];
-        }
     }
-    if (kind == 0) {
-        half_t* dst = a.q16 + (tok * H + head) * HD + lane * EPL;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) dst[i] = half_t(o[i] * a.q_scale);
+    if (is_q) {
+        half4 h = {half_t(o[0] * a.q_scale), half_t(o[1] * a.q_scale), half_t(o[2] * a.q_scale),
+                   half_t(o[3] * a.q_scale)};
+        *reinterpret_cast<half4*>(a.q16 + (tok * H + head) * HD + e0) = h;
     } else {
-        half_t* dst = a.kc + (int64_t(head) * a.cap_pad + row) * HD + lane * EPL;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) dst[i] = half_t(o[i]);
+        half4 h = {half_t(o[0]), half_t(o[1]), half_t(o[2]), half_t(o[3])};
+        *reinterpret_cast<half4*>(a.kc + (int64_t(head) * a.cap_pad + row) * HD + e0) = h;
     }
 }
 
 void launch_qk_prep(hipStream_t s, const QkArgs& a) {
     if (a.t <= 0) return;
-    const int slots = a.heads + (a.has_kv ? 2 * a.kv_heads : 0);
     if (a.base + a.t > a.cap_pad || a.cap_pad % 64) fail(E_INVALID, "qk_prep: cache rows out of range");
     if (a.hd != 256) fail(E_INVALID, "qk_prep: head_dim must be 256");
-    qk_prep_kernel<256><<<dim3(unsigned(a.t), unsigned((slots + 3) / 4)), dim3(256), 0, s>>>(a, slots);
+    if (a.rope_rows <= 0 || a.rope_dims > a.hd) fail(E_INVALID, "qk_prep: rope table");
+    const int qk_slots = a.heads + (a.has_kv ? a.kv_heads : 0);
+    const int64_t tiles = a.has_kv ? (a.base + a.t + 63) / 64 - a.base / 64 : 0;
+    const int64_t vblocks = tiles * a.kv_heads;
+    const int64_t blocks = vblocks + (a.t * qk_slots + 3) / 4;
+    qk_prep_kernel<256><<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(a, vblocks, qk_slots);
+    OMG_HIP(hipGetLastError());
+}
+
+__global__ __launch_bounds__(256) void rope_table_kernel(const float* inv_freq, int64_t rows, int64_t half,
+                                                         float2* out) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= rows * half) return;
+    const int64_t p = i / half, dd = i - p * half;
+    const float ang = float(p) * inv_freq[dd];
+    out[i] = make_float2(cosf(ang), sinf(ang));
+}
+
+void launch_rope_table(hipStream_t s, const float* inv_freq, int64_t rows, int64_t half, float2* out) {
+    if (rows <= 0 || half <= 0) fail(E_INVALID, "rope table: empty");
+    if (rows >= (int64_t(1) << 24)) fail(E_INVALID, "rope table: positions must stay below 2^24");
+    rope_table_kernel<<<dim3(unsigned((rows * half + 255) / 256)), dim3(256), 0, s>>>(inv_freq, rows, half, out);
     OMG_HIP(hipGetLastError());
 }
 
