@@ -2,39 +2,42 @@
 // matmul_gated.wgsl's job): Y[M,N] = f16(X)[M,K] . deq(W)[N,K]^T with f32
 // accumulation on v_mfma_f32_16x16x32_f16.
 //
-// One workgroup = WGM x 2 wave64s over a BM x BN output tile (8 waves for
-// the large tiles, so two waves share each SIMD); K advances 64 at a time
-// ("stages").  Data path of one stage:
+// Row-owner tiles: NW wave64s per workgroup over a BM x BN output tile,
+// BM = 16 * MI activation rows.  Each wave owns 16 * NJ weight rows (gated:
+// NJ / 2 row blocks of the gate matrix and the same rows of the up matrix)
+// across all BM rows, so every weight row is decoded by exactly one wave,
+// straight from its codes into MFMA operand registers.  K advances 64 at a
+// time ("stages").  Data path of one stage:
 //
-//   global --LDS DMA--> ring slot (NS slots): X tile f16 [BM][64], raw weight
-//       codes (Q4: [BNW][2 blocks][16 B], Q8: [BNW][64 B]) and the two block
-//       scales of every weight row;
-//   ring slot --decode (all threads, one stage ahead)--> f16 weight tile
-//       [BNW][64] (two buffers);
-//   X tile + f16 weight tile --ds_read_b128--> MFMA.
+//   global --LDS DMA--> ring slot (NS slots): X tile f16 [BM][64], raw
+//       weight codes (Q4: [rows][2 blocks][16 B], Q8: [rows][64 B], F16:
+//       [rows][64] f16) and one dword of two block scales per weight row;
+//   ring slot --ds_read--> X fragments (b128) and this wave's codes and
+//       scales --decode in registers--> weight fragments --> MFMA.
 //
-// The DMA (buffer_load ... lds, 16 B or 4 B per lane) keeps NS - 2 stages of
-// loads in flight beyond the one being decoded, with no registers held for
-// them; the weight is decoded once per workgroup and stage (the reference's
-// f16 rounding point, shaders/weight.wgsl:40-54) and read by all BM rows.
-// F16 weights skip the decode: their tile is DMA'd straight into the ring.
-// One barrier per stage; the decode's arithmetic is interleaved with the
-// stage's MFMAs.
+// The DMA (buffer_load ... lds, 16 B or 4 B per lane) keeps NS - 1 stages
+// in flight with no registers held for them; the stage's K offset rides in
+// the instruction's scalar offset, so the per-lane offsets are fixed for
+// the whole loop.  One barrier per stage.  The ring alone sets the LDS
+// footprint, so several workgroups share a CU.  The decode rounds
+// (q - 8) * d (or q * d) to f16 once, the reference's f16 rounding point
+// (shaders/weight.wgsl:40-54).
 //
-// X and f16-weight tiles are 128 B per row with the 16 B chunk c of row r
+// X and f16 weight tiles are 128 B per row with the 16 B chunk c of row r
 // stored at c ^ ((r >> 1) & 7), so the 16 rows x 4 chunks of one fragment
 // read hit distinct banks.
 //
 // MFMA operand layout (16x16x32 f16): lane l supplies A[l % 16][8*(l/16)..+8)
 // and B[8*(l/16)..+8)[l % 16]; the f32 result D[4*(l/16) + r][l % 16] lands
-// in element r of the lane's float4.  The weight tile is the A operand and
-// the activation tile the B operand, so D = (X W^T)^T and each lane ends up
-// with four consecutive output columns of one row: the epilogue stores them
-// as one vector.
+// in element r of the lane's float4.  The weight fragment is the A operand
+// and the activation fragment the B operand, so D = (X W^T)^T and each lane
+// ends up with four consecutive output columns of one row: the epilogue
+// stores them as one vector.
 //
 // Bounds: every global read is a buffer load on a per-tile resource, so rows
-// past M or N read as zero in hardware; the K tail (K % 64 == 32) is sent
-// out of range for X and decoded as zero for W.
+// past M or N read as zero in hardware; in the K tail (K % 64 == 32) the X
+// lanes and weight lanes past K are sent out of range by their lane offset
+// (a zero activation times a zero weight).
 #include <string>
 
 #include "common.h"
@@ -45,44 +48,8 @@ namespace omg {
 constexpr int G_BK = 64;  // k per stage
 constexpr int G_ROW = G_BK * 2;  // bytes per LDS tile row
 constexpr uint32_t OOB = 0x7ffffff0u;  // an offset past every resource
-// VALU instructions scheduled after each MFMA of the main loop (0: leave
-// the order to the compiler).
-constexpr int G_SCHED = 4;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-template <int QUANT, int BM, int BN, bool GATED, int NS, int WGM>
-struct Cfg {
-    // WGM x 2 waves; wave (wm, wn) computes rows wm * WM.. and columns wn * BN / 2..
-    static constexpr int NW = WGM * 2, T = NW * WAVE, WM = BM / WGM;
-    static constexpr int BNW = GATED ? 2 * BN : BN;  // weight rows per tile
-    static constexpr int MI = WM / 16, NI = BN / 32, NJ = GATED ? 2 * NI : NI;
-    // 16-byte chunks per stage and DMA instructions per wave per stage.
-    static constexpr int X_CH = BM * 8;
-    static constexpr int X_I = X_CH / T;
-    static constexpr int W_CPR = QUANT == Q4_DT ? 2 : (QUANT == Q8_DT ? 4 : 8);  // chunks per weight row
-    static constexpr int W_CH = BNW * W_CPR;
-    static constexpr int W_I = (W_CH + T - 1) / T;
-    // Scales: one dword (two f16) per weight row, gate and up rows apart.
-    static constexpr int S_HALF = QUANT == F16_DT ? 0 : BN;  // rows per matrix
-    static constexpr int S_I = QUANT == F16_DT ? 0 : (S_HALF + T - 1) / T;
-    static constexpr int S_MATS = GATED ? 2 : 1;
-    static constexpr int C = X_I + W_I + S_I * S_MATS;  // DMA instructions per wave per stage
-    static constexpr int X_BYTES = BM * G_ROW;
-    static constexpr int W_BYTES = W_I * T * 16;
-    static constexpr int S_BYTES = S_I * T * 4;  // per matrix
-    static constexpr int STAGE = X_BYTES + W_BYTES + S_MATS * S_BYTES;
-    static constexpr int W16_BYTES = QUANT == F16_DT ? 0 : BNW * G_ROW;
-    static constexpr int LDS = NS * STAGE + 2 * W16_BYTES;
-    // Decode work per thread and stage: one 16 B f16 chunk (8 weights) each.
-    static constexpr int DQ = BNW * 8 / T;
-    static_assert(WM % 16 == 0 && BN % 32 == 0, "tile sizes");
-    static_assert(X_CH % T == 0, "X tile must split evenly over the waves");
-    static_assert(QUANT != F16_DT || W_CH % T == 0, "f16 weight tile must split evenly");
-    static_assert(QUANT == F16_DT || (BNW * 8) % T == 0, "decode must split evenly");
-    static_assert(NS >= 3, "ring needs >= 3 slots");
-    static_assert(C <= 63, "vmcnt range");
-};
 
 struct GemmArgs {
     const half_t* x;
@@ -122,14 +89,36 @@ __device__ inline float gelu_tanh(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-template <int QUANT, int BM, int BN, bool GATED, int NS, int WGM>
-__global__ __launch_bounds__(WGM * 2 * WAVE) void gemm_kernel(GemmArgs g) {
-    using P = Cfg<QUANT, BM, BN, GATED, NS, WGM>;
-    constexpr int NW = P::NW;
+template <int QUANT, int MI, int NJ, bool GATED, int NS, int NW_ = 4>
+struct Cfg {
+    static constexpr int NW = NW_, T = NW * WAVE;
+    static constexpr int BM = 16 * MI;
+    static constexpr int WR = 16 * NJ;                 // weight rows per wave
+    static constexpr int BNW = NW * WR;                // weight rows per tile
+    static constexpr int BN = GATED ? BNW / 2 : BNW;   // output columns per tile
+    static constexpr int X_CH = BM * 8, X_I = X_CH / T;
+    static constexpr int W_CPR = QUANT == Q4_DT ? 2 : (QUANT == Q8_DT ? 4 : 8);
+    static constexpr int W_CH = BNW * W_CPR, W_I = (W_CH + T - 1) / T;
+    static constexpr int S_I = QUANT == F16_DT ? 0 : (BNW + T - 1) / T;
+    static constexpr int C = X_I + W_I + S_I;  // DMA instructions per wave per stage
+    static constexpr int X_BYTES = BM * G_ROW, W_BYTES = W_I * T * 16, S_BYTES = S_I * T * 4;
+    static constexpr int STAGE = X_BYTES + W_BYTES + S_BYTES;
+    static constexpr int LDS = NS * STAGE;
+    static_assert(X_CH % T == 0, "the X tile must split evenly over the waves");
+    static_assert(LDS <= 160 * 1024, "ring larger than the LDS");
+    static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
+    static_assert(BN % 64 == 0 || !GATED, "a scale DMA instruction must stay in one matrix");
+    static_assert(NS >= 3, "ring needs >= 3 slots");
+    static_assert(C <= 63, "vmcnt range");
+};
+
+template <int QUANT, int MI, int NJ, bool GATED, int NS, int NW_>
+__global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
+    using P = Cfg<QUANT, MI, NJ, GATED, NS, NW_>;
+    constexpr int NW = P::NW, BM = P::BM, BN = P::BN, WR = P::WR;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = int(threadIdx.x), lane = tid % WAVE;
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
-    const int wm = wave / 2, wn = wave % 2;  // wave grid WGM x 2
 
     // Workgroups are dispatched round-robin over the 8 XCDs (each with its
     // own L2): workgroup b runs on XCD b % 8.  Give each XCD a contiguous run
@@ -143,20 +132,18 @@ __global__ __launch_bounds__(WGM * 2 * WAVE) void gemm_kernel(GemmArgs g) {
     if (tile >= ntiles) return;
     const int64_t n0 = int64_t(tile % ntn) * BN, m0 = int64_t(tile / ntn) * BM;
     const int nk = int((K + G_BK - 1) / G_BK);
-    const int K32 = int(K), KB32 = int(KB);
+    const int K32 = int(K);
     const int64_t rows_m = M - m0 < BM ? M - m0 : BM;
     const int64_t rows_n = N - n0 < BN ? N - n0 : BN;
 
-    // ---- per-tile buffer resources and per-lane DMA offsets (stage 0)
     const __amdgpu_buffer_rsrc_t rx = rsrc(g.x + m0 * g.ldx, rows_m * g.ldx * 2);
-    const int64_t wrow = QUANT == Q4_DT ? KB * 16 : (QUANT == Q8_DT ? K : 2 * K);  // bytes per weight row
+    const int64_t wrow = QUANT == Q4_DT ? KB * 16 : (QUANT == Q8_DT ? K : 2 * K);
     const uint8_t* const wbase0 = static_cast<const uint8_t*>(g.w0.data) + n0 * wrow;
     const uint8_t* const wbase1 = static_cast<const uint8_t*>(g.w1.data) + n0 * wrow;
     const uint16_t* const sbase0 = g.w0.scales ? g.w0.scales + n0 * g.w0.sld : nullptr;
     const uint16_t* const sbase1 = g.w1.scales ? g.w1.scales + n0 * g.w1.sld : nullptr;
     const int64_t sbytes = g.w0.scales ? rows_n * g.w0.sld * 2 : 0;
 
-    // X chunk of this lane in instruction i: LDS slot (i * 4 + wave) * 64 + lane.
     uint32_t xoff[P::X_I];
     int xcol[P::X_I];
 #pragma unroll
@@ -166,211 +153,165 @@ __global__ __launch_bounds__(WGM * 2 * WAVE) void gemm_kernel(GemmArgs g) {
         xcol[i] = lc * 8;
         xoff[i] = uint32_t((r * g.ldx + lc * 8) * 2);
     }
-    uint32_t woff[P::W_I];
+    uint32_t woff[P::W_I], wtail[P::W_I];  // wtail: the lane's offset in the K-tail stage
     bool wup[P::W_I];
 #pragma unroll
     for (int i = 0; i < P::W_I; ++i) {
-        const int blk = i * NW + wave;  // wave-uniform
+        const int blk = i * NW + wave;
         const int slot = blk * WAVE + lane;
         const int rw = slot / P::W_CPR, c = slot % P::W_CPR;
-        wup[i] = GATED && blk * WAVE / P::W_CPR >= BN;  // whole instruction on one matrix
+        wup[i] = GATED && blk * WAVE / P::W_CPR >= BN;
         const int n = GATED && rw >= BN ? rw - BN : rw;
         uint32_t o;
+        bool past;  // chunk past K when only the stage's first 32 k exist
         if constexpr (QUANT == Q4_DT) {
             o = uint32_t((n * KB + c) * 16);
+            past = c >= 1;
         } else if constexpr (QUANT == Q8_DT) {
             o = uint32_t(n * K + c * 16);
+            past = c >= 2;
         } else {
             const int lc = c ^ swz(rw);
             o = uint32_t((n * K + lc * 8) * 2);
+            past = lc >= 4;
         }
         woff[i] = slot < P::W_CH ? o : OOB;
+        wtail[i] = slot < P::W_CH && !past ? o : OOB;
     }
     uint32_t soff[P::S_I > 0 ? P::S_I : 1];
+    bool sup[P::S_I > 0 ? P::S_I : 1];
 #pragma unroll
     for (int i = 0; i < P::S_I; ++i) {
-        const int slot = (i * NW + wave) * WAVE + lane;  // weight row within one matrix
-        soff[i] = slot < BN ? uint32_t(slot * g.w0.sld * 2) : OOB;
+        const int rw = (i * NW + wave) * WAVE + lane;  // one scale dword per weight row
+        sup[i] = GATED && (i * NW + wave) * WAVE >= BN;
+        const int n = GATED && rw >= BN ? rw - BN : rw;
+        soff[i] = rw < P::BNW ? uint32_t(n * g.w0.sld * 2) : OOB;
     }
 
+    // Issue stage s's DMA into its ring slot.  The stage's K offset rides in
+    // the scalar offset, so the lane offsets stay fixed; only the K-tail
+    // stage (K % 64 == 32) masks X lanes per lane.  Stages past the end use
+    // empty resources (every lane out of range), so every wave always
+    // issues P::C instructions per stage.
     auto slot_base = [&](int s) { return smem + (s % NS) * P::STAGE; };
-
-    // Issue stage s's DMA into its ring slot (all lanes OOB past the end, so
-    // every wave always issues P::C instructions per stage).
     auto issue = [&](int s) {
         uint8_t* base = slot_base(s);
         const bool live = s < nk;
         const int k0 = s * G_BK;
-        const int kk = live ? K32 : 0;  // past the end: every lane out of range
+        const int64_t xbytes = live ? rows_m * g.ldx * 2 : 0;
+        // (Range checks cover the lane offset only: a row's offset plus the
+        // stage offset stays inside the row, and rows past M are out of
+        // range by their lane offset.  Each resource is a named value built
+        // at its use: passed inline, or held across branches, it is not
+        // accepted by the host-side compile of this kernel.)
+        const bool tail = k0 + G_BK > K32;
 #pragma unroll
         for (int i = 0; i < P::X_I; ++i) {
-            const uint32_t o = k0 + xcol[i] < kk ? xoff[i] + uint32_t(k0 * 2) : OOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rx, (lds_ptr_t)(base + (i * NW + wave) * WAVE * 16), 16, o, 0, 0, 0);
+            const uint32_t o = tail && xcol[i] >= K32 - k0 ? OOB : xoff[i];
+            const __amdgpu_buffer_rsrc_t r = rsrc(g.x + m0 * g.ldx, xbytes);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(base + (i * NW + wave) * WAVE * 16), 16, o,
+                                                     k0 * 2, 0, 0);
         }
-        const uint32_t wstep = QUANT == Q4_DT ? uint32_t(k0 / 2) : (QUANT == Q8_DT ? uint32_t(k0) : uint32_t(k0 * 2));
+        // (So in the K-tail stage the weight lanes past K are masked by
+        // offset as well.)
+        const int wstep = QUANT == Q4_DT ? k0 / 2 : (QUANT == Q8_DT ? k0 : k0 * 2);
 #pragma unroll
         for (int i = 0; i < P::W_I; ++i) {
-            const uint32_t o = live ? woff[i] + wstep : OOB;
-            // (A select between two buffer resources is not accepted by
-            // the host-side compile of this kernel; select the base.)
-            const __amdgpu_buffer_rsrc_t rw = rsrc(wup[i] ? wbase1 : wbase0, rows_n * wrow);
+            const uint32_t o = tail ? wtail[i] : woff[i];
+            const __amdgpu_buffer_rsrc_t r = rsrc(wup[i] ? wbase1 : wbase0, live ? rows_n * wrow : 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(base + P::X_BYTES + (i * NW + wave) * WAVE * 16),
+                                                     16, o, wstep, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < P::S_I; ++i) {
+            const __amdgpu_buffer_rsrc_t r = rsrc(sup[i] ? sbase1 : sbase0, live ? sbytes : 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rw, (lds_ptr_t)(base + P::X_BYTES + (i * NW + wave) * WAVE * 16), 16, o, 0, 0, 0);
-        }
-#pragma unroll
-        for (int mat = 0; mat < P::S_MATS * (P::S_I > 0 ? 1 : 0); ++mat) {
-#pragma unroll
-            for (int i = 0; i < P::S_I; ++i) {
-                const uint32_t o = live ? soff[i] + uint32_t(k0 / 16) : OOB;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rsrc(mat ? sbase1 : sbase0, sbytes),
-                    (lds_ptr_t)(base + P::X_BYTES + P::W_BYTES + mat * P::S_BYTES + (i * NW + wave) * WAVE * 4),
-                    4, o, 0, 0, 0);
-            }
+                r, (lds_ptr_t)(base + P::X_BYTES + P::W_BYTES + (i * NW + wave) * WAVE * 4), 4, soff[i], k0 / 16, 0, 0);
         }
     };
 
-    // Decode stage s (raw codes in its ring slot) into f16 tile buffer s & 1,
-    // in two halves: the LDS reads of the codes and scales, issued early,
-    // and per 16 B chunk the arithmetic and the LDS write, spread between
-    // the MFMAs of the current stage.
-    struct Raw {
-        uint2 code[P::DQ];
-        half2v dd[P::DQ];  // the block scale, twice
-    };
-    auto decode_read = [&](int s, Raw& r) {
-        if constexpr (QUANT != F16_DT) {
-            const uint8_t* base = slot_base(s);
-            const uint8_t* raw = base + P::X_BYTES;
-            const uint8_t* sc = base + P::X_BYTES + P::W_BYTES;
-            const int kb0 = s * 2;
-#pragma unroll
-            for (int q = 0; q < P::DQ; ++q) {
-                const int w = tid + q * P::T;  // 16 B output chunk: row w / 8, k chunk w % 8
-                const int rw = w / 8, lc = w % 8, blk = lc / 4;
-                const int srow = GATED && rw >= BN ? P::S_BYTES + (rw - BN) * 4 : rw * 4;
-                half_t d = *reinterpret_cast<const half_t*>(sc + srow + blk * 2);
-                // K tail: codes past K are garbage but finite ((q - 8) or an
-                // int8), so a zero scale zeroes them.
-                if (kb0 + blk >= KB32) d = half_t(0.0f);
-                r.dd[q] = half2v{d, d};
-                if constexpr (QUANT == Q4_DT)
-                    r.code[q].x = *reinterpret_cast<const uint32_t*>(raw + rw * 32 + blk * 16 + (lc % 4) * 4);
-                else
-                    r.code[q] = *reinterpret_cast<const uint2*>(raw + rw * 64 + lc * 8);
-            }
-        }
-    };
-    auto decode_write = [&](int s, const Raw& r, int q) {
-        if constexpr (QUANT != F16_DT) {
-            uint8_t* dst = smem + NS * P::STAGE + (s & 1) * P::W16_BYTES;
-            const int w = tid + q * P::T;
-            const int rw = w / 8, lc = w % 8;
-            half8 v;
-            if constexpr (QUANT == Q4_DT)
-                v = dq4_word(r.code[q].x, r.dd[q]);
-            else
-                v = dq8_words(r.code[q].x, r.code[q].y, r.dd[q]);
-            *reinterpret_cast<half8*>(dst + rw * G_ROW + ((lc ^ swz(rw)) * 16)) = v;
-        }
-    };
-    auto decode = [&](int s) {
-        Raw r;
-        decode_read(s, r);
-#pragma unroll
-        for (int q = 0; q < P::DQ; ++q) decode_write(s, r, q);
+    // Tile-local weight row of this wave's row block j.
+    auto wrow_of = [&](int j) {
+        if constexpr (GATED)
+            return j < NJ / 2 ? wave * (WR / 2) + 16 * j : BN + wave * (WR / 2) + 16 * (j - NJ / 2);
+        else
+            return wave * WR + 16 * j;
     };
 
-    floatx4 acc[P::MI][P::NJ];
+    floatx4 acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < P::MI; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < P::NJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Per-lane LDS byte offsets of the fragment reads (row l % 16 of a
-    // 16-row block, chunk ks * 4 + l / 16, swizzled; blocks start at
-    // multiples of 16 so the swizzle depends on l % 16 only).
-    const int lr = lane % 16;
+    const int lr = lane % 16, lg = lane / 16;
     int foff[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) foff[ks] = lr * G_ROW + (((ks * 4 + lane / 16) ^ swz(lr)) * 16);
+    for (int ks = 0; ks < 2; ++ks) foff[ks] = lr * G_ROW + (((ks * 4 + lg) ^ swz(lr)) * 16);
 
-    // ---- prologue: stages 0 .. NS-2 in flight, stage 0 decoded
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue(s);
-    wait_vm<(NS - 2) * P::C>();
-    lds_barrier();
-    decode(0);
 
     for (int kt = 0; kt < nk; ++kt) {
-        // stage kt + 1 landed (this wave's DMA), then everyone's, and
-        // everyone is done with stage kt - 1 (its slot and f16 buffer)
-        wait_vm<(NS - 3) * P::C>();
+        // This wave's DMA of stage kt landed, then everyone's; everyone is
+        // done reading stage kt - 1, whose slot the next DMA reuses.
+        wait_vm<(NS - 2) * P::C>();
         lds_barrier();
         issue(kt + NS - 1);
-
-        // Past the last stage the decode below turns the zeros of an
-        // out-of-range DMA into a buffer nobody reads; unconditional keeps
-        // the loop simple.
-        Raw raw;
-        decode_read(kt + 1, raw);
         const uint8_t* X = slot_base(kt);
-        const uint8_t* W = QUANT == F16_DT ? slot_base(kt) + P::X_BYTES
-                                           : smem + NS * P::STAGE + (kt & 1) * P::W16_BYTES;
-        half8 af[2][P::MI], bf[2][P::NJ];
+        const uint8_t* Wr = X + P::X_BYTES;
+        const uint8_t* S = Wr + P::W_BYTES;
+        uint32_t sc[NJ];
+        if constexpr (QUANT != F16_DT) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) sc[j] = *reinterpret_cast<const uint32_t*>(S + (wrow_of(j) + lr) * 4);
+        }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
+            half8 xf[MI], wf[NJ];
 #pragma unroll
-            for (int i = 0; i < P::MI; ++i)
-                af[ks][i] = *reinterpret_cast<const half8*>(X + (wm * P::WM + i * 16) * G_ROW + foff[ks]);
+            for (int i = 0; i < MI; ++i) xf[i] = *reinterpret_cast<const half8*>(X + i * 16 * G_ROW + foff[ks]);
 #pragma unroll
-            for (int j = 0; j < P::NJ; ++j) {
-                const int brow = (GATED && j >= P::NI) ? BN + wn * (BN / 2) + (j - P::NI) * 16 : wn * (BN / 2) + j * 16;
-                bf[ks][j] = *reinterpret_cast<const half8*>(W + brow * G_ROW + foff[ks]);
-            }
-        }
-        constexpr int NMF = P::MI * P::NJ * 2;
-        constexpr int PER = P::DQ > 0 ? (NMF / P::DQ > 0 ? NMF / P::DQ : 1) : NMF + 1;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int i = 0; i < P::MI; ++i)
-#pragma unroll
-                for (int j = 0; j < P::NJ; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[ks][j], af[ks][i], acc[i][j], 0, 0, 0);
-                    const int m = (ks * P::MI + i) * P::NJ + j + 1;
-                    if (m % PER == 0 && m / PER <= P::DQ) decode_write(kt + 1, raw, m / PER - 1);
+            for (int j = 0; j < NJ; ++j) {
+                const int rw = wrow_of(j) + lr;
+                if constexpr (QUANT == F16_DT) {
+                    wf[j] = *reinterpret_cast<const half8*>(Wr + wrow_of(j) * G_ROW + foff[ks]);
+                } else {
+                    const uint16_t db = uint16_t(sc[j] >> (16 * ks));
+                    const half_t d = __builtin_bit_cast(half_t, db);
+                    if constexpr (QUANT == Q4_DT) {
+                        const uint32_t w = *reinterpret_cast<const uint32_t*>(Wr + rw * 32 + ks * 16 + lg * 4);
+                        wf[j] = dq4_word(w, half2v{d, d});
+                    } else {
+                        const uint2 u = *reinterpret_cast<const uint2*>(Wr + rw * 64 + ks * 32 + lg * 8);
+                        wf[j] = dq8_words(u.x, u.y, half2v{d, d});
+                    }
                 }
-        if constexpr (G_SCHED > 0) {
-            // Issue order for the stage: the DMA, every LDS read (fragments
-            // and raw codes), then the MFMAs with the decode's VALU work in
-            // their shadow, then the decode's LDS writes.
-            constexpr int NDSR = (P::MI + P::NJ) * 2 + (QUANT == F16_DT ? 0 : 2 * P::DQ);
-            __builtin_amdgcn_sched_group_barrier(0x020, P::C, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, NDSR, 0);
-#pragma unroll
-            for (int q = 0; q < NMF; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, G_SCHED, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x200, P::DQ, 0);
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], xf[i], acc[i][j], 0, 0, 0);
         }
     }
-    wait_vm<0>();  // the trailing (out-of-range) DMA before the workgroup ends
+    wait_vm<0>();
 
-    // ---- epilogue: lane (lr, G) holds columns 4G..4G+3 of row lr of each 16 x 16 tile.
+    // Epilogue: lane (lr, lg) holds output columns 4 lg..4 lg + 3 of row lr
+    // of each 16 x 16 block.
+    constexpr int NO = GATED ? NJ / 2 : NJ;
+    const int64_t nw0 = n0 + (GATED ? wave * (WR / 2) : wave * WR);
 #pragma unroll
-    for (int i = 0; i < P::MI; ++i) {
-        const int64_t m = m0 + wm * P::WM + i * 16 + lr;
+    for (int i = 0; i < MI; ++i) {
+        const int64_t m = m0 + i * 16 + lr;
         if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < P::NI; ++j) {
-            const int64_t n = n0 + wn * (BN / 2) + j * 16 + (lane / 16) * 4;
+        for (int j = 0; j < NO; ++j) {
+            const int64_t n = nw0 + j * 16 + lg * 4;
             float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                v[r] = GATED ? gelu_tanh(acc[i][j][r]) * acc[i][j + (GATED ? P::NI : 0)][r] : acc[i][j][r];
+                v[r] = GATED ? gelu_tanh(acc[i][j][r]) * acc[i][j + (GATED ? NJ / 2 : 0)][r] : acc[i][j][r];
             if (n + 3 < N) {
                 if constexpr (GATED) {
                     *reinterpret_cast<half4*>(static_cast<half_t*>(g.y) + m * g.ldy + n) =
@@ -393,38 +334,48 @@ __global__ __launch_bounds__(WGM * 2 * WAVE) void gemm_kernel(GemmArgs g) {
     }
 }
 
-template <int QUANT, int BM, int BN, bool GATED, int NS, int WGM = 2>
+template <int QUANT, int MI, int NJ, bool GATED, int NS, int NW = 4>
 static void run(hipStream_t s, const GemmArgs& g) {
-    using P = Cfg<QUANT, BM, BN, GATED, NS, WGM>;
-    static bool lds_set = false;  // once per instantiation (per process)
+    using P = Cfg<QUANT, MI, NJ, GATED, NS, NW>;
+    static bool lds_set = false;
     if (!lds_set) {
-        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<QUANT, BM, BN, GATED, NS, WGM>),
+        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<QUANT, MI, NJ, GATED, NS, NW>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
         lds_set = true;
     }
     const int64_t N = g.w0.rows;
-    const int64_t tiles = ((N + BN - 1) / BN) * ((g.m + BM - 1) / BM);
+    const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + P::BM - 1) / P::BM);
     const dim3 grid(unsigned((tiles + 7) / 8 * 8));
-    gemm_kernel<QUANT, BM, BN, GATED, NS, WGM><<<grid, dim3(P::T), P::LDS, s>>>(g);
+    gemm_kernel<QUANT, MI, NJ, GATED, NS, NW><<<grid, dim3(P::T), P::LDS, s>>>(g);
     OMG_HIP(hipGetLastError());
 }
 
-// Tile choice (measured on MI355X over the 270M / 1B decoder shapes):
-// 128 x 128 (128 x 64 gated) tiles with 8 waves while they still give about
-// 160+ workgroups; smaller tiles for the short branch-only passes.
+// Tile choice, measured on MI355X over the 270M / 1B / 4B decoder shapes
+// (cold passes of 2,384 tokens, warm passes of 384):
+//   short passes (M <= 512): small tiles, many workgroups;
+//   narrow outputs (N <= 1280, the o and down projections): 64 x 64 tiles
+//   with a four-stage ring;
+//   wide outputs: 64 x 128 tiles.
+// Long K (>= 4096) and Q8 codes take 96-row tiles: the decode is spread
+// over more MFMAs.  Gated: 64 x 128 weight rows (64 output columns),
+// 96 rows for long K / Q8, 128 x 256 for very wide layers.
 template <int QUANT, bool GATED>
 static void dispatch(hipStream_t s, const GemmArgs& g) {
-    const int64_t N = g.w0.rows, M = g.m;
-    auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
+    const bool big_mi = K >= 4096 || QUANT == Q8_DT;
     if constexpr (!GATED) {
-        if (tiles(128, 128) >= 160) return run<QUANT, 128, 128, false, 4, 4>(s, g);
-        if (tiles(128, 64) >= 160) return run<QUANT, 128, 64, false, 4, 4>(s, g);
-        if (tiles(64, 64) >= 128) return run<QUANT, 64, 64, false, 4, 4>(s, g);
-        return run<QUANT, 32, 32, false, 8, 2>(s, g);
+        if (M <= 512) return run<QUANT, 2, 1, false, 4, 2>(s, g);
+        if (N <= 1280) {
+            if (big_mi) return run<QUANT, 6, 1, false, 4, 4>(s, g);
+            return run<QUANT, 4, 1, false, 4, 4>(s, g);
+        }
+        if (big_mi) return run<QUANT, 6, 2, false, 3, 4>(s, g);
+        return run<QUANT, 4, 2, false, 3, 4>(s, g);
     } else {
-        if (tiles(128, 64) >= 160) return run<QUANT, 128, 64, true, 4, 4>(s, g);
-        if (tiles(128, 32) >= 160) return run<QUANT, 128, 32, true, 4, 4>(s, g);
-        return run<QUANT, 64, 32, true, 4, 4>(s, g);
+        if (N >= 8192) return run<QUANT, 8, 4, true, 3, 4>(s, g);
+        if (big_mi || K >= 1024) return run<QUANT, 6, 2, true, 3, 4>(s, g);
+        if (M <= 512) return run<QUANT, 2, 2, true, 3, 4>(s, g);
+        return run<QUANT, 4, 2, true, 3, 4>(s, g);
     }
 }
 
@@ -439,8 +390,8 @@ static void check(const half_t* x, int64_t ldx, const DevWeight& w, int64_t ldy,
     if (w.dtype != F16_DT && (!w.scales || w.sld < (w.cols / 32 + 1) / 2 * 2))
         fail(E_INVALID, "gemm: quantized weight without padded scales");
     // Buffer offsets are 32-bit.
-    if (m * ldx * 2 > 0x7fffffffLL || w.rows * w.cols * 2 > 0x7fffffffLL)
-        fail(E_INVALID, "gemm: operand larger than 2 GiB");
+    if (m * ldx * 2 >= 0x7fff0000LL || w.rows * w.cols * 2 >= 0x7fff0000LL)
+        fail(E_INVALID, "gemm: operand of 2 GiB or more");
 }
 
 void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,

@@ -35,18 +35,29 @@ __device__ inline float half_bits_to_f32(uint16_t h) {
 
 __device__ inline half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
+// (a & mask) | bits in one instruction (gfx9 VOP3 encodings take no
+// literal and one scalar operand: the mask sits in a VGPR, the bits in an
+// SGPR).
+__device__ inline uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "s"(bits));
+    return r;
+}
+
 // One Q4 device word (elements 8w..8w+7, see kernels.h) as eight f16 values
-// (q - 8) * d.  1024 + q is built exactly as an f16 by or-ing the nibble
-// into the mantissa of 1024.0 (0x6400); subtracting 1032 leaves q - 8
-// exactly, so the only rounding is the product with d, as in the
-// reference's f16 decode (shaders/weight.wgsl:50-54).
+// (q - 8) * d.  Each nibble pair is or-ed into the mantissa of an f16 whose
+// mantissa step at the nibble's position is 1: nibbles at bits 0-3 under
+// 1024.0 (0x6400), nibbles at bits 4-7 under 64.0 (0x5400); the upper two
+// pairs take one shift by 8 first.  base + q is exact and subtracting
+// base + 8 leaves q - 8 exactly; the only rounding is the product with d,
+// as in the reference's f16 decode (shaders/weight.wgsl:50-54).
 __device__ inline half8 dq4_word(uint32_t w, half2v dd) {
-    const uint32_t m = 0x000F000Fu, magic = 0x64006400u;
-    const half2v off = {half_t(1032.0f), half_t(1032.0f)};
-    const half2v h0 = (as_half2((w & m) | magic) - off) * dd;
-    const half2v h1 = (as_half2(((w >> 4) & m) | magic) - off) * dd;
-    const half2v h2 = (as_half2(((w >> 8) & m) | magic) - off) * dd;
-    const half2v h3 = (as_half2(((w >> 12) & m) | magic) - off) * dd;
+    const half2v o0 = {half_t(1032.0f), half_t(1032.0f)}, o1 = {half_t(72.0f), half_t(72.0f)};
+    const uint32_t u = w >> 8;
+    const half2v h0 = (as_half2(and_or(w, 0x000F000Fu, 0x64006400u)) - o0) * dd;
+    const half2v h1 = (as_half2(and_or(w, 0x00F000F0u, 0x54005400u)) - o1) * dd;
+    const half2v h2 = (as_half2(and_or(u, 0x000F000Fu, 0x64006400u)) - o0) * dd;
+    const half2v h3 = (as_half2(and_or(u, 0x00F000F0u, 0x54005400u)) - o1) * dd;
     return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
 }
 

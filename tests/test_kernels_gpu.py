@@ -39,7 +39,8 @@ def dev(a: np.ndarray):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m,n,k", [(23, 96, 64), (130, 200, 96), (64, 128, 32), (1, 640, 2048),
-                                   (384, 1536, 640), (2384, 640, 2048), (257, 1152, 1152)])
+                                   (384, 1536, 640), (2384, 640, 2048), (257, 1152, 1152),
+                                   (600, 1536, 4096), (1000, 640, 4128)])
 def test_gemm_matches_cpu(m, n, k, dtype):
     rng = np.random.default_rng(m * n * k + dtype)
     x = (rng.uniform(-1, 1, (m, k)) * 4).astype(np.float16)
@@ -56,7 +57,8 @@ def test_gemm_matches_cpu(m, n, k, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("m,n,k", [(23, 96, 64), (70, 100, 160), (384, 2048, 640), (2384, 2048, 640)])
+@pytest.mark.parametrize("m,n,k", [(23, 96, 64), (70, 100, 160), (384, 2048, 640), (2384, 2048, 640),
+                                   (600, 256, 1184), (130, 8192, 96)])
 def test_gated_matches_cpu(m, n, k, dtype):
     rng = np.random.default_rng(7 * m * n * k + dtype)
     x = rng.uniform(-1, 1, (m, k)).astype(np.float16)
