@@ -75,42 +75,26 @@ struct AttnSmem {
 };
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
-typedef __attribute__((address_space(1))) void* global_void_ptr;
 
-// Issue this wave's share of one K/V tile as direct global -> LDS loads
-// (global_load_lds_dwordx4: lane i of an instruction writes 16 bytes at LDS
-// base + 16 i).  Every lane picks the global chunk that belongs at its LDS
-// slot, which is how the swizzle is applied.  Wave 0 also brings the keys'
-// metadata (rows past the cache's valid range read as never visible).
-template <int HD>
-__device__ __attribute__((always_inline)) inline void dma_tile(AttnSmem<HD>& sm, int buf, const half_t* kt,
-                                                               const half_t* vt, const int4* meta, int wave,
-                                                               int lane) {
-    constexpr int KROW = HD / 8;                     // 16 B chunks per K row
-    constexpr int KINS = A_KT * HD / 8 / WAVE / A_NW;   // instructions per wave for K
-    constexpr int VINS = HD * A_KT / 8 / WAVE / A_NW;
-#pragma unroll
-    for (int i = 0; i < KINS; ++i) {
-        const int blk = wave * KINS + i;            // 1 KB block of the tile
-        const int slot = blk * WAVE + lane;         // physical chunk index in the tile
-        const int row = slot / KROW, pc = slot % KROW;
-        const int lc = pc ^ (row & 15);
-        __builtin_amdgcn_global_load_lds((global_void_ptr)(kt + row * HD + lc * 8),
-                                         (lds_void_ptr)(sm.k[buf] + blk * WAVE * 8), 16, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < VINS; ++i) {
-        const int blk = wave * VINS + i;
-        const int slot = blk * WAVE + lane;
-        const int row = slot / (A_KT / 8), pc = slot % (A_KT / 8);
-        const int lc = pc ^ vt_swz(row);
-        __builtin_amdgcn_global_load_lds((global_void_ptr)(vt + row * 64 + lc * 8),
-                                         (lds_void_ptr)(sm.v[buf] + blk * WAVE * 8), 16, 0, 0);
-    }
-    if (wave == 0)
-        __builtin_amdgcn_global_load_lds((global_void_ptr)(meta + (lane % A_KT)), (lds_void_ptr)(sm.kmeta[buf]), 16, 0,
-                                         0);
+constexpr int RSRC_RAW = 0x00020000;  // raw (untyped) 32-bit buffer
+
+__device__ inline __amdgpu_buffer_rsrc_t attn_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7fffffff ? 0x7fffffff : int(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, RSRC_RAW);
 }
+
+// Geometry of one K/V tile's DMA: buffer loads to LDS (lane i of an
+// instruction writes 16 bytes at LDS base + 16 i) where every lane picks
+// the global chunk that belongs at its LDS slot, which is how the swizzle
+// is applied.  The lane offsets are the same for every tile (the compiler
+// keeps them out of the loop); the tile's position rides in the scalar
+// offset.
+template <int HD>
+struct TileDma {
+    static constexpr int KROW = HD / 8;                       // 16 B chunks per K row
+    static constexpr int KINS = A_KT * HD / 8 / WAVE / A_NW;  // instructions per wave for K
+    static constexpr int VINS = HD * A_KT / 8 / WAVE / A_NW;
+};
 
 // One work item per workgroup: A_ROWS query rows (TPW tokens x HPG heads
 // per wave, A_NW waves) against key tiles [tb, te) of the KV head
@@ -139,6 +123,43 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     const bool valid = tq < a.t;
     const int4* meta = reinterpret_cast<const int4*>(a.meta);
 
+    const half_t* kbase = a.kc + int64_t(g) * a.cap_pad * HD;
+    const half_t* vbase = a.vt + int64_t(g) * (a.cap_pad / 64) * HD * 64;
+    using TD = TileDma<HD>;
+    const int64_t cache_bytes = a.cap_pad * HD * 2;
+    // Issue this wave's share of key tile `tile` into buffer `buf`; wave 0
+    // also brings the keys' metadata (rows past the cache's valid range
+    // read as never visible).
+    auto issue = [&](int tile, int buf) {
+        const int k0 = tile * A_KT;
+#pragma unroll
+        for (int i = 0; i < TD::KINS; ++i) {
+            const int slot = (wave * TD::KINS + i) * WAVE + lane;  // physical chunk index in the tile
+            const int row = slot / TD::KROW, pc = slot % TD::KROW;
+            const uint32_t o = uint32_t((row * HD + (pc ^ (row & 15)) * 8) * 2);
+            const __amdgpu_buffer_rsrc_t r = attn_rsrc(kbase, cache_bytes);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(sm.k[buf] + (wave * TD::KINS + i) * WAVE * 8),
+                                                     16, o, k0 * HD * 2, 0, 0);
+        }
+        const int vtile = (k0 / 64) * HD * 64 + k0 % 64;  // first element of the tile's V^T columns
+#pragma unroll
+        for (int i = 0; i < TD::VINS; ++i) {
+            const int slot = (wave * TD::VINS + i) * WAVE + lane;
+            const int row = slot / (A_KT / 8), pc = slot % (A_KT / 8);
+            const uint32_t o = uint32_t((row * 64 + (pc ^ vt_swz(row)) * 8) * 2);
+            const __amdgpu_buffer_rsrc_t r = attn_rsrc(vbase, cache_bytes);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(sm.v[buf] + (wave * TD::VINS + i) * WAVE * 8),
+                                                     16, o, vtile * 2, 0, 0);
+        }
+        if (wave == 0) {
+            const __amdgpu_buffer_rsrc_t r = attn_rsrc(meta, a.cap_pad * 16);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(sm.kmeta[buf]), 16,
+                                                     uint32_t((lane % A_KT) * 16), k0 * 16, 0, 0);
+        }
+    };
+    // The first tile goes out before the query loads.
+    if (tb < te) issue(tb, 0);
+
     // Positions and sequence ids of the wave's tokens, wave-uniform.
     int qpos[TPW], qseq[TPW];
 #pragma unroll
@@ -158,13 +179,6 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     for (int c = 0; c < CT; ++c) o[c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const half_t* kbase = a.kc + int64_t(g) * a.cap_pad * HD;
-    const half_t* vbase = a.vt + int64_t(g) * (a.cap_pad / 64) * HD * 64;
-    auto issue = [&](int tile, int buf) {
-        const int64_t k0 = int64_t(tile) * A_KT;  // first key (cache row) of the tile
-        dma_tile<HD>(sm, buf, kbase + k0 * HD, vbase + (k0 / 64) * HD * 64 + k0 % 64, meta + k0, wave, lane);
-    };
-    if (tb < te) issue(tb, 0);
     for (int tile = tb; tile < te; ++tile) {
         const int cur = (tile - tb) & 1;
         // This wave's loads of `tile` are the only ones outstanding.
@@ -231,11 +245,17 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         }
         mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
         mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-        const float m_new = fmaxf(m_run, mt);
-        // A row that has seen nothing yet keeps m = -inf; exponents are
-        // taken against 0 then, which gives exactly 0 for every -inf score.
+        // Lazy rescaling: the running max moves only when the tile's max
+        // exceeds it by more than TAU (log2 units), so most tiles skip the
+        // rescale of O; probabilities then reach at most 2^TAU, which f16
+        // holds with the same relative precision.  A row that has seen
+        // nothing yet keeps m = -inf; exponents are taken against 0 then,
+        // which gives exactly 0 for every -inf score.
+        constexpr float TAU = 8.0f;
+        const bool grow = mt > m_run + TAU;
+        const float m_new = grow ? mt : m_run;
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
         half8 pb[A_TT];
         float psum = 0.0f;
 #pragma unroll
@@ -254,7 +274,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         }
         l_run = l_run * alpha + psum;
         m_run = m_new;
-        if (__ballot(alpha != 1.0f) != 0ull) {
+        if (__ballot(grow) != 0ull) {
 #pragma unroll
             for (int c = 0; c < CT; ++c) o[c] *= alpha;
         }
@@ -302,12 +322,13 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 // the chunks the row saw anything in.  A row with one such chunk gets
 // exactly O / l, as if its tile had not been split.  One wave per row (four
 // rows per workgroup); lane l owns columns 4l .. 4l + 3, so every partial
-// row is one contiguous 1 KB wave load, and the loads of all chunks are in
-// flight together.
+// row is one contiguous 1 KB wave load.  The statistics and partial rows of
+// up to MAXC chunks are loaded together (one round trip after the merge
+// record), the max taken from the loaded statistics.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const int4* __restrict__ merges) {
     static_assert(HD == 4 * WAVE, "one float4 column per lane");
-    constexpr int MAXC = 16;  // chunks merged per pass over the partials
+    constexpr int MAXC = 8;  // chunks loaded per round
     const int4 mg = merges[blockIdx.x / (A_ROWS / 4)];
     const int qtile = mg.x, slot0 = mg.y, n = mg.z;
     const int g = int(blockIdx.y);
@@ -318,10 +339,10 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
     if (tq >= a.t) return;
     const int head = g * hpg + (row % 16) % hpg;
     auto base = [&](int c) { return (int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row; };
-    float M = -INFINITY;
-    for (int c = 0; c < n; ++c) M = fmaxf(M, a.part_ml[base(c) * 2]);
+    // Running merge over rounds of MAXC chunks (one round for n <= MAXC):
+    // (M, L, acc) rescaled when a later round raises the max.
+    float M = -INFINITY, L = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float L = 0.0f;
     for (int c0 = 0; c0 < n; c0 += MAXC) {
         float4 v[MAXC];
         float2 ml[MAXC];
@@ -330,11 +351,24 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
             if (c0 + c < n) {
                 ml[c] = *reinterpret_cast<const float2*>(a.part_ml + base(c0 + c) * 2);
                 v[c] = *reinterpret_cast<const float4*>(a.part_o + base(c0 + c) * HD + lane * 4);
+            } else {
+                ml[c] = make_float2(-INFINITY, 0.0f);
             }
         }
+        float Mr = M;
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) Mr = fmaxf(Mr, ml[c].x);
+        if (Mr == -INFINITY) continue;
+        const float r = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mr);
+        L *= r;
+        acc.x *= r;
+        acc.y *= r;
+        acc.z *= r;
+        acc.w *= r;
+        M = Mr;
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
-            if (c0 + c >= n || ml[c].x == -INFINITY) continue;
+            if (ml[c].x == -INFINITY) continue;
             const float w = __builtin_amdgcn_exp2f(ml[c].x - M);
             L += ml[c].y * w;
             acc.x += v[c].x * w;
