@@ -4,9 +4,10 @@
 // query's position and, on sliding layers, less than `window` positions
 // back (attention.wgsl:70-76).  Online softmax in f32, flash style.
 //
-// Work split: a work item is one query tile (64 rows = (64 / hpg) tokens x
-// the hpg query heads sharing one KV head, 16 rows per wave) and a range of
-// 32-key tiles; the host builds the item lists from the pass's metadata
+// Work split: a work item is one query tile (A_ROWS rows = A_ROWS / hpg
+// tokens x the hpg query heads sharing one KV head; each wave holds A_QB
+// blocks of 16 rows, and every K / V fragment read from LDS feeds the
+// MFMAs of all of them) and a range of 32-key tiles; the host builds the item lists from the pass's metadata
 // (AttnWork).  A tile's key range is cut at fixed multiples of `chunk`
 // tiles (sliding layers: 256 keys; global layers: 512 keys or more) and the
 // per-chunk partial results are merged in key order by attention_merge.
@@ -16,7 +17,8 @@
 // are bit-equal to a full pass.
 //
 // Per item: K and V^T tiles are double-buffered in LDS, loaded by LDS DMA
-// one tile ahead; one barrier per tile.  A wave that sees no key of a tile
+// one tile ahead (issued once the current tile's fragments are in
+// registers); one barrier per tile.  A wave that sees no key of a tile
 // skips it; a wave that sees every key of it skips the masking.  Masks are
 // per-token 64-bit ballots over the tile's keys.
 //
@@ -38,12 +40,15 @@
 
 namespace omg {
 
-// Geometry: A_KT keys per K/V tile, A_NW waves of 16 query rows per work
-// item.
+// Geometry: A_KT keys per K/V tile, A_NW waves of A_QB 16-row query blocks
+// per work item.
 constexpr int A_KT = 32;
 constexpr int A_NW = 4;
+// One block per wave measured faster than two on MI355X (two need about 270
+// registers per lane: one wave per SIMD).
+constexpr int A_QB = 1;  // 16-row query blocks per wave
 constexpr int A_THREADS = A_NW * 64;
-constexpr int A_ROWS = A_NW * 16;  // query rows per tile
+constexpr int A_ROWS = A_NW * 16 * A_QB;  // query rows per work item
 constexpr int A_KB = A_KT / 16;    // 16-key MFMA blocks per tile
 constexpr int A_TT = A_KT / 32;    // 32-key MFMA steps of the O product per tile
 static_assert(A_KT == 32 || A_KT == 64, "key tile");
@@ -66,12 +71,10 @@ __device__ inline bool visible(int qp, int qs, int kp, int ks, int window) {
 // (16 lanes on 16 consecutive rows at one logical chunk) hit distinct banks:
 //   K   [64 keys][HD]:  physical chunk = logical ^ (row & 15)  (32-chunk rows)
 //   V^T [HD][A_KT keys]:  physical chunk = logical ^ vt_swz(row)
-// The key metadata (cache rows' int4 meta) of each tile comes along.
 template <int HD>
 struct AttnSmem {
     half_t k[2][A_KT * HD];
     half_t v[2][HD * A_KT];
-    int4 kmeta[2][64];  // A_KT keys (repeated to 64 rows)
 };
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
@@ -97,14 +100,15 @@ struct TileDma {
 };
 
 // One work item per workgroup: A_ROWS query rows (TPW tokens x HPG heads
-// per wave, A_NW waves) against key tiles [tb, te) of the KV head
-// blockIdx.y.
+// per wave in QB blocks of 16 rows, A_NW waves) against key tiles [tb, te)
+// of the KV head blockIdx.y.
 template <int HD, int HPG>
 __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const int4* __restrict__ items) {
     using SM = AttnSmem<HD>;
     constexpr int DS = HD / 32;  // MFMA steps over the head dim
     constexpr int CT = HD / 16;  // 16-wide output column tiles
-    constexpr int TPW = 16 / HPG, TPB = A_NW * TPW;
+    constexpr int QB = A_QB, TPQ = 16 / HPG;  // tokens per 16-row block
+    constexpr int TPW = QB * TPQ, TPB = A_NW * TPW;
     constexpr float LOG2E = 1.4426950408889634f;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     SM& sm = *reinterpret_cast<SM*>(smem_raw);
@@ -117,19 +121,15 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     const int g = int(blockIdx.y);
     const int64_t tok0 = int64_t(qtile) * TPB + wave * TPW;
     const int lr = lane % 16, G = lane / 16;
-    const int u_lane = lr / HPG;  // the lane's token within the wave
-    const int64_t tq = tok0 + u_lane;
+    const int u_lane = lr / HPG;  // the lane's token within each block
     const int head = g * HPG + lr % HPG;
-    const bool valid = tq < a.t;
     const int4* meta = reinterpret_cast<const int4*>(a.meta);
 
     const half_t* kbase = a.kc + int64_t(g) * a.cap_pad * HD;
     const half_t* vbase = a.vt + int64_t(g) * (a.cap_pad / 64) * HD * 64;
     using TD = TileDma<HD>;
     const int64_t cache_bytes = a.cap_pad * HD * 2;
-    // Issue this wave's share of key tile `tile` into buffer `buf`; wave 0
-    // also brings the keys' metadata (rows past the cache's valid range
-    // read as never visible).
+    // Issue this wave's share of key tile `tile` into buffer `buf`.
     auto issue = [&](int tile, int buf) {
         const int k0 = tile * A_KT;
 #pragma unroll
@@ -151,14 +151,15 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(sm.v[buf] + (wave * TD::VINS + i) * WAVE * 8),
                                                      16, o, vtile * 2, 0, 0);
         }
-        if (wave == 0) {
-            const __amdgpu_buffer_rsrc_t r = attn_rsrc(meta, a.cap_pad * 16);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(sm.kmeta[buf]), 16,
-                                                     uint32_t((lane % A_KT) * 16), k0 * 16, 0, 0);
-        }
     };
-    // The first tile goes out before the query loads.
-    if (tb < te) issue(tb, 0);
+    // The first tile goes out before the query loads.  Key metadata (one
+    // key per lane) travels in registers one tile ahead; rows past the
+    // cache's valid range read as never visible.
+    int4 km_next = make_int4(0, 0, 0, 0);
+    if (tb < te) {
+        issue(tb, 0);
+        km_next = meta[tb * A_KT + lane % A_KT];
+    }
 
     // Positions and sequence ids of the wave's tokens, wave-uniform.
     int qpos[TPW], qseq[TPW];
@@ -170,14 +171,27 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         qseq[u] = __builtin_amdgcn_readfirstlane(m.y);
     }
 
-    half8 qf[DS];
+    // Block b holds tokens tok0 + b * TPQ .. (lane: token tok0 + b * TPQ + u_lane).
+    half8 qf[QB][DS];
 #pragma unroll
-    for (int s = 0; s < DS; ++s)
-        qf[s] = valid ? *reinterpret_cast<const half8*>(a.q16 + (tq * H + head) * HD + s * 32 + G * 8) : half8{};
-    floatx4 o[CT];
+    for (int b = 0; b < QB; ++b) {
+        const int64_t tq = tok0 + b * TPQ + u_lane;
 #pragma unroll
-    for (int c = 0; c < CT; ++c) o[c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = -INFINITY, l_run = 0.0f;
+        for (int s = 0; s < DS; ++s)
+            qf[b][s] = tq < a.t ? *reinterpret_cast<const half8*>(a.q16 + (tq * H + head) * HD + s * 32 + G * 8)
+                                : half8{};
+    }
+    floatx4 o[QB][CT];
+#pragma unroll
+    for (int b = 0; b < QB; ++b)
+#pragma unroll
+        for (int c = 0; c < CT; ++c) o[b][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run[QB], l_run[QB];
+#pragma unroll
+    for (int b = 0; b < QB; ++b) {
+        m_run[b] = -INFINITY;
+        l_run[b] = 0.0f;
+    }
 
     for (int tile = tb; tile < te; ++tile) {
         const int cur = (tile - tb) & 1;
@@ -186,12 +200,31 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         // Every wave's part of `tile` has landed, and every wave is done
         // with the other buffer (tile - 1), which the next loads overwrite.
         __syncthreads();
-        if (tile + 1 < te) issue(tile + 1, cur ^ 1);
+        // The keys' metadata of this tile arrived in registers with the
+        // previous tile; the next tile's K / V and metadata go out now.
+        const int4 km = km_next;
+        if (tile + 1 < te) {
+            issue(tile + 1, cur ^ 1);
+            km_next = meta[(tile + 1) * A_KT + lane % A_KT];
+        }
+
+        // All of the tile's K fragments are read at once (their LDS latency
+        // hides behind the mask ballots), then the QK products run with the
+        // accumulation chains interleaved.
+        const half_t* K = sm.k[cur];
+        half8 kf[A_KB][DS];
+#pragma unroll
+        for (int j = 0; j < A_KB; ++j)
+#pragma unroll
+            for (int s = 0; s < DS; ++s) {
+                const int pc = (s * 4 + G) ^ lr;  // row & 15 == lr
+                kf[j][s] = *reinterpret_cast<const half8*>(K + (j * 16 + lr) * HD + pc * 8);
+            }
+        __builtin_amdgcn_sched_barrier(0);
 
         // Which keys of the tile each of the wave's tokens sees: lane = key.
         // Rows at or past the pass's end are never visible (their stale
         // metadata may look valid).
-        const int4 km = sm.kmeta[cur][lane];
         const bool key_ok = int64_t(tile) * A_KT + (lane % A_KT) < a.base + a.t;
         constexpr uint64_t KEYS = A_KT == 64 ? ~0ull : 0xffffffffull;
         uint64_t vis[TPW];
@@ -205,114 +238,139 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         if (any == 0ull) continue;
         const bool full = all == KEYS;
 
-        const half_t* K = sm.k[cur];
-        floatx4 sacc[A_KB];
+        // S^T blocks: every K fragment feeds the MFMAs of all QB blocks.
+        floatx4 sacc[QB][A_KB];
 #pragma unroll
-        for (int j = 0; j < A_KB; ++j) {
-            sacc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < QB; ++b)
 #pragma unroll
-            for (int s = 0; s < DS; ++s) {
-                const int pc = (s * 4 + G) ^ lr;  // row & 15 == lr
-                const half8 kf = *reinterpret_cast<const half8*>(K + (j * 16 + lr) * HD + pc * 8);
-                sacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sacc[j], 0, 0, 0);
-            }
-        }
-        float mt = -INFINITY;
-        if (full) {
+            for (int j = 0; j < A_KB; ++j) sacc[b][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < DS; ++s)
 #pragma unroll
             for (int j = 0; j < A_KB; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    sacc[j][r] *= LOG2E;
-                    mt = fmaxf(mt, sacc[j][r]);
-                }
-        } else {
-            // The lane's 16 keys are bits 16j + 4G + r of its token's mask.
-            uint64_t mk = vis[0];
-#pragma unroll
-            for (int u = 1; u < TPW; ++u) mk = u_lane == u ? vis[u] : mk;
-            uint32_t bits = 0;
-#pragma unroll
-            for (int j = 0; j < A_KB; ++j) bits |= uint32_t((mk >> (16 * j + 4 * G)) & 0xfu) << (4 * j);
-#pragma unroll
-            for (int j = 0; j < A_KB; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float sv = (bits >> (4 * j + r)) & 1u ? sacc[j][r] * LOG2E : -INFINITY;
-                    sacc[j][r] = sv;
-                    mt = fmaxf(mt, sv);
-                }
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-        // Lazy rescaling: the running max moves only when the tile's max
-        // exceeds it by more than TAU (log2 units), so most tiles skip the
-        // rescale of O; probabilities then reach at most 2^TAU, which f16
-        // holds with the same relative precision.  A row that has seen
-        // nothing yet keeps m = -inf; exponents are taken against 0 then,
-        // which gives exactly 0 for every -inf score.
-        constexpr float TAU = 8.0f;
-        const bool grow = mt > m_run + TAU;
-        const float m_new = grow ? mt : m_run;
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
-        half8 pb[A_TT];
-        float psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < A_KB; ++j) {
-            half2v pr[2];
-#pragma unroll
-            for (int r = 0; r < 4; r += 2) {
-                pr[r / 2] = half2v{half_t(__builtin_amdgcn_exp2f(sacc[j][r] - m_use)),
-                                   half_t(__builtin_amdgcn_exp2f(sacc[j][r + 1] - m_use))};
-                psum = __builtin_amdgcn_fdot2(pr[r / 2], half2v{half_t(1.0f), half_t(1.0f)}, psum, false);
-            }
-            pb[j / 2][(j % 2) * 4 + 0] = pr[0].x;
-            pb[j / 2][(j % 2) * 4 + 1] = pr[0].y;
-            pb[j / 2][(j % 2) * 4 + 2] = pr[1].x;
-            pb[j / 2][(j % 2) * 4 + 3] = pr[1].y;
-        }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (__ballot(grow) != 0ull) {
-#pragma unroll
-            for (int c = 0; c < CT; ++c) o[c] *= alpha;
-        }
+                for (int b = 0; b < QB; ++b)
+                    sacc[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][s], qf[b][s], sacc[b][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // The V^T fragments go out before the softmax, whose arithmetic then
+        // hides their latency.
         const half_t* V = sm.v[cur];
+        half8 vf[A_TT][CT];
 #pragma unroll
-        for (int tt = 0; tt < A_TT; ++tt) {
+        for (int tt = 0; tt < A_TT; ++tt)
 #pragma unroll
             for (int c = 0; c < CT; ++c) {
                 const int row = c * 16 + lr;
-                const half8 vf = *reinterpret_cast<const half8*>(V + row * A_KT + (((tt * 4 + G) ^ vt_swz(row)) * 8));
-                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[tt], o[c], 0, 0, 0);
+                vf[tt][c] = *reinterpret_cast<const half8*>(V + row * A_KT + (((tt * 4 + G) ^ vt_swz(row)) * 8));
             }
+        __builtin_amdgcn_sched_barrier(0);
+
+        half8 pb[QB][A_TT];
+        bool any_grow = false;
+        float alpha[QB];
+#pragma unroll
+        for (int b = 0; b < QB; ++b) {
+            float mt = -INFINITY;
+            if (full) {
+#pragma unroll
+                for (int j = 0; j < A_KB; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        sacc[b][j][r] *= LOG2E;
+                        mt = fmaxf(mt, sacc[b][j][r]);
+                    }
+            } else {
+                // The lane's 16 keys are bits 16j + 4G + r of its token's mask.
+                uint64_t mk = vis[b * TPQ];
+#pragma unroll
+                for (int u = 1; u < TPQ; ++u) mk = u_lane == u ? vis[b * TPQ + u] : mk;
+                uint32_t bits = 0;
+#pragma unroll
+                for (int j = 0; j < A_KB; ++j) bits |= uint32_t((mk >> (16 * j + 4 * G)) & 0xfu) << (4 * j);
+#pragma unroll
+                for (int j = 0; j < A_KB; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float sv = (bits >> (4 * j + r)) & 1u ? sacc[b][j][r] * LOG2E : -INFINITY;
+                        sacc[b][j][r] = sv;
+                        mt = fmaxf(mt, sv);
+                    }
+            }
+            mt = max_lanes_16_32(mt);
+            // Lazy rescaling: the running max moves only when the tile's max
+            // exceeds it by more than TAU (log2 units), so most tiles skip
+            // the rescale of O; probabilities then reach at most 2^TAU, which
+            // f16 holds with the same relative precision.  A row that has
+            // seen nothing yet keeps m = -inf; exponents are taken against 0
+            // then, which gives exactly 0 for every -inf score.
+            constexpr float TAU = 8.0f;
+            const bool grow = mt > m_run[b] + TAU;
+            const float m_new = grow ? mt : m_run[b];
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            alpha[b] = grow ? __builtin_amdgcn_exp2f(m_run[b] - m_use) : 1.0f;
+            any_grow = any_grow || grow;
+            float psum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < A_KB; ++j) {
+                half2v pr[2];
+#pragma unroll
+                for (int r = 0; r < 4; r += 2) {
+                    pr[r / 2] = half2v{half_t(__builtin_amdgcn_exp2f(sacc[b][j][r] - m_use)),
+                                       half_t(__builtin_amdgcn_exp2f(sacc[b][j][r + 1] - m_use))};
+                    psum = __builtin_amdgcn_fdot2(pr[r / 2], half2v{half_t(1.0f), half_t(1.0f)}, psum, false);
+                }
+                pb[b][j / 2][(j % 2) * 4 + 0] = pr[0].x;
+                pb[b][j / 2][(j % 2) * 4 + 1] = pr[0].y;
+                pb[b][j / 2][(j % 2) * 4 + 2] = pr[1].x;
+                pb[b][j / 2][(j % 2) * 4 + 3] = pr[1].y;
+            }
+            l_run[b] = l_run[b] * alpha[b] + psum;
+            m_run[b] = m_new;
         }
+        if (__ballot(any_grow) != 0ull) {
+#pragma unroll
+            for (int b = 0; b < QB; ++b)
+#pragma unroll
+                for (int c = 0; c < CT; ++c) o[b][c] *= alpha[b];
+        }
+        // O^T blocks: every V^T fragment feeds the MFMAs of all QB blocks.
+#pragma unroll
+        for (int tt = 0; tt < A_TT; ++tt)
+#pragma unroll
+            for (int c = 0; c < CT; ++c)
+#pragma unroll
+                for (int b = 0; b < QB; ++b)
+                    o[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[tt][c], pb[b][tt], o[b][c], 0, 0, 0);
     }
 
-    float l = l_run + __shfl_xor(l_run, 16, WAVE);
-    l += __shfl_xor(l, 32, WAVE);
-    const int row = wave * 16 + lr;
-    if (slot >= 0) {
-        // Partial result of this chunk: unnormalised O (f32), max and sum.
-        const int64_t prow = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row;
-        float* op = a.part_o + prow * HD + G * 4;
 #pragma unroll
-        for (int c = 0; c < CT; ++c) *reinterpret_cast<floatx4*>(op + c * 16) = o[c];
-        if (G == 0) {
-            a.part_ml[prow * 2] = m_run;
-            a.part_ml[prow * 2 + 1] = l;
+    for (int b = 0; b < QB; ++b) {
+        float l = l_run[b] + __shfl_xor(l_run[b], 16, WAVE);
+        l += __shfl_xor(l, 32, WAVE);
+        const int row = (wave * QB + b) * 16 + lr;
+        if (slot >= 0) {
+            // Partial result of this chunk: unnormalised O (f32), max and sum.
+            const int64_t prow = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row;
+            float* op = a.part_o + prow * HD + G * 4;
+#pragma unroll
+            for (int c = 0; c < CT; ++c) *reinterpret_cast<floatx4*>(op + c * 16) = o[b][c];
+            if (G == 0) {
+                a.part_ml[prow * 2] = m_run[b];
+                a.part_ml[prow * 2 + 1] = l;
+            }
+            continue;
         }
-        return;
-    }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    if (valid) {
-        half_t* dst = a.out + (tq * H + head) * HD + G * 4;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        const int64_t tq = tok0 + b * TPQ + u_lane;
+        if (tq < a.t) {
+            half_t* dst = a.out + (tq * H + head) * HD + G * 4;
 #pragma unroll
-        for (int c = 0; c < CT; ++c) {
-            const half4 v = {half_t(o[c][0] * inv), half_t(o[c][1] * inv), half_t(o[c][2] * inv),
-                             half_t(o[c][3] * inv)};
-            *reinterpret_cast<half4*>(dst + c * 16) = v;
+            for (int c = 0; c < CT; ++c) {
+                const half4 v = {half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
+                                 half_t(o[b][c][3] * inv)};
+                *reinterpret_cast<half4*>(dst + c * 16) = v;
+            }
         }
     }
 }
@@ -334,8 +392,10 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
     const int g = int(blockIdx.y);
     const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
     const int row = int(blockIdx.x % (A_ROWS / 4)) * 4 + wave;
-    const int hpg = a.heads / a.kv_heads, tpw = 16 / hpg, tpb = A_NW * tpw;
-    const int64_t tq = int64_t(qtile) * tpb + (row / 16) * tpw + (row % 16) / hpg;
+    // Row r of a work item: 16-row block r / 16 (wave-major), 16 / hpg tokens
+    // per block, the lane's token (r % 16) / hpg within it.
+    const int hpg = a.heads / a.kv_heads, tpq = 16 / hpg, tpb = A_NW * A_QB * tpq;
+    const int64_t tq = int64_t(qtile) * tpb + (row / 16) * tpq + (row % 16) / hpg;
     if (tq >= a.t) return;
     const int head = g * hpg + (row % 16) % hpg;
     auto base = [&](int c) { return (int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row; };
@@ -386,7 +446,7 @@ void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int
                     AttnWork& w) {
     w.items.clear();
     w.merges.clear();
-    const int hpg = heads / kv_heads, tpb = A_NW * (16 / hpg);
+    const int hpg = heads / kv_heads, tpb = A_NW * A_QB * (16 / hpg);
     int slot = 0;
     for (int64_t q0 = 0, qt = 0; q0 < t; q0 += tpb, ++qt) {
         int64_t lo = INT64_MAX, hi = 0;

@@ -261,38 +261,52 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
         const uint8_t* X = slot_base(kt);
         const uint8_t* Wr = X + P::X_BYTES;
         const uint8_t* S = Wr + P::W_BYTES;
-        uint32_t sc[NJ];
-        if constexpr (QUANT != F16_DT) {
+        // Every LDS read of the stage goes out first (X fragments, this
+        // wave's codes and scales), so their latencies overlap; then the
+        // decode and the MFMAs.
+        half8 xf[2][MI];
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) sc[j] = *reinterpret_cast<const uint32_t*>(S + (wrow_of(j) + lr) * 4);
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < MI; ++i) xf[ks][i] = *reinterpret_cast<const half8*>(X + i * 16 * G_ROW + foff[ks]);
+        uint32_t sc[NJ];
+        uint2 code[2][NJ];  // Q4: .x only; Q8: both words
+        half8 wf16[2][NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int rw = wrow_of(j) + lr;
+            if constexpr (QUANT != F16_DT) sc[j] = *reinterpret_cast<const uint32_t*>(S + rw * 4);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                if constexpr (QUANT == F16_DT)
+                    wf16[ks][j] = *reinterpret_cast<const half8*>(Wr + wrow_of(j) * G_ROW + foff[ks]);
+                else if constexpr (QUANT == Q4_DT)
+                    code[ks][j].x = *reinterpret_cast<const uint32_t*>(Wr + rw * 32 + ks * 16 + lg * 4);
+                else
+                    code[ks][j] = *reinterpret_cast<const uint2*>(Wr + rw * 64 + ks * 32 + lg * 8);
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            half8 xf[MI], wf[NJ];
-#pragma unroll
-            for (int i = 0; i < MI; ++i) xf[i] = *reinterpret_cast<const half8*>(X + i * 16 * G_ROW + foff[ks]);
+            half8 wf[NJ];
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const int rw = wrow_of(j) + lr;
                 if constexpr (QUANT == F16_DT) {
-                    wf[j] = *reinterpret_cast<const half8*>(Wr + wrow_of(j) * G_ROW + foff[ks]);
+                    wf[j] = wf16[ks][j];
                 } else {
-                    const uint16_t db = uint16_t(sc[j] >> (16 * ks));
-                    const half_t d = __builtin_bit_cast(half_t, db);
-                    if constexpr (QUANT == Q4_DT) {
-                        const uint32_t w = *reinterpret_cast<const uint32_t*>(Wr + rw * 32 + ks * 16 + lg * 4);
-                        wf[j] = dq4_word(w, half2v{d, d});
-                    } else {
-                        const uint2 u = *reinterpret_cast<const uint2*>(Wr + rw * 64 + ks * 32 + lg * 8);
-                        wf[j] = dq8_words(u.x, u.y, half2v{d, d});
-                    }
+                    const half_t d = __builtin_bit_cast(half_t, uint16_t(sc[j] >> (16 * ks)));
+                    if constexpr (QUANT == Q4_DT)
+                        wf[j] = dq4_word(code[ks][j].x, half2v{d, d});
+                    else
+                        wf[j] = dq8_words(code[ks][j].x, code[ks][j].y, half2v{d, d});
                 }
             }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < NJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], xf[i], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j], xf[ks][i], acc[i][j], 0, 0, 0);
         }
     }
     wait_vm<0>();

@@ -29,6 +29,18 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
+// Max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one row of an MFMA
+// 16x16 result) without LDS: v_permlane16_swap / v_permlane32_swap with both
+// operands the same value return the pair {x[l], x[l ^ 16]} (resp. ^ 32).
+__device__ inline float max_lanes_16_32(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float m = fmaxf(__builtin_bit_cast(float, uint32_t(p[0])), __builtin_bit_cast(float, uint32_t(p[1])));
+    const uint32_t w = __builtin_bit_cast(uint32_t, m);
+    const auto q = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return fmaxf(__builtin_bit_cast(float, uint32_t(q[0])), __builtin_bit_cast(float, uint32_t(q[1])));
+}
+
 __device__ inline float half_bits_to_f32(uint16_t h) {
     return float(__builtin_bit_cast(half_t, h));
 }
