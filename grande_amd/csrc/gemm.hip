@@ -365,30 +365,30 @@ static void run(hipStream_t s, const GemmArgs& g) {
 }
 
 // Tile choice, measured on MI355X over the 270M / 1B / 4B decoder shapes
-// (cold passes of 2,384 tokens, warm passes of 384):
-//   short passes (M <= 512): small tiles, many workgroups;
-//   narrow outputs (N <= 1280, the o and down projections): 64 x 64 tiles
-//   with a four-stage ring;
-//   wide outputs: 64 x 128 tiles.
-// Long K (>= 4096) and Q8 codes take 96-row tiles: the decode is spread
-// over more MFMAs.  Gated: 64 x 128 weight rows (64 output columns),
-// 96 rows for long K / Q8, 128 x 256 for very wide layers.
+// (cold passes of 2,384 tokens, warm passes of 384); the MI x (NW * 16 NJ)
+// tiles in the comments are activation rows x weight rows:
+//   short passes (M <= 512): 32 x 64, two waves;
+//   narrow outputs (N <= 1280, the o and down projections): 64 x 64 with a
+//   four-stage ring, 96 x 64 from N = 768, 96 x 128 for long K;
+//   wide outputs (the qkv projection): 128 x 64, 96 x 128 for long K.
+//   Gated: 64 x 128 weight rows (64 output columns), 96 x 256 for K >= 1024,
+//   128 x 256 for very wide layers, 32 x 128 for short passes.
 template <int QUANT, bool GATED>
 static void dispatch(hipStream_t s, const GemmArgs& g) {
     const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
-    const bool big_mi = K >= 4096 || QUANT == Q8_DT;
     if constexpr (!GATED) {
         if (M <= 512) return run<QUANT, 2, 1, false, 4, 2>(s, g);
         if (N <= 1280) {
-            if (big_mi) return run<QUANT, 6, 1, false, 4, 4>(s, g);
+            if (K >= 4096) return run<QUANT, 6, 2, false, 4, 4>(s, g);
+            if (N > 768) return run<QUANT, 6, 1, false, 4, 4>(s, g);
             return run<QUANT, 4, 1, false, 4, 4>(s, g);
         }
-        if (big_mi) return run<QUANT, 6, 2, false, 3, 4>(s, g);
-        return run<QUANT, 4, 2, false, 3, 4>(s, g);
+        if (K >= 4096) return run<QUANT, 6, 2, false, 3, 4>(s, g);
+        return run<QUANT, 8, 1, false, 3, 4>(s, g);
     } else {
-        if (N >= 8192) return run<QUANT, 8, 4, true, 3, 4>(s, g);
-        if (big_mi || K >= 1024) return run<QUANT, 6, 2, true, 3, 4>(s, g);
         if (M <= 512) return run<QUANT, 2, 2, true, 3, 4>(s, g);
+        if (N >= 8192) return run<QUANT, 8, 4, true, 3, 4>(s, g);
+        if (K >= 1024) return run<QUANT, 6, 4, true, 3, 4>(s, g);
         return run<QUANT, 4, 2, true, 3, 4>(s, g);
     }
 }

@@ -40,7 +40,7 @@ def dev(a: np.ndarray):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m,n,k", [(23, 96, 64), (130, 200, 96), (64, 128, 32), (1, 640, 2048),
                                    (384, 1536, 640), (2384, 640, 2048), (257, 1152, 1152),
-                                   (600, 1536, 4096), (1000, 640, 4128)])
+                                   (600, 1536, 4096), (1000, 640, 4128), (700, 1152, 1024), (1100, 1536, 640)])
 def test_gemm_matches_cpu(m, n, k, dtype):
     rng = np.random.default_rng(m * n * k + dtype)
     x = (rng.uniform(-1, 1, (m, k)) * 4).astype(np.float16)
