@@ -349,19 +349,24 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         float l = l_run[b] + __shfl_xor(l_run[b], 16, WAVE);
         l += __shfl_xor(l, 32, WAVE);
         const int row = (wave * QB + b) * 16 + lr;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         if (slot >= 0) {
-            // Partial result of this chunk: unnormalised O (f32), max and sum.
+            // Partial result of this chunk: O / l rounded to f16 exactly as
+            // an unsplit tile's output, and the chunk's max and sum.
             const int64_t prow = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row;
-            float* op = a.part_o + prow * HD + G * 4;
+            half_t* op = a.part_o + prow * HD + G * 4;
 #pragma unroll
-            for (int c = 0; c < CT; ++c) *reinterpret_cast<floatx4*>(op + c * 16) = o[b][c];
+            for (int c = 0; c < CT; ++c) {
+                const half4 v = {half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
+                                 half_t(o[b][c][3] * inv)};
+                *reinterpret_cast<half4*>(op + c * 16) = v;
+            }
             if (G == 0) {
                 a.part_ml[prow * 2] = m_run[b];
                 a.part_ml[prow * 2 + 1] = l;
             }
             continue;
         }
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const int64_t tq = tok0 + b * TPQ + u_lane;
         if (tq < a.t) {
             half_t* dst = a.out + (tq * H + head) * HD + G * 4;
@@ -375,17 +380,18 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     }
 }
 
-// Merge the chunk partials of one query tile in key order:
-// out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), M = max_c m_c, over
-// the chunks the row saw anything in.  A row with one such chunk gets
-// exactly O / l, as if its tile had not been split.  One wave per row (four
-// rows per workgroup); lane l owns columns 4l .. 4l + 3, so every partial
-// row is one contiguous 1 KB wave load.  The statistics and partial rows of
-// up to MAXC chunks are loaded together (one round trip after the merge
-// record), the max taken from the loaded statistics.
+// Merge the chunk partials of one query tile in key order: with O_c the
+// chunk's normalised output (f16), m_c its max and l_c its sum,
+// out = sum_c O_c l_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), M = max_c m_c,
+// over the chunks the row saw anything in.  A row with one such chunk gets
+// that chunk's f16 output unchanged, exactly what an unsplit tile writes.
+// One wave per row (four rows per workgroup); lane l owns columns
+// 4l .. 4l + 3, so every partial row is one contiguous 512-byte wave load.
+// The statistics and partial rows of up to MAXC chunks are loaded together
+// (one round trip after the merge record).
 template <int HD>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const int4* __restrict__ merges) {
-    static_assert(HD == 4 * WAVE, "one float4 column per lane");
+    static_assert(HD == 4 * WAVE, "one half4 column group per lane");
     constexpr int MAXC = 8;  // chunks loaded per round
     const int4 mg = merges[blockIdx.x / (A_ROWS / 4)];
     const int qtile = mg.x, slot0 = mg.y, n = mg.z;
@@ -403,14 +409,16 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
     // (M, L, acc) rescaled when a later round raises the max.
     float M = -INFINITY, L = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int seen = 0;
+    half4 only = {};
     for (int c0 = 0; c0 < n; c0 += MAXC) {
-        float4 v[MAXC];
+        half4 v[MAXC];
         float2 ml[MAXC];
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
             if (c0 + c < n) {
                 ml[c] = *reinterpret_cast<const float2*>(a.part_ml + base(c0 + c) * 2);
-                v[c] = *reinterpret_cast<const float4*>(a.part_o + base(c0 + c) * HD + lane * 4);
+                v[c] = *reinterpret_cast<const half4*>(a.part_o + base(c0 + c) * HD + lane * 4);
             } else {
                 ml[c] = make_float2(-INFINITY, 0.0f);
             }
@@ -429,16 +437,19 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
             if (ml[c].x == -INFINITY) continue;
-            const float w = __builtin_amdgcn_exp2f(ml[c].x - M);
-            L += ml[c].y * w;
-            acc.x += v[c].x * w;
-            acc.y += v[c].y * w;
-            acc.z += v[c].z * w;
-            acc.w += v[c].w * w;
+            ++seen;
+            only = v[c];
+            const float w = ml[c].y * __builtin_amdgcn_exp2f(ml[c].x - M);
+            L += w;
+            acc.x += float(v[c].x) * w;
+            acc.y += float(v[c].y) * w;
+            acc.z += float(v[c].z) * w;
+            acc.w += float(v[c].w) * w;
         }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const half4 o = {half_t(acc.x * inv), half_t(acc.y * inv), half_t(acc.z * inv), half_t(acc.w * inv)};
+    const half4 o = seen == 1 ? only
+                              : half4{half_t(acc.x * inv), half_t(acc.y * inv), half_t(acc.z * inv), half_t(acc.w * inv)};
     *reinterpret_cast<half4*>(a.out + (tq * a.heads + head) * HD + lane * 4) = o;
 }
 

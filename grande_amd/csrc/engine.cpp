@@ -351,7 +351,7 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
             E.attn_merges_[k] = DevBuf(size_t(qtiles) * 16);
         }
         E.part_slots_ = qtiles * 4;
-        E.part_o_ = DevBuf(size_t(E.part_slots_ * c.kv_heads * attention_rows()) * size_t(hd) * 4);
+        E.part_o_ = DevBuf(size_t(E.part_slots_ * c.kv_heads * attention_rows()) * size_t(hd) * 2);
         E.part_ml_ = DevBuf(size_t(E.part_slots_ * c.kv_heads * attention_rows()) * 2 * 4);
         (void)key_tiles;
     }
@@ -518,7 +518,7 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         if (w.slots > part_slots_) {
             part_slots_ = w.slots;
             const size_t rows = size_t(part_slots_ * cfg_.kv_heads * attention_rows());
-            part_o_ = DevBuf(rows * size_t(cfg_.head_dim[0]) * 4);
+            part_o_ = DevBuf(rows * size_t(cfg_.head_dim[0]) * 2);
             part_ml_ = DevBuf(rows * 2 * 4);
         }
         n_items_[kind] = int64_t(w.items.size());
@@ -587,7 +587,7 @@ void Engine::forward(int64_t t, int64_t base) {
         att.kv_heads = int(c.kv_heads);
         att.hd = int(hd);
         att.window = c.sliding[size_t(l)] ? int(c.window) : 0;
-        att.part_o = part_o_.as<float>();
+        att.part_o = part_o_.as<half_t>();
         att.part_ml = part_ml_.as<float>();
         const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
         step("attention", [&] { launch_attention(stream_, att, attn_items_[kind].as<int4>(), n_items_[kind]); });

@@ -98,8 +98,8 @@ struct AttnArgs {
     const half_t* vt;    // [kv_heads][cap_pad/64][hd][64]
     const int32_t* meta; // per cache row
     half_t* out;         // [t][heads][hd]
-    float* part_o;       // chunk partials: [slot][kv_heads][64 rows][hd] unnormalised O
-    float* part_ml;      // [slot][kv_heads][64 rows][2]: running max (log2 units), sum
+    half_t* part_o;      // chunk partials: [slot][kv_heads][rows][hd] O / l (f16)
+    float* part_ml;      // [slot][kv_heads][rows][2]: running max (log2 units), sum
     int64_t t, base, cap_pad;
     int heads, kv_heads, hd;
     int window;          // 0 = global layer
