@@ -108,7 +108,7 @@ struct Cfg {
     static_assert(LDS <= 160 * 1024, "ring larger than the LDS");
     static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
     static_assert(BN % 64 == 0 || !GATED, "a scale DMA instruction must stay in one matrix");
-    static_assert(NS >= 3, "ring needs >= 3 slots");
+    static_assert(NS >= 2, "ring needs >= 2 slots");
     static_assert(C <= 63, "vmcnt range");
 };
 
@@ -365,31 +365,35 @@ static void run(hipStream_t s, const GemmArgs& g) {
 }
 
 // Tile choice, measured on MI355X over the 270M / 1B / 4B decoder shapes
-// (cold passes of 2,384 tokens, warm passes of 384); the MI x (NW * 16 NJ)
-// tiles in the comments are activation rows x weight rows:
-//   short passes (M <= 512): 32 x 64, two waves;
-//   narrow outputs (N <= 1280, the o and down projections): 64 x 64 with a
-//   four-stage ring, 96 x 64 from N = 768, 96 x 128 for long K;
-//   wide outputs (the qkv projection): 128 x 64, 96 x 128 for long K.
-//   Gated: 64 x 128 weight rows (64 output columns), 96 x 256 for K >= 1024,
-//   128 x 256 for very wide layers, 32 x 128 for short passes.
+// (cold passes of 2,384 tokens, warm passes of 384); tiles below are
+// activation rows x weight rows.  A two-slot ring (one stage of DMA in
+// flight, its latency covered by the other workgroups on the CU) fits more
+// workgroups per CU, which wins for the gated and wide launches that would
+// otherwise spill into a second round; the narrow o / down launches keep
+// four slots (between the pass's other kernels their loads wait longer).
+//   short passes (M <= 512): 32 x 64, two waves, four slots;
+//   narrow outputs (N <= 1280, the o and down projections): 64 x 64,
+//   96 x 64 from N = 768, four slots;
+//   wide outputs (the qkv projection): 128 x 64, 96 x 128 for K >= 4096.
+//   Gated: 128 x 128 weight rows (64 output columns), 96 x 256 for Q8
+//   codes (heavier decode), 128 x 256 with three slots for very wide
+//   layers, 64 x 128 for short passes.
 template <int QUANT, bool GATED>
 static void dispatch(hipStream_t s, const GemmArgs& g) {
     const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
     if constexpr (!GATED) {
         if (M <= 512) return run<QUANT, 2, 1, false, 4, 2>(s, g);
         if (N <= 1280) {
-            if (K >= 4096) return run<QUANT, 6, 2, false, 4, 4>(s, g);
             if (N > 768) return run<QUANT, 6, 1, false, 4, 4>(s, g);
             return run<QUANT, 4, 1, false, 4, 4>(s, g);
         }
-        if (K >= 4096) return run<QUANT, 6, 2, false, 3, 4>(s, g);
-        return run<QUANT, 8, 1, false, 3, 4>(s, g);
+        if (K >= 4096) return run<QUANT, 6, 2, false, 2, 4>(s, g);
+        return run<QUANT, 8, 1, false, 2, 4>(s, g);
     } else {
-        if (M <= 512) return run<QUANT, 2, 2, true, 3, 4>(s, g);
+        if (M <= 512) return run<QUANT, 4, 2, true, 2, 4>(s, g);
         if (N >= 8192) return run<QUANT, 8, 4, true, 3, 4>(s, g);
-        if (K >= 1024) return run<QUANT, 6, 4, true, 3, 4>(s, g);
-        return run<QUANT, 4, 2, true, 3, 4>(s, g);
+        if constexpr (QUANT == Q8_DT) return run<QUANT, 6, 4, true, 2, 4>(s, g);
+        return run<QUANT, 8, 2, true, 2, 4>(s, g);
     }
 }
 

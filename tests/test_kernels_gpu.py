@@ -58,7 +58,7 @@ def test_gemm_matches_cpu(m, n, k, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m,n,k", [(23, 96, 64), (70, 100, 160), (384, 2048, 640), (2384, 2048, 640),
-                                   (600, 256, 1184), (130, 8192, 96)])
+                                   (600, 256, 1184), (130, 8192, 96), (600, 8192, 96)])
 def test_gated_matches_cpu(m, n, k, dtype):
     rng = np.random.default_rng(7 * m * n * k + dtype)
     x = rng.uniform(-1, 1, (m, k)).astype(np.float16)
