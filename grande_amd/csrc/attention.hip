@@ -60,11 +60,6 @@ int attention_rows() { return A_ROWS; }
 // spreads 16 consecutive rows over distinct banks.
 __device__ inline int vt_swz(int row) { return A_KT == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
 
-__device__ inline bool visible(int qp, int qs, int kp, int ks, int window) {
-    const bool same_group = ((ks ^ qs) >> 12) == 0;
-    return same_group && ((ks & 0xfff) == 0 || ks == qs) && kp <= qp &&
-           (window == 0 || unsigned(qp - kp) < unsigned(window));
-}
 
 // LDS of one work item.  K and V^T tiles are stored without padding; the
 // 16-byte chunks of each row are XOR-swizzled so that the MFMA operand reads
@@ -225,15 +220,25 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         // Which keys of the tile each of the wave's tokens sees: lane = key.
         // Rows at or past the pass's end are never visible (their stale
         // metadata may look valid).
-        const bool key_ok = int64_t(tile) * A_KT + (lane % A_KT) < a.base + a.t;
+        // Each condition of `visible` is one lane ballot (a vector compare
+        // into a scalar mask); the masks combine in scalar code.
         constexpr uint64_t KEYS = A_KT == 64 ? ~0ull : 0xffffffffull;
+        const uint64_t ok = __ballot(int64_t(tile) * A_KT + (lane % A_KT) < a.base + a.t) & KEYS;
+        const uint64_t prefix_keys = __ballot((km.y & 0xfff) == 0);
+        const int kgroup = km.y >> 12;
+        const unsigned reach = a.window > 0 ? unsigned(a.window) : 0x7fffffffu;
         uint64_t vis[TPW];
         uint64_t any = 0, all = KEYS;
 #pragma unroll
         for (int u = 0; u < TPW; ++u) {
-            vis[u] = __ballot(key_ok && visible(qpos[u], qseq[u], km.x, km.y, a.window)) & KEYS;
-            any |= vis[u];
-            all &= vis[u];
+            // (reach = window, or 2^31 - 1 on global layers: then the test
+            // only repeats kp <= qp)
+            const uint64_t m = ok & __ballot(kgroup == (qseq[u] >> 12)) &
+                               (prefix_keys | __ballot(km.y == qseq[u])) & __ballot(km.x <= qpos[u]) &
+                               __ballot(unsigned(qpos[u] - km.x) < reach);
+            vis[u] = m;
+            any |= m;
+            all &= m;
         }
         if (any == 0ull) continue;
         const bool full = all == KEYS;
@@ -267,19 +272,19 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         __builtin_amdgcn_sched_barrier(0);
 
         half8 pb[QB][A_TT];
-        bool any_grow = false;
+        bool any_rescale = false;
         float alpha[QB];
 #pragma unroll
         for (int b = 0; b < QB; ++b) {
+            // Scores stay in natural units; the max is scaled to log2 units
+            // once (scaling by LOG2E > 0 commutes with the max) and each
+            // exponent is one fma(s, LOG2E, -m).
             float mt = -INFINITY;
             if (full) {
 #pragma unroll
                 for (int j = 0; j < A_KB; ++j)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        sacc[b][j][r] *= LOG2E;
-                        mt = fmaxf(mt, sacc[b][j][r]);
-                    }
+                    for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sacc[b][j][r]);
             } else {
                 // The lane's 16 keys are bits 16j + 4G + r of its token's mask.
                 uint64_t mk = vis[b * TPQ];
@@ -292,12 +297,12 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
                 for (int j = 0; j < A_KB; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float sv = (bits >> (4 * j + r)) & 1u ? sacc[b][j][r] * LOG2E : -INFINITY;
+                        const float sv = (bits >> (4 * j + r)) & 1u ? sacc[b][j][r] : -INFINITY;
                         sacc[b][j][r] = sv;
                         mt = fmaxf(mt, sv);
                     }
             }
-            mt = max_lanes_16_32(mt);
+            mt = max_lanes_16_32(mt) * LOG2E;
             // Lazy rescaling: the running max moves only when the tile's max
             // exceeds it by more than TAU (log2 units), so most tiles skip
             // the rescale of O; probabilities then reach at most 2^TAU, which
@@ -309,15 +314,16 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             const float m_new = grow ? mt : m_run[b];
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             alpha[b] = grow ? __builtin_amdgcn_exp2f(m_run[b] - m_use) : 1.0f;
-            any_grow = any_grow || grow;
+            // A row that had seen nothing still holds O = 0: no rescale.
+            any_rescale = any_rescale || (grow && m_run[b] != -INFINITY);
             float psum = 0.0f;
 #pragma unroll
             for (int j = 0; j < A_KB; ++j) {
                 half2v pr[2];
 #pragma unroll
                 for (int r = 0; r < 4; r += 2) {
-                    pr[r / 2] = half2v{half_t(__builtin_amdgcn_exp2f(sacc[b][j][r] - m_use)),
-                                       half_t(__builtin_amdgcn_exp2f(sacc[b][j][r + 1] - m_use))};
+                    pr[r / 2] = half2v{half_t(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][j][r], LOG2E, -m_use))),
+                                       half_t(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][j][r + 1], LOG2E, -m_use)))};
                     psum = __builtin_amdgcn_fdot2(pr[r / 2], half2v{half_t(1.0f), half_t(1.0f)}, psum, false);
                 }
                 pb[b][j / 2][(j % 2) * 4 + 0] = pr[0].x;
@@ -328,7 +334,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             l_run[b] = l_run[b] * alpha[b] + psum;
             m_run[b] = m_new;
         }
-        if (__ballot(any_grow) != 0ull) {
+        if (__ballot(any_rescale) != 0ull) {
 #pragma unroll
             for (int b = 0; b < QB; ++b)
 #pragma unroll
