@@ -32,6 +32,7 @@
 // keys a lane holds probabilities for are one contiguous 16-byte read.  A
 // lane owns one query row for the softmax statistics and the output, so the
 // running max and sum need only the 4 lanes of that row.
+#include <algorithm>
 #include <climits>
 #include <string>
 
@@ -485,6 +486,12 @@ void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int
         w.merges.push_back({int(qt), first, slot - first, 0});
     }
     w.slots = slot;
+    // Longest items first: the workgroup dispatcher places one workgroup
+    // per CU before it doubles up, so the long items each start on a CU of
+    // their own and the short ones share.  (The result does not depend on
+    // the order.)
+    std::stable_sort(w.items.begin(), w.items.end(),
+                     [](const int4& x, const int4& y) { return x.z - x.y > y.z - y.y; });
 }
 
 template <int HD, int HPG>
