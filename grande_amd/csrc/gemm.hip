@@ -96,15 +96,14 @@ struct Cfg {
     static constexpr int WR = 16 * NJ;                 // weight rows per wave
     static constexpr int BNW = NW * WR;                // weight rows per tile
     static constexpr int BN = GATED ? BNW / 2 : BNW;   // output columns per tile
-    static constexpr int X_CH = BM * 8, X_I = X_CH / T;
+    static constexpr int X_CH = BM * 8, X_I = (X_CH + T - 1) / T;  // padded lanes go out of range
     static constexpr int W_CPR = QUANT == Q4_DT ? 2 : (QUANT == Q8_DT ? 4 : 8);
     static constexpr int W_CH = BNW * W_CPR, W_I = (W_CH + T - 1) / T;
     static constexpr int S_I = QUANT == F16_DT ? 0 : (BNW + T - 1) / T;
     static constexpr int C = X_I + W_I + S_I;  // DMA instructions per wave per stage
-    static constexpr int X_BYTES = BM * G_ROW, W_BYTES = W_I * T * 16, S_BYTES = S_I * T * 4;
+    static constexpr int X_BYTES = X_I * T * 16, W_BYTES = W_I * T * 16, S_BYTES = S_I * T * 4;
     static constexpr int STAGE = X_BYTES + W_BYTES + S_BYTES;
     static constexpr int LDS = NS * STAGE;
-    static_assert(X_CH % T == 0, "the X tile must split evenly over the waves");
     static_assert(LDS <= 160 * 1024, "ring larger than the LDS");
     static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
     static_assert(BN % 64 == 0 || !GATED, "a scale DMA instruction must stay in one matrix");
@@ -151,7 +150,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
         const int slot = (i * NW + wave) * WAVE + lane;
         const int r = slot / 8, lc = (slot % 8) ^ swz(r);
         xcol[i] = lc * 8;
-        xoff[i] = uint32_t((r * g.ldx + lc * 8) * 2);
+        xoff[i] = slot < P::X_CH ? uint32_t((r * g.ldx + lc * 8) * 2) : OOB;
     }
     uint32_t woff[P::W_I], wtail[P::W_I];  // wtail: the lane's offset in the K-tail stage
     bool wup[P::W_I];
@@ -375,9 +374,11 @@ static void run(hipStream_t s, const GemmArgs& g) {
 //   narrow outputs (N <= 1280, the o and down projections): 64 x 64,
 //   96 x 64 from N = 768, four slots;
 //   wide outputs (the qkv projection): 128 x 64, 96 x 128 for K >= 4096.
-//   Gated: 128 x 128 weight rows (64 output columns), 96 x 256 for Q8
-//   codes (heavier decode), 128 x 256 with three slots for very wide
-//   layers, 64 x 128 for short passes.
+//   Gated: 160 x 128 weight rows (64 output columns; a 2,384-token pass
+//   of the 270M model is 480 tiles, at most two per CU, where 128-row
+//   tiles made 608 and left 96 CUs a third), 96 x 256 for Q8 codes
+//   (heavier decode), 128 x 256 with three slots for very wide layers,
+//   64 x 128 for short passes.
 template <int QUANT, bool GATED>
 static void dispatch(hipStream_t s, const GemmArgs& g) {
     const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
@@ -393,7 +394,7 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         if (M <= 512) return run<QUANT, 4, 2, true, 2, 4>(s, g);
         if (N >= 8192) return run<QUANT, 8, 4, true, 3, 4>(s, g);
         if constexpr (QUANT == Q8_DT) return run<QUANT, 6, 4, true, 2, 4>(s, g);
-        return run<QUANT, 8, 2, true, 2, 4>(s, g);
+        return run<QUANT, 10, 2, true, 2, 4>(s, g);
     }
 }
 
