@@ -40,6 +40,18 @@ class omg_config_t(C.Structure):
                 ("capacity", C.c_uint64), ("max_rows", C.c_uint64)]
 
 
+class omg_laya_seq(C.Structure):
+    _fields_ = [("ids", C.POINTER(C.c_uint32)), ("nids", C.c_size_t), ("markers", C.POINTER(C.c_uint32)),
+                ("nmarkers", C.c_size_t), ("qtype", C.c_int)]
+
+
+class omg_laya_config_t(C.Structure):
+    _fields_ = [("vocab", C.c_uint32), ("d", C.c_uint32), ("layers", C.c_uint32), ("heads", C.c_uint32),
+                ("ff", C.c_uint32), ("head_layers", C.c_uint32), ("act_out", C.c_uint32), ("max_len", C.c_uint32),
+                ("cls", C.c_uint32), ("sep", C.c_uint32), ("mask", C.c_uint32), ("pad", C.c_uint32),
+                ("capacity", C.c_uint64), ("max_rows", C.c_uint64)]
+
+
 _P = C.c_void_p
 _SIGS = {
     "omg_last_error": (C.c_char_p, []),
@@ -92,6 +104,31 @@ _SIGS = {
     "omg_dev_gemm": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
     "omg_dev_gemm_geglu": (C.c_int, [_P, _P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
     "omg_dev_embed_norm": (C.c_int, [_P, _P, C.c_int64, C.c_float, _P, C.c_float, _P, _P, _P]),
+    "omg_dev_gemm_geglu_erf": (C.c_int, [_P, _P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
+    "omg_dev_gemm_bias_relu": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, _P, C.c_int64, _P]),
+    "omg_dev_qkv_heads": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, _P, _P, C.c_float, C.c_int64, _P, _P, _P,
+                                    _P]),
+    "omg_dev_attention_bi": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int64, C.c_int64, C.c_int, _P, _P]),
+    "omg_laya_builder_new": (_P, [C.c_char_p]),
+    "omg_laya_builder_push": (C.c_int, [_P, C.c_char_p, C.c_int, C.POINTER(C.c_int64), C.c_size_t, _P, C.c_size_t,
+                                        _P, C.c_size_t]),
+    "omg_laya_builder_push_weights": (C.c_int, [_P, _P]),
+    "omg_laya_builder_missing": (C.c_size_t, [_P, C.c_char_p, C.c_size_t]),
+    "omg_laya_builder_finish": (_P, [_P, C.c_size_t, C.c_size_t]),
+    "omg_laya_builder_free": (None, [_P]),
+    "omg_laya_synth": (_P, [C.c_char_p, C.c_uint64, C.c_int, C.c_int]),
+    "omg_laya_close": (None, [_P]),
+    "omg_laya_config": (C.c_int, [_P, C.POINTER(omg_laya_config_t)]),
+    "omg_laya_warmup": (C.c_int, [_P]),
+    "omg_laya_hidden": (C.c_int, [_P, C.POINTER(omg_laya_seq), C.c_size_t, C.POINTER(C.c_float), C.c_size_t]),
+    "omg_laya_evaluate": (C.c_int, [_P, C.POINTER(omg_laya_seq), C.c_size_t, C.POINTER(C.c_float), C.c_size_t,
+                                    C.POINTER(C.c_float), C.c_size_t]),
+    "omg_laya_temperature": (C.c_int, [_P, C.c_int, C.c_size_t, C.POINTER(C.c_float)]),
+    "omg_laya_prepare": (C.c_int, [_P, C.POINTER(omg_laya_seq), C.c_size_t]),
+    "omg_laya_launch": (C.c_int, [_P]),
+    "omg_laya_sync": (C.c_int, [_P]),
+    "omg_laya_profile": (C.c_int, [_P, C.c_int]),
+    "omg_laya_profile_report": (C.c_size_t, [_P, C.c_char_p, C.c_size_t]),
 }
 
 _lib: C.CDLL | None = None

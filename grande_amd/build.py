@@ -25,11 +25,11 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", f"-I{INCL
 # Device code never uses packed-FP32 VALU instructions.
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
-SOURCES = ["gemm.hip", "attention.hip", "norm.hip", "model.cpp", "engine.cpp", "capi.cpp"]
+SOURCES = ["gemm.hip", "attention.hip", "norm.hip", "laya.hip", "model.cpp", "engine.cpp", "laya.cpp", "capi.cpp"]
 # Per-file device flags.  The GEMM and attention kernels keep their MFMA
 # accumulators in ordinary VGPRs: with the AGPR form the register allocator
 # shuffles them between loop iterations (v_accvgpr moves in the main loop).
-EXTRA = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA = {name: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for name in ("gemm.hip", "attention.hip", "laya.hip")}
 HEADERS = sorted(CSRC.glob("*.h")) + [INCLUDE / "omg_hip.h"]
 
 

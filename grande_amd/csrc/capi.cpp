@@ -4,11 +4,14 @@
 #include "../../include/omg_hip.h"
 
 #include <cstdlib>
+#include <cstring>
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
 
 #include "engine.h"
+#include "laya.h"
 
 struct omg_builder {
     std::unique_ptr<omg::Builder> b;
@@ -20,15 +23,21 @@ struct omg_weight {
     omg::DevTensor t;
 };
 struct omg_weights {
-    omg::Weights w;
+    std::map<std::string, omg::QTensor> tensors;
     std::vector<const std::pair<const std::string, omg::QTensor>*> order;  // catalogue order
-    void index() {
+    void index(const std::vector<omg::TensorSpec>& specs) {
         order.clear();
-        for (const auto& spec : w.config.tensors()) {
-            auto it = w.tensors.find(spec.name);
-            if (it != w.tensors.end()) order.push_back(&*it);
+        for (const auto& spec : specs) {
+            auto it = tensors.find(spec.name);
+            if (it != tensors.end()) order.push_back(&*it);
         }
     }
+};
+struct omg_laya_builder {
+    std::unique_ptr<omg::LayaBuilder> b;
+};
+struct omg_laya {
+    std::unique_ptr<omg::LayaEngine> e;
 };
 
 namespace {
@@ -127,8 +136,8 @@ omg_weights* omg_synth(const char* config_json, uint64_t seed, int linear_dtype,
             omg::fail(omg::E_INVALID, "unknown dtype");
         auto cfg = omg::Config::from_json(omg::Json::parse(config_json));
         auto w = std::make_unique<omg_weights>();
-        w->w = omg::synth_weights(cfg, seed, omg::Dtype(linear_dtype), omg::Dtype(embed_dtype));
-        w->index();
+        w->tensors = omg::synth_weights(cfg, seed, omg::Dtype(linear_dtype), omg::Dtype(embed_dtype)).tensors;
+        w->index(cfg.tensors());
         out = w.release();
     });
     return out;
@@ -139,8 +148,9 @@ omg_weights* omg_load_dir(const char* dir) {
     guard([&] {
         if (!dir) omg::fail(omg::E_INVALID, "null dir");
         auto w = std::make_unique<omg_weights>();
-        w->w = omg::load_dir(dir);
-        w->index();
+        omg::Weights loaded = omg::load_dir(dir);
+        w->tensors = std::move(loaded.tensors);
+        w->index(loaded.config.tensors());
         out = w.release();
     });
     return out;
@@ -170,7 +180,7 @@ void omg_weights_free(omg_weights* w) { delete w; }
 int omg_builder_push_weights(omg_builder* b, const omg_weights* w) {
     return guard([&] {
         if (!b || !b->b || !w) omg::fail(omg::E_INVALID, "null argument");
-        for (const auto& kv : w->w.tensors) b->b->push(kv.first, kv.second);
+        for (const auto& kv : w->tensors) b->b->push(kv.first, kv.second);
     });
 }
 
@@ -411,6 +421,231 @@ int omg_dev_embed_norm(const omg_weight* embed, const uint32_t* ids, int64_t t, 
         omg::launch_embed_norm(static_cast<hipStream_t>(stream), embed->t.w, ids, t, scale, w, eps, x,
                                static_cast<omg::half_t*>(hn_f16));
     });
+}
+
+int omg_dev_gemm_geglu_erf(const omg_weight* wg, const omg_weight* wu, const void* x_f16, int64_t ldx, int64_t m,
+                           void* act_f16, int64_t ldact, void* stream) {
+    return guard([&] {
+        if (!wg || !wu || !x_f16 || !act_f16) omg::fail(omg::E_INVALID, "null argument");
+        omg::launch_gemm_geglu(static_cast<hipStream_t>(stream), static_cast<const omg::half_t*>(x_f16), ldx, wg->t.w,
+                               wu->t.w, static_cast<omg::half_t*>(act_f16), ldact, m, true);
+    });
+}
+
+int omg_dev_gemm_bias_relu(const omg_weight* w, const void* x_f16, int64_t ldx, int64_t m, const void* bias_f16,
+                           void* y_f16, int64_t ldy, void* stream) {
+    return guard([&] {
+        if (!w || !x_f16 || !bias_f16 || !y_f16) omg::fail(omg::E_INVALID, "null argument");
+        omg::launch_gemm_bias_relu(static_cast<hipStream_t>(stream), static_cast<const omg::half_t*>(x_f16), ldx, w->t.w,
+                                   static_cast<const uint16_t*>(bias_f16), static_cast<omg::half_t*>(y_f16), ldy, m);
+    });
+}
+
+int omg_dev_qkv_heads(const omg_weight* w, const void* x_f16, int64_t ldx, int64_t m, const void* bias_f16,
+                      const float* rope, const int32_t* meta, float qscale, int64_t tpad, void* q16, void* k16,
+                      void* vt, void* stream) {
+    return guard([&] {
+        if (!w || !x_f16) omg::fail(omg::E_INVALID, "null argument");
+        omg::QkvHeads o{};
+        o.rope = reinterpret_cast<const float2*>(rope);
+        o.meta = meta;
+        o.qscale = qscale;
+        o.dq = w->t.w.rows / 3;
+        o.tpad = tpad;
+        o.q16 = static_cast<omg::half_t*>(q16);
+        o.k16 = static_cast<omg::half_t*>(k16);
+        o.vt = static_cast<omg::half_t*>(vt);
+        omg::launch_gemm_qkv_heads(static_cast<hipStream_t>(stream), static_cast<const omg::half_t*>(x_f16), ldx,
+                                   w->t.w, static_cast<const uint16_t*>(bias_f16), o, m);
+    });
+}
+
+int omg_dev_attention_bi(const void* q16, const void* k16, const void* vt, const int32_t* meta, int heads, int64_t t,
+                         int64_t tpad, int window, void* out_f16, void* stream) {
+    return guard([&] {
+        omg::QkvHeads o{};
+        o.meta = meta;
+        o.dq = int64_t(heads) * 64;
+        o.tpad = tpad;
+        o.q16 = static_cast<omg::half_t*>(const_cast<void*>(q16));
+        o.k16 = static_cast<omg::half_t*>(const_cast<void*>(k16));
+        o.vt = static_cast<omg::half_t*>(const_cast<void*>(vt));
+        omg::launch_attention_bi(static_cast<hipStream_t>(stream), o, heads, t, window,
+                                 static_cast<omg::half_t*>(out_f16));
+    });
+}
+
+/* ---- the bidirectional encoder path ---- */
+
+omg_laya_builder* omg_laya_builder_new(const char* config_json) {
+    omg_laya_builder* out = nullptr;
+    guard([&] {
+        if (!config_json) omg::fail(omg::E_INVALID, "null config");
+        auto cfg = omg::LayaConfig::from_json(omg::Json::parse(config_json));
+        out = new omg_laya_builder{std::make_unique<omg::LayaBuilder>(std::move(cfg))};
+    });
+    return out;
+}
+
+int omg_laya_builder_push(omg_laya_builder* b, const char* name, int dtype, const int64_t* shape, size_t ndim,
+                          const void* data, size_t nbytes, const void* scales, size_t nscale_bytes) {
+    return guard([&] {
+        if (!b || !b->b || !name || (ndim && !shape)) omg::fail(omg::E_INVALID, "null argument");
+        b->b->push(name, make_tensor(dtype, shape, ndim, data, nbytes, scales, nscale_bytes));
+    });
+}
+
+int omg_laya_builder_push_weights(omg_laya_builder* b, const omg_weights* w) {
+    return guard([&] {
+        if (!b || !b->b || !w) omg::fail(omg::E_INVALID, "null argument");
+        for (const auto& kv : w->tensors) b->b->push(kv.first, kv.second);
+    });
+}
+
+size_t omg_laya_builder_missing(omg_laya_builder* b, char* buf, size_t len) {
+    if (!b || !b->b) return 0;
+    const auto m = b->b->missing();
+    std::string s;
+    for (const auto& n : m) s += n + "\n";
+    if (buf && len) {
+        const size_t k = s.size() < len - 1 ? s.size() : len - 1;
+        std::memcpy(buf, s.data(), k);
+        buf[k] = 0;
+    }
+    return m.size();
+}
+
+omg_laya* omg_laya_builder_finish(omg_laya_builder* b, size_t capacity, size_t max_rows) {
+    omg_laya* out = nullptr;
+    guard([&] {
+        if (!b || !b->b) omg::fail(omg::E_INVALID, "null builder");
+        std::unique_ptr<omg::LayaBuilder> own = std::move(b->b);
+        out = new omg_laya{own->finish(int64_t(capacity), int64_t(max_rows))};
+    });
+    delete b;
+    return out;
+}
+
+void omg_laya_builder_free(omg_laya_builder* b) { delete b; }
+
+omg_weights* omg_laya_synth(const char* config_json, uint64_t seed, int linear_dtype, int embed_dtype) {
+    omg_weights* out = nullptr;
+    guard([&] {
+        if (!config_json) omg::fail(omg::E_INVALID, "null config");
+        if (linear_dtype < 0 || linear_dtype > 2 || embed_dtype < 0 || embed_dtype > 2)
+            omg::fail(omg::E_INVALID, "unknown dtype");
+        auto cfg = omg::LayaConfig::from_json(omg::Json::parse(config_json));
+        auto w = std::make_unique<omg_weights>();
+        w->tensors = omg::synth_laya(cfg, seed, omg::Dtype(linear_dtype), omg::Dtype(embed_dtype)).tensors;
+        w->index(cfg.tensors());
+        out = w.release();
+    });
+    return out;
+}
+
+void omg_laya_close(omg_laya* e) { delete e; }
+
+}  // extern "C"
+
+namespace {
+
+omg::LayaEngine& laya(omg_laya* e) {
+    if (!e || !e->e) omg::fail(omg::E_INVALID, "null engine");
+    return *e->e;
+}
+
+std::vector<omg::LayaSeq> laya_seqs(const omg_laya_seq* s, size_t n) {
+    if (n && !s) omg::fail(omg::E_INVALID, "null sequences");
+    std::vector<omg::LayaSeq> v;
+    for (size_t i = 0; i < n; ++i) {
+        if ((s[i].nids && !s[i].ids) || (s[i].nmarkers && !s[i].markers)) omg::fail(omg::E_INVALID, "null sequence data");
+        v.push_back({s[i].ids, int64_t(s[i].nids), s[i].markers, int64_t(s[i].nmarkers), s[i].qtype});
+    }
+    return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+int omg_laya_hidden(omg_laya* e, const omg_laya_seq* seqs, size_t n, float* out, size_t out_floats) {
+    return guard([&] {
+        auto v = laya_seqs(seqs, n);
+        if (!out) omg::fail(omg::E_INVALID, "null output");
+        laya(e).hidden(v.data(), int64_t(n), out, int64_t(out_floats));
+    });
+}
+
+int omg_laya_evaluate(omg_laya* e, const omg_laya_seq* seqs, size_t n, float* logits, size_t nlogits, float* act,
+                      size_t nact) {
+    return guard([&] {
+        auto v = laya_seqs(seqs, n);
+        if ((nlogits && !logits) || (nact && !act)) omg::fail(omg::E_INVALID, "null output");
+        laya(e).evaluate(v.data(), int64_t(n), logits, int64_t(nlogits), act, int64_t(nact));
+    });
+}
+
+int omg_laya_warmup(omg_laya* e) {
+    return guard([&] { laya(e).warmup(); });
+}
+
+int omg_laya_config(const omg_laya* e, omg_laya_config_t* out) {
+    return guard([&] {
+        if (!e || !e->e || !out) omg::fail(omg::E_INVALID, "null argument");
+        const omg::LayaConfig& c = e->e->config();
+        out->vocab = uint32_t(c.vocab);
+        out->d = uint32_t(c.d);
+        out->layers = uint32_t(c.layers);
+        out->heads = uint32_t(c.heads);
+        out->ff = uint32_t(c.ff);
+        out->head_layers = uint32_t(c.head_layers);
+        out->act_out = uint32_t(c.act_out);
+        out->max_len = uint32_t(c.max_len);
+        out->cls = c.cls;
+        out->sep = c.sep;
+        out->mask = c.mask;
+        out->pad = c.pad;
+        out->capacity = uint64_t(e->e->capacity());
+        out->max_rows = uint64_t(e->e->max_rows());
+    });
+}
+
+int omg_laya_temperature(const omg_laya* e, int qtype, size_t k, float* out) {
+    return guard([&] {
+        if (!e || !e->e || !out) omg::fail(omg::E_INVALID, "null argument");
+        if (qtype < 0 || qtype >= 3) omg::fail(omg::E_INVALID, "question type " + std::to_string(qtype));
+        *out = e->e->config().temperature_for(qtype, int64_t(k));
+    });
+}
+
+int omg_laya_prepare(omg_laya* e, const omg_laya_seq* seqs, size_t n) {
+    return guard([&] {
+        auto v = laya_seqs(seqs, n);
+        laya(e).prepare(v.data(), int64_t(n));
+    });
+}
+
+int omg_laya_launch(omg_laya* e) {
+    return guard([&] { laya(e).launch_prepared(); });
+}
+
+int omg_laya_sync(omg_laya* e) {
+    return guard([&] { laya(e).sync(); });
+}
+
+int omg_laya_profile(omg_laya* e, int on) {
+    return guard([&] { laya(e).set_profile(on != 0); });
+}
+
+size_t omg_laya_profile_report(omg_laya* e, char* buf, size_t len) {
+    std::string s;
+    guard([&] { s = laya(e).profile_report(); });
+    if (buf && len) {
+        const size_t k = s.size() < len - 1 ? s.size() : len - 1;
+        std::memcpy(buf, s.data(), k);
+        buf[k] = 0;
+    }
+    return s.size();
 }
 
 }  // extern "C"

@@ -51,12 +51,23 @@ constexpr uint32_t OOB = 0x7ffffff0u;  // an offset past every resource
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Epilogues: what a tile does with its f32 accumulators.
+//   EPI_F32        y[m][n] = acc (f32)
+//   EPI_GELU_TANH  y[m][n] = f16(gelu_tanh(acc_gate) * acc_up)  (gated)
+//   EPI_GELU_ERF   y[m][n] = f16(gelu_erf(acc_gate) * acc_up)   (gated)
+//   EPI_RELU_F16   y[m][n] = f16(max(acc + bias[n], 0))
+//   EPI_QKV        the fused [q | k | v] projection of a bidirectional
+//                  encoder, scattered per head as f16 (see QkvHeads)
+constexpr int EPI_F32 = 0, EPI_GELU_TANH = 1, EPI_GELU_ERF = 2, EPI_RELU_F16 = 3, EPI_QKV = 4;
+
 struct GemmArgs {
     const half_t* x;
     int64_t ldx, m;
     DevWeight w0, w1;  // w1: the up projection of the gated kernel
     void* y;
     int64_t ldy;
+    const uint16_t* bias;  // f16 per output column (EPI_RELU_F16; EPI_QKV, may be null)
+    QkvHeads qkv;          // EPI_QKV
 };
 
 constexpr int RSRC_FLAGS = 0x00020000;  // raw (untyped) 32-bit buffer
@@ -79,6 +90,20 @@ __device__ inline void wait_vm() {
 // LDS writes done, then the workgroup barrier; a compiler fence for memory.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// matmul_gated.wgsl:117-129: exact GELU, 0.5 x (1 + erf(x / sqrt 2)), with
+// erf from Abramowitz & Stegun 7.1.26 (|error| < 1.5e-7), the form the
+// reference evaluates.
+__device__ inline float gelu_erf(float x) {
+    const float z = x * 0.7071067811865476f;
+    const float a = fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
+    const float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+                        0.254829592f) * t;
+    const float e = __builtin_amdgcn_exp2f(-a * a * 1.4426950408889634f);  // e^(-a^2)
+    const float y = 1.0f - poly * e;
+    return 0.5f * x * (1.0f + (z < 0.0f ? -y : y));
+}
+
 // matmul_gated.wgsl:126-134: tanh GELU with the argument clamped to +-15,
 // through the identity 0.5 (1 + tanh z) = 1 / (1 + e^(-2z)) evaluated with
 // the hardware exp2 and reciprocal.
@@ -89,8 +114,9 @@ __device__ inline float gelu_tanh(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-template <int QUANT, int MI, int NJ, bool GATED, int NS, int NW_ = 4>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_ = 4>
 struct Cfg {
+    static constexpr bool GATED = EPI == EPI_GELU_TANH || EPI == EPI_GELU_ERF;
     static constexpr int NW = NW_, T = NW * WAVE;
     static constexpr int BM = 16 * MI;
     static constexpr int WR = 16 * NJ;                 // weight rows per wave
@@ -109,11 +135,13 @@ struct Cfg {
     static_assert(BN % 64 == 0 || !GATED, "a scale DMA instruction must stay in one matrix");
     static_assert(NS >= 2, "ring needs >= 2 slots");
     static_assert(C <= 63, "vmcnt range");
+    static_assert(EPI != EPI_QKV || WR == 64, "the Q/K/V epilogue gives each wave one 64-wide head");
 };
 
-template <int QUANT, int MI, int NJ, bool GATED, int NS, int NW_>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_>
 __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
-    using P = Cfg<QUANT, MI, NJ, GATED, NS, NW_>;
+    using P = Cfg<QUANT, MI, NJ, EPI, NS, NW_>;
+    constexpr bool GATED = P::GATED;
     constexpr int NW = P::NW, BM = P::BM, BN = P::BN, WR = P::WR;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = int(threadIdx.x), lane = tid % WAVE;
@@ -135,7 +163,6 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     const int64_t rows_m = M - m0 < BM ? M - m0 : BM;
     const int64_t rows_n = N - n0 < BN ? N - n0 : BN;
 
-    const __amdgpu_buffer_rsrc_t rx = rsrc(g.x + m0 * g.ldx, rows_m * g.ldx * 2);
     const int64_t wrow = QUANT == Q4_DT ? KB * 16 : (QUANT == Q8_DT ? K : 2 * K);
     const uint8_t* const wbase0 = static_cast<const uint8_t*>(g.w0.data) + n0 * wrow;
     const uint8_t* const wbase1 = static_cast<const uint8_t*>(g.w1.data) + n0 * wrow;
@@ -312,8 +339,72 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
 
     // Epilogue: lane (lr, lg) holds output columns 4 lg..4 lg + 3 of row lr
     // of each 16 x 16 block.
+    if constexpr (EPI == EPI_QKV) {
+        // The wave's 64 columns are one head of q, k or v (the q width and
+        // the tile edges are multiples of 64).  RoPE pairs dims (c, c + 32),
+        // which sit in blocks j and j + 2 of the same lane.
+        const QkvHeads& o = g.qkv;
+        const int64_t c0 = n0 + wave * WR;
+        if (c0 >= N) return;
+        const int sec = int(c0 / o.dq);
+        const int64_t head = (c0 % o.dq) / 64;
+        float bias[NJ][4];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                bias[j][r] = g.bias ? float(__builtin_bit_cast(half_t, g.bias[c0 + 16 * j + 4 * lg + r])) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            const int64_t m = m0 + i * 16 + lr;
+            if (m >= M) continue;
+            float v[NJ][4];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[j][r] = acc[i][j][r] + bias[j][r];
+            if (sec < 2 && o.rope) {
+                // rope_bi.wgsl:30-49: a' = a cos - b sin, b' = b cos + a sin.
+                const float2* rp = o.rope + int64_t(o.meta[4 * m]) * 32;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float2 cs = rp[16 * j + 4 * lg + r];
+                        const float a = v[j][r], b = v[j + 2][r];
+                        v[j][r] = a * cs.x - b * cs.y;
+                        v[j + 2][r] = b * cs.x + a * cs.y;
+                    }
+            }
+            if (sec < 2) {
+                const float sc = sec == 0 ? o.qscale : 1.0f;
+                half_t* dst = (sec == 0 ? o.q16 : o.k16) + (head * o.tpad + m) * 64;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    *reinterpret_cast<half4*>(dst + 16 * j + 4 * lg) =
+                        half4{half_t(v[j][0] * sc), half_t(v[j][1] * sc), half_t(v[j][2] * sc), half_t(v[j][3] * sc)};
+            } else {
+                half_t* dst = o.vt + (head * (o.tpad / 32) + m / 32) * (64 * 32) + vt_col32(int(m % 32));
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) dst[(16 * j + 4 * lg + r) * 32] = half_t(v[j][r]);
+            }
+        }
+        return;
+    }
     constexpr int NO = GATED ? NJ / 2 : NJ;
     const int64_t nw0 = n0 + (GATED ? wave * (WR / 2) : wave * WR);
+    float cbias[EPI == EPI_RELU_F16 ? NO : 1][4];
+    if constexpr (EPI == EPI_RELU_F16) {
+#pragma unroll
+        for (int j = 0; j < NO; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t n = nw0 + j * 16 + lg * 4 + r;
+                cbias[j][r] = n < N ? float(__builtin_bit_cast(half_t, g.bias[n])) : 0.0f;
+            }
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
         const int64_t m = m0 + i * 16 + lr;
@@ -323,10 +414,19 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
             const int64_t n = nw0 + j * 16 + lg * 4;
             float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                v[r] = GATED ? gelu_tanh(acc[i][j][r]) * acc[i][j + (GATED ? NJ / 2 : 0)][r] : acc[i][j][r];
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (EPI == EPI_GELU_TANH)
+                    v[r] = gelu_tanh(acc[i][j][r]) * acc[i][j + NJ / 2][r];
+                else if constexpr (EPI == EPI_GELU_ERF)
+                    v[r] = gelu_erf(acc[i][j][r]) * acc[i][j + NJ / 2][r];
+                else if constexpr (EPI == EPI_RELU_F16)
+                    v[r] = fmaxf(acc[i][j][r] + cbias[j][r], 0.0f);
+                else
+                    v[r] = acc[i][j][r];
+            }
+            constexpr bool F16_OUT = EPI != EPI_F32;
             if (n + 3 < N) {
-                if constexpr (GATED) {
+                if constexpr (F16_OUT) {
                     *reinterpret_cast<half4*>(static_cast<half_t*>(g.y) + m * g.ldy + n) =
                         half4{half_t(v[0]), half_t(v[1]), half_t(v[2]), half_t(v[3])};
                 } else {
@@ -337,7 +437,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if (n + r >= N) break;
-                    if constexpr (GATED)
+                    if constexpr (F16_OUT)
                         static_cast<half_t*>(g.y)[m * g.ldy + n + r] = half_t(v[r]);
                     else
                         static_cast<float*>(g.y)[m * g.ldy + n + r] = v[r];
@@ -347,19 +447,19 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     }
 }
 
-template <int QUANT, int MI, int NJ, bool GATED, int NS, int NW = 4>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4>
 static void run(hipStream_t s, const GemmArgs& g) {
-    using P = Cfg<QUANT, MI, NJ, GATED, NS, NW>;
+    using P = Cfg<QUANT, MI, NJ, EPI, NS, NW>;
     static bool lds_set = false;
     if (!lds_set) {
-        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<QUANT, MI, NJ, GATED, NS, NW>),
+        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<QUANT, MI, NJ, EPI, NS, NW>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
         lds_set = true;
     }
     const int64_t N = g.w0.rows;
     const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + P::BM - 1) / P::BM);
     const dim3 grid(unsigned((tiles + 7) / 8 * 8));
-    gemm_kernel<QUANT, MI, NJ, GATED, NS, NW><<<grid, dim3(P::T), P::LDS, s>>>(g);
+    gemm_kernel<QUANT, MI, NJ, EPI, NS, NW><<<grid, dim3(P::T), P::LDS, s>>>(g);
     OMG_HIP(hipGetLastError());
 }
 
@@ -376,25 +476,35 @@ static void run(hipStream_t s, const GemmArgs& g) {
 //   wide outputs (the qkv projection): 128 x 64, 96 x 128 for K >= 4096.
 //   Gated: 160 x 128 weight rows (64 output columns; a 2,384-token pass
 //   of the 270M model is 480 tiles, at most two per CU, where 128-row
-//   tiles made 608 and left 96 CUs a third), 96 x 256 for Q8 codes
-//   (heavier decode), 128 x 256 with three slots for very wide layers,
-//   64 x 128 for short passes.
-template <int QUANT, bool GATED>
+//   tiles made 608 and left 96 CUs a third), 128 x 256 with three slots
+//   for very wide layers, 64 x 128 for short passes.
+template <int QUANT, int EPI>
 static void dispatch(hipStream_t s, const GemmArgs& g) {
     const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
-    if constexpr (!GATED) {
-        if (M <= 512) return run<QUANT, 2, 1, false, 4, 2>(s, g);
+    if constexpr (EPI == EPI_QKV) {
+        if (M <= 512) return run<QUANT, 2, 4, EPI, 4, 4>(s, g);
+        return run<QUANT, 8, 4, EPI, 2, 4>(s, g);
+    } else if constexpr (EPI == EPI_F32 || EPI == EPI_RELU_F16) {
+        if (M <= 512) return run<QUANT, 2, 1, EPI, 4, 2>(s, g);
         if (N <= 1280) {
-            if (N > 768) return run<QUANT, 6, 1, false, 4, 4>(s, g);
-            return run<QUANT, 4, 1, false, 4, 4>(s, g);
+            if (N > 768) return run<QUANT, 6, 1, EPI, 4, 4>(s, g);
+            return run<QUANT, 4, 1, EPI, 4, 4>(s, g);
         }
-        if (K >= 4096) return run<QUANT, 6, 2, false, 2, 4>(s, g);
-        return run<QUANT, 8, 1, false, 2, 4>(s, g);
+        if (K >= 4096) return run<QUANT, 6, 2, EPI, 2, 4>(s, g);
+        return run<QUANT, 8, 1, EPI, 2, 4>(s, g);
     } else {
-        if (M <= 512) return run<QUANT, 4, 2, true, 2, 4>(s, g);
-        if (N >= 8192) return run<QUANT, 8, 4, true, 3, 4>(s, g);
-        if constexpr (QUANT == Q8_DT) return run<QUANT, 6, 4, true, 2, 4>(s, g);
-        return run<QUANT, 10, 2, true, 2, 4>(s, g);
+        if (M <= 512) return run<QUANT, 4, 2, EPI, 2, 4>(s, g);
+        if (N >= 8192) return run<QUANT, 8, 4, EPI, 3, 4>(s, g);
+        return run<QUANT, 10, 2, EPI, 2, 4>(s, g);
+    }
+}
+
+template <int EPI>
+static void dispatch_dtype(hipStream_t s, const GemmArgs& g) {
+    switch (g.w0.dtype) {
+        case F16_DT: return dispatch<F16_DT, EPI>(s, g);
+        case Q8_DT: return dispatch<Q8_DT, EPI>(s, g);
+        default: return dispatch<Q4_DT, EPI>(s, g);
     }
 }
 
@@ -417,26 +527,37 @@ void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w
                  int64_t m) {
     check(x, ldx, w, ldy, m);
     if (m == 0) return;
-    const GemmArgs g{x, ldx, m, w, w, y, ldy};
-    switch (w.dtype) {
-        case F16_DT: return dispatch<F16_DT, false>(s, g);
-        case Q8_DT: return dispatch<Q8_DT, false>(s, g);
-        default: return dispatch<Q4_DT, false>(s, g);
-    }
+    dispatch_dtype<EPI_F32>(s, GemmArgs{x, ldx, m, w, w, y, ldy, nullptr, {}});
 }
 
 void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,
-                       const DevWeight& wu, half_t* act, int64_t ldact, int64_t m) {
+                       const DevWeight& wu, half_t* act, int64_t ldact, int64_t m, bool erf) {
     check(x, ldx, wg, ldact, m);
     if (wu.rows != wg.rows || wu.cols != wg.cols || wu.dtype != wg.dtype || wu.sld != wg.sld)
         fail(E_INVALID, "gemm_geglu: gate and up must share shape and storage type");
     if (m == 0) return;
-    const GemmArgs g{x, ldx, m, wg, wu, act, ldact};
-    switch (wg.dtype) {
-        case F16_DT: return dispatch<F16_DT, true>(s, g);
-        case Q8_DT: return dispatch<Q8_DT, true>(s, g);
-        default: return dispatch<Q4_DT, true>(s, g);
-    }
+    const GemmArgs g{x, ldx, m, wg, wu, act, ldact, nullptr, {}};
+    if (erf) return dispatch_dtype<EPI_GELU_ERF>(s, g);
+    dispatch_dtype<EPI_GELU_TANH>(s, g);
+}
+
+void launch_gemm_bias_relu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w,
+                           const uint16_t* bias, half_t* y, int64_t ldy, int64_t m) {
+    check(x, ldx, w, ldy, m);
+    if (!bias) fail(E_INVALID, "gemm_bias_relu: bias required");
+    if (m == 0) return;
+    dispatch_dtype<EPI_RELU_F16>(s, GemmArgs{x, ldx, m, w, w, y, ldy, bias, {}});
+}
+
+void launch_gemm_qkv_heads(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w,
+                           const uint16_t* bias, const QkvHeads& o, int64_t m) {
+    check(x, ldx, w, w.rows, m);
+    if (o.dq <= 0 || o.dq % 64 != 0 || w.rows != 3 * o.dq)
+        fail(E_INVALID, "gemm_qkv_heads: N must be 3 x the q width, a multiple of 64");
+    if (o.tpad < m || o.tpad % 32 != 0) fail(E_INVALID, "gemm_qkv_heads: padded rows must cover M, multiple of 32");
+    if (!o.q16 || !o.k16 || !o.vt || (o.rope && !o.meta)) fail(E_INVALID, "gemm_qkv_heads: missing output");
+    if (m == 0) return;
+    dispatch_dtype<EPI_QKV>(s, GemmArgs{x, ldx, m, w, w, nullptr, 0, bias, o});
 }
 
 }  // namespace omg

@@ -41,6 +41,16 @@ __device__ inline float max_lanes_16_32(float v) {
     return fmaxf(__builtin_bit_cast(float, uint32_t(q[0])), __builtin_bit_cast(float, uint32_t(q[1])));
 }
 
+// Sum over the same four lanes.
+__device__ inline float sum_lanes_16_32(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float m = __builtin_bit_cast(float, uint32_t(p[0])) + __builtin_bit_cast(float, uint32_t(p[1]));
+    const uint32_t w = __builtin_bit_cast(uint32_t, m);
+    const auto q = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return __builtin_bit_cast(float, uint32_t(q[0])) + __builtin_bit_cast(float, uint32_t(q[1]));
+}
+
 __device__ inline float half_bits_to_f32(uint16_t h) {
     return float(__builtin_bit_cast(half_t, h));
 }
@@ -94,6 +104,31 @@ __device__ inline half8 dq8_words(uint32_t w0, uint32_t w1, half2v dd) {
     const half2v h2 = (q8_pair(b, 0x04010400u) - off) * dd;
     const half2v h3 = (q8_pair(b, 0x04030402u) - off) * dd;
     return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
+}
+
+// Elements (row, c..c+3) (c % 4 == 0) of a device weight, f32.
+template <int DT>
+__device__ inline void load4_f32(const DevWeight& w, int64_t row, int64_t c, float v[4]) {
+    const int64_t e = row * w.cols + c;
+    if constexpr (DT == F16_DT) {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const half_t*>(w.data) + e);
+        const half2v a = as_half2(u.x), b = as_half2(u.y);
+        v[0] = float(a.x);
+        v[1] = float(a.y);
+        v[2] = float(b.x);
+        v[3] = float(b.y);
+    } else if constexpr (DT == Q8_DT) {
+        const float d = half_bits_to_f32(w.scales[row * w.sld + c / 32]);
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(w.data) + e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = float(int8_t(u >> (8 * i))) * d;
+    } else {
+        const int j = int(c % 32);
+        const float d = half_bits_to_f32(w.scales[row * w.sld + c / 32]);
+        const uint32_t word = static_cast<const uint32_t*>(w.data)[(e / 32) * 4 + j / 8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = q4_elem_f32(word, (j % 8) + i, d);
+    }
 }
 
 }  // namespace omg

@@ -74,13 +74,59 @@ void launch_kv_gather(hipStream_t s, const half_t* kc, const half_t* vt, int64_t
 void launch_kv_scatter(hipStream_t s, half_t* kc, half_t* vt, int64_t cap_pad, int kv_heads, int hd,
                        int64_t row0, int64_t rows, const half_t* in);
 
+// Column of key k (0..31) inside its 32-key V^T tile of the bidirectional
+// encoder's attention: the eight keys one MFMA lane holds probabilities
+// for (4g..4g+3 and 16+4g..16+4g+3) are adjacent.
+__host__ __device__ inline int vt_col32(int k) { return 8 * ((k % 16) / 4) + 4 * (k / 16) + k % 4; }
+
+// The fused [q | k | v] projection of a bidirectional encoder layer
+// (64-wide heads), scattered per head as f16 for the attention kernel:
+// bias added, q and k rotated (rope_bi.wgsl) when `rope` is set, q scaled.
+struct QkvHeads {
+    const float2* rope;   // [max pos + 1][32]: (cos, sin) of pos * inv_freq[i]; null = no rotation
+    const int32_t* meta;  // 4 ints per token: pos, seq, first row, last row + 1
+    float qscale;
+    int64_t dq;           // q width = heads * 64
+    int64_t tpad;         // rows of the head arrays (>= t, multiple of 32)
+    half_t* q16;          // [heads][tpad][64]
+    half_t* k16;          // [heads][tpad][64]
+    half_t* vt;           // [heads][tpad / 32][64][32], key columns ordered by vt_col32
+};
+
 // ---- MFMA GEMMs (gemm.hip) ----
 // y[M][N] (f32) = f16(X)[M][K] . deq(W)[N][K]^T, f32 accumulation.
 void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
                  int64_t m);
-// act[M][F] (f16) = gelu_tanh(X . Wg^T) * (X . Wu^T).
+// act[M][F] (f16) = gelu(X . Wg^T) * (X . Wu^T); gelu_tanh, or the exact
+// (erf) form when `erf`.
 void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,
-                       const DevWeight& wu, half_t* act, int64_t ldact, int64_t m);
+                       const DevWeight& wu, half_t* act, int64_t ldact, int64_t m, bool erf = false);
+// y[M][N] (f16) = max(X . W^T + bias, 0) (bias f16 [N]).
+void launch_gemm_bias_relu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w,
+                           const uint16_t* bias, half_t* y, int64_t ldy, int64_t m);
+// The [q | k | v] projection X . W^T (+ bias) into QkvHeads' arrays.
+void launch_gemm_qkv_heads(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w,
+                           const uint16_t* bias, const QkvHeads& o, int64_t m);
+
+// ---- bidirectional encoder rows and attention (laya.hip) ----
+// out[t][h * 64 + c] (f16) = sum over visible keys j of softmax_j(q_t . k_j) v_j[c]:
+// visible = same sequence (the span meta[2]..meta[3] of the query row) and,
+// when window > 0, |t - j| <= window (attention_bi.wgsl).
+void launch_attention_bi(hipStream_t s, const QkvHeads& a, int heads, int64_t t, int window, half_t* out);
+// x[r] = LayerNorm(deq(E[ids[r]]); w) (f32), x16[r] = f16(x[r]).
+void launch_embed_ln(hipStream_t s, const DevWeight& E, const uint32_t* ids, int64_t t, const float* w,
+                     float eps, float* x, half_t* x16);
+// x[r] = (x[r] + a[r]) (+ rb);  h16[r] = f16(LayerNorm(x[r]; w, b)).  rb, b may be null.
+void launch_add_ln(hipStream_t s, float* x, const float* a, const float* rb, const float* w, const float* b,
+                   float eps, int64_t t, int64_t d, half_t* h16);
+// x[r] = LayerNorm(x[r] + a[r]; wf);  x[r] += temb[qtypes[r]] (if temb);
+// h16[r] = f16(LayerNorm(x[r]; w1, b1)) (if w1).
+void launch_add_ln_final(hipStream_t s, float* x, const float* a, const float* wf, const float* temb,
+                         const uint32_t* qtypes, const float* w1, const float* b1, float eps, int64_t t,
+                         int64_t d, half_t* h16);
+// out[i] = (a[rows[i]] + bias) + x[rows[i]] (f32), or x[rows[i]] when a is null.
+void launch_gather_rows(hipStream_t s, const float* x, const float* a, const float* bias, const int32_t* rows,
+                        int64_t n, int64_t d, float* out);
 
 // Column of cache row `row` inside its 64-row V^T tile.  Within each half
 // of 32 keys, key k sits at 8 * ((k % 16) / 4) + 4 * (k / 16) + k % 4: the

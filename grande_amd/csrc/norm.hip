@@ -11,33 +11,6 @@
 
 namespace omg {
 
-// ---------------------------------------------------------------- decode
-
-// Elements (row, c..c+3) (c % 4 == 0) of a device weight, f32.
-template <int DT>
-__device__ inline void load4_f32(const DevWeight& w, int64_t row, int64_t c, float v[4]) {
-    const int64_t e = row * w.cols + c;
-    if constexpr (DT == F16_DT) {
-        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const half_t*>(w.data) + e);
-        const half2v a = as_half2(u.x), b = as_half2(u.y);
-        v[0] = float(a.x);
-        v[1] = float(a.y);
-        v[2] = float(b.x);
-        v[3] = float(b.y);
-    } else if constexpr (DT == Q8_DT) {
-        const float d = half_bits_to_f32(w.scales[row * w.sld + c / 32]);
-        const uint32_t u = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(w.data) + e);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = float(int8_t(u >> (8 * i))) * d;
-    } else {
-        const int j = int(c % 32);
-        const float d = half_bits_to_f32(w.scales[row * w.sld + c / 32]);
-        const uint32_t word = static_cast<const uint32_t*>(w.data)[(e / 32) * 4 + j / 8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = q4_elem_f32(word, (j % 8) + i, d);
-    }
-}
-
 // ------------------------------------------------------------ embedding
 
 // embed.wgsl:15-48 + the layer-0 input norm (rmsnorm.wgsl:41-61), one wave

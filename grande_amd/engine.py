@@ -300,3 +300,23 @@ class DeviceWeight:
     def embed_norm(self, ids_ptr: int, t: int, scale: float, w_ptr: int, eps: float, x_ptr: int, hn_ptr: int,
                    stream: int | None = None) -> None:
         L.check(L.lib().omg_dev_embed_norm(self._h, ids_ptr, t, scale, w_ptr, eps, x_ptr, hn_ptr, stream))
+
+    def gemm_geglu_erf(self, up: "DeviceWeight", x_ptr: int, ldx: int, m: int, act_ptr: int, ldact: int,
+                       stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_gemm_geglu_erf(self._h, up._h, x_ptr, ldx, m, act_ptr, ldact, stream))
+
+    def gemm_bias_relu(self, x_ptr: int, ldx: int, m: int, bias_ptr: int, y_ptr: int, ldy: int,
+                       stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_gemm_bias_relu(self._h, x_ptr, ldx, m, bias_ptr, y_ptr, ldy, stream))
+
+    def qkv_heads(self, x_ptr: int, ldx: int, m: int, bias_ptr: int | None, rope_ptr: int | None,
+                  meta_ptr: int | None, qscale: float, tpad: int, q_ptr: int, k_ptr: int, vt_ptr: int,
+                  stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_qkv_heads(self._h, x_ptr, ldx, m, bias_ptr, rope_ptr, meta_ptr, qscale, tpad, q_ptr,
+                                          k_ptr, vt_ptr, stream))
+
+
+def attention_bi(q_ptr: int, k_ptr: int, vt_ptr: int, meta_ptr: int, heads: int, t: int, tpad: int, window: int,
+                 out_ptr: int, stream: int | None = None) -> None:
+    """The encoder path's attention kernel on device pointers."""
+    L.check(L.lib().omg_dev_attention_bi(q_ptr, k_ptr, vt_ptr, meta_ptr, heads, t, tpad, window, out_ptr, stream))

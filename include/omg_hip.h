@@ -208,6 +208,91 @@ int omg_dev_gemm_geglu(const omg_weight *wg, const omg_weight *wu, const void *x
 int omg_dev_embed_norm(const omg_weight *embed, const uint32_t *ids, int64_t t, float scale, const float *w,
                        float eps, float *x, void *hn_f16, void *stream);
 
+/* Kernel-level entry points of the encoder path, on device pointers:
+ * the gated GEMM with the exact (erf) GELU (matmul_gated.wgsl GELU_ERF = 1);
+ * Y = f16(max(X.W^T + bias, 0)) (matmul.wgsl then bias_act.wgsl mode 1);
+ * the fused [q | k | v] projection scattered per 64-wide head as f16 with
+ * bias, RoPE from `rope` ([pos][32] (cos, sin) pairs; NULL = none, then
+ * `meta` may be NULL) and the q scale (rope_bi.wgsl): q16 / k16
+ * [heads][tpad][64], vt [heads][tpad/32][64][32] with key k of a tile at
+ * column 8*((k%16)/4) + 4*(k/16) + k%4; and the bidirectional attention
+ * over those arrays (attention_bi.wgsl): out [t][heads*64] f16. */
+int omg_dev_gemm_geglu_erf(const omg_weight *wg, const omg_weight *wu, const void *x_f16, int64_t ldx, int64_t m,
+                           void *act_f16, int64_t ldact, void *stream);
+int omg_dev_gemm_bias_relu(const omg_weight *w, const void *x_f16, int64_t ldx, int64_t m, const void *bias_f16,
+                           void *y_f16, int64_t ldy, void *stream);
+int omg_dev_qkv_heads(const omg_weight *w, const void *x_f16, int64_t ldx, int64_t m, const void *bias_f16,
+                      const float *rope, const int32_t *meta, float qscale, int64_t tpad, void *q16, void *k16,
+                      void *vt, void *stream);
+int omg_dev_attention_bi(const void *q16, const void *k16, const void *vt, const int32_t *meta, int heads, int64_t t,
+                         int64_t tpad, int window, void *out_f16, void *stream);
+
+/* ---- the bidirectional encoder path (crates/omg-wgpu/src/laya.rs) ----
+ * An mmBERT / ModernBERT encoder with Laya's decision head: every question
+ * is one sequence; a request's sequences run as one packed pass isolated by
+ * the attention mask; the scorer reads the [CLS] and [MASK] rows on the
+ * host. */
+typedef struct omg_laya omg_laya;
+typedef struct omg_laya_builder omg_laya_builder;
+
+/* laya.rs:468-476 Sequence: token ids, the token index of each option's
+ * [MASK] (option order), question type (0 choice, 1 score, 2 noul). */
+typedef struct {
+    const uint32_t *ids;
+    size_t nids;
+    const uint32_t *markers;
+    size_t nmarkers;
+    int qtype;
+} omg_laya_seq;
+
+typedef struct {
+    uint32_t vocab, d, layers, heads, ff, head_layers, act_out, max_len;
+    uint32_t cls, sep, mask, pad;
+    uint64_t capacity, max_rows;
+} omg_laya_config_t;
+
+/* LayaBuilder::new(config_from_export(config.json)) (laya.rs:312-323,
+ * 623-645): the encoder config.json with the agent config under
+ * "laya_agent" and the special token ids under "laya_tokens"
+ * ({"cls_token": id, ...}; the reference resolves surface forms with its
+ * tokenizer, which stays on the caller's side). */
+omg_laya_builder *omg_laya_builder_new(const char *config_json);
+/* LayaBuilder::push (laya.rs:662-709). */
+int omg_laya_builder_push(omg_laya_builder *b, const char *name, int dtype, const int64_t *shape, size_t ndim,
+                          const void *data, size_t nbytes, const void *scales, size_t nscale_bytes);
+/* LayaEngine::new's loop over the catalogue (laya.rs:1115-1124). */
+int omg_laya_builder_push_weights(omg_laya_builder *b, const omg_weights *w);
+/* LayaBuilder::missing (laya.rs:651-660). */
+size_t omg_laya_builder_missing(omg_laya_builder *b, char *buf, size_t len);
+/* LayaBuilder::finish (laya.rs:711-1083); consumes the builder. */
+omg_laya *omg_laya_builder_finish(omg_laya_builder *b, size_t capacity, size_t max_rows);
+void omg_laya_builder_free(omg_laya_builder *b);
+/* Seeded weights for a config (LayaConfig::tensors order, laya.rs:252-305)
+ * from the xorshift of tests/reference.rs:17-38: linears U(-1, 1) /
+ * sqrt(fan-in), embedding U(-1, 1), type embedding x 0.15, norm weights
+ * 1 + U/2, biases U/50; the reference ships no generator for this model. */
+omg_weights *omg_laya_synth(const char *config_json, uint64_t seed, int linear_dtype, int embed_dtype);
+void omg_laya_close(omg_laya *e);
+int omg_laya_config(const omg_laya *e, omg_laya_config_t *out);
+/* LayaEngine::warmup (laya.rs:1126-1135). */
+int omg_laya_warmup(omg_laya *e);
+/* LayaEngine::hidden (laya.rs:1138-1432): per sequence the [CLS] row then
+ * each marker's row, d floats each, dense in sequence order. */
+int omg_laya_hidden(omg_laya *e, const omg_laya_seq *seqs, size_t n, float *out, size_t out_floats);
+/* LayaEngine::evaluate (laya.rs:1435-1485): the scorer's raw logit per
+ * marker, dense in sequence order, and the act probability per sequence
+ * (NaN without an act head). */
+int omg_laya_evaluate(omg_laya *e, const omg_laya_seq *seqs, size_t n, float *logits, size_t nlogits, float *act,
+                      size_t nact);
+/* LayaConfig::temperature_for (laya.rs:234-248). */
+int omg_laya_temperature(const omg_laya *e, int qtype, size_t k, float *out);
+/* Measurement, as omg_pass_prepare / omg_pass_launch / omg_sync / omg_profile. */
+int omg_laya_prepare(omg_laya *e, const omg_laya_seq *seqs, size_t n);
+int omg_laya_launch(omg_laya *e);
+int omg_laya_sync(omg_laya *e);
+int omg_laya_profile(omg_laya *e, int on);
+size_t omg_laya_profile_report(omg_laya *e, char *buf, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

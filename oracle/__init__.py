@@ -43,6 +43,13 @@ class orc_config(C.Structure):
                 ("norm_offset", C.c_float), ("v_norm", C.c_int32), ("softcap", C.c_float), ("bos", C.c_int32)]
 
 
+class orc_laya_config(C.Structure):
+    _fields_ = [("vocab", C.c_int32), ("d", C.c_int32), ("layers", C.c_int32), ("heads", C.c_int32),
+                ("ff", C.c_int32), ("window", C.c_int32), ("head_layers", C.c_int32), ("type_emb", C.c_int32),
+                ("act_hidden", C.c_int32), ("act_out", C.c_int32), ("sliding", C.c_int32 * MAX_LAYERS),
+                ("theta_global", C.c_float), ("theta_local", C.c_float), ("eps", C.c_float)]
+
+
 class orc_branch(C.Structure):
     _fields_ = [("tokens", C.POINTER(C.c_uint32)), ("ntokens", C.c_int64), ("want", C.POINTER(C.c_int64)),
                 ("nwant", C.c_int64)]
@@ -90,6 +97,17 @@ def lib() -> C.CDLL:
             "orc_label_readout": (None, [P, C.c_int64, P, C.c_int64, C.c_float, P, P, C.POINTER(C.c_double)]),
             "orc_pointer_logits": (None, [C.c_int64, C.c_int64, P, P, P, P, P, P, C.c_int64, P]),
             "orc_fold_mean": (None, [C.c_int64, C.c_int64, P, P, C.c_float, P]),
+            "orc_laya_new": (P, [C.POINTER(orc_laya_config)]),
+            "orc_laya_free": (None, [P]),
+            "orc_laya_set": (C.c_int, [P, C.c_char_p, C.c_int, C.c_int64, C.c_int64, P, P]),
+            "orc_laya_missing": (C.c_int, [P, C.c_char_p, C.c_size_t]),
+            "orc_laya_hidden": (C.c_int, [P, P, P, P, C.c_int64, P, C.c_int64, P]),
+            "orc_laya_score": (None, [P, P, C.c_int64, P, P]),
+            "orc_layer_norm": (None, [P, C.c_int64, P, P, C.c_float, P]),
+            "orc_erf": (C.c_float, [C.c_float]),
+            "orc_gelu_erf": (C.c_float, [C.c_float]),
+            "orc_rope_bi": (None, [P, C.c_int32, C.c_float, C.c_float]),
+            "orc_linear": (None, [P, C.c_int64, C.c_int64, P, C.c_int64, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -325,3 +343,120 @@ def fold_mean(orders, logits, excluded: float = -1e4) -> np.ndarray:
     out = np.zeros(k, np.float32)
     lib().orc_fold_mean(k, nruns, _ptr(orders), _ptr(logits), excluded, _ptr(out))
     return out
+
+
+# ------------------------------------------------- bidirectional encoder
+
+def laya_config_from_json(text: str) -> orc_laya_config:
+    """The encoder config.json fields laya.rs:88-206 reads (the agent config
+    under laya_agent)."""
+    v = json.loads(text)
+    a = v.get("laya_agent", {})
+    L = int(v["num_hidden_layers"])
+    if "layer_types" in v:
+        sliding = [t == "sliding_attention" for t in v["layer_types"]]
+    else:
+        every = int(v.get("global_attn_every_n_layers", 3))
+        sliding = [every != 0 and i % every != 0 for i in range(L)]
+    c = orc_laya_config()
+    c.vocab, c.d, c.layers = int(v["vocab_size"]), int(v["hidden_size"]), L
+    c.heads, c.ff = int(v["num_attention_heads"]), int(v["intermediate_size"])
+    c.window = int(v.get("local_attention", 128)) // 2
+    c.head_layers = int(a.get("head_layers", 2))
+    c.type_emb = int(bool(a.get("type_emb", True)))
+    c.act_hidden = 256
+    c.act_out = 0 if a.get("act_head") is False else (len(a.get("act_costs", {})) + 1 if "act_costs" in a else 0)
+    for i in range(L):
+        c.sliding[i] = int(sliding[i])
+    rope = v.get("rope_parameters", {})
+    c.theta_global = float(rope.get("full_attention", {}).get("rope_theta", v.get("global_rope_theta", 160000.0)))
+    c.theta_local = float(rope.get("sliding_attention", {}).get("rope_theta", v.get("local_rope_theta", 10000.0)))
+    c.eps = float(v.get("norm_eps", v.get("layer_norm_eps", 1e-5)))
+    return c
+
+
+class Laya:
+    """orc_laya: the encoder path's CPU restatement (laya.c)."""
+
+    def __init__(self, config_text: str, tensors):
+        self.cfg = laya_config_from_json(config_text)
+        self._h = lib().orc_laya_new(C.byref(self.cfg))
+        if not self._h:
+            raise ValueError("oracle: bad encoder config")
+        for t in tensors:
+            rows, cols = (t.shape[0], t.shape[1]) if len(t.shape) == 2 else (1, t.shape[0])
+            rc = lib().orc_laya_set(self._h, t.name.encode(), t.dtype, rows, cols, _ptr(t.data),
+                                    _ptr(t.scales) if t.scales.size else None)
+            if rc != 0:
+                raise ValueError(f"oracle: cannot set {t.name}")
+        buf = C.create_string_buffer(1 << 16)
+        if lib().orc_laya_missing(self._h, buf, len(buf)):
+            raise ValueError("oracle: missing " + buf.value.decode())
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_laya_free(self._h)
+            self._h = None
+
+    def hidden(self, seqs) -> list[np.ndarray]:
+        """Per sequence (ids, markers, qtype): the [CLS] row then each
+        marker's row, as LayaEngine::hidden returns them."""
+        ids, meta, qt, rows = pack_laya(seqs)
+        out = np.zeros((rows.size, self.cfg.d), np.float32)
+        rc = lib().orc_laya_hidden(self._h, _ptr(ids), _ptr(meta), _ptr(qt), ids.size, _ptr(rows), rows.size,
+                                   _ptr(out))
+        if rc != 0:
+            raise ValueError(f"oracle encoder pass failed ({rc})")
+        res, at = [], 0
+        for s in seqs:
+            n = 1 + len(s[1])
+            res.append(out[at:at + n])
+            at += n
+        return res
+
+    def score(self, rows: np.ndarray) -> tuple[np.ndarray, float]:
+        rows = np.ascontiguousarray(rows, np.float32)
+        k = rows.shape[0] - 1
+        logits = np.zeros(k, np.float32)
+        act = C.c_float(0.0)
+        lib().orc_laya_score(self._h, _ptr(rows), k, _ptr(logits), C.byref(act))
+        return logits, float(act.value)
+
+
+def pack_laya(seqs):
+    """laya.rs:1165-1187: sequences back to back; meta = (position, sequence,
+    first row, last row + 1); rows read back = each sequence's first token,
+    then its markers."""
+    ids, meta, qt, rows = [], [], [], []
+    for si, (tok, markers, qtype) in enumerate(seqs):
+        start = len(ids)
+        for i, t in enumerate(tok):
+            ids.append(t)
+            qt.append(qtype)
+            meta += [i, si, start, start + len(tok)]
+        rows.append(start)
+        rows += [start + m for m in markers]
+    return (np.array(ids, np.uint32), np.array(meta, np.int32), np.array(qt, np.int32), np.array(rows, np.int64))
+
+
+def layer_norm(x, w, b=None, eps: float = 1e-5) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, np.float32)
+    y = np.zeros_like(x)
+    lib().orc_layer_norm(_ptr(x), x.size, _ptr(w), None if bb is None else _ptr(bb), eps, _ptr(y))
+    return y
+
+
+def erf(x: float) -> float:
+    return float(lib().orc_erf(C.c_float(x)))
+
+
+def gelu_erf(x: float) -> float:
+    return float(lib().orc_gelu_erf(C.c_float(x)))
+
+
+def rope_bi(v, pos: int, theta: float, scale: float = 1.0) -> np.ndarray:
+    v = np.array(v, np.float32)
+    lib().orc_rope_bi(_ptr(v), pos, theta, scale)
+    return v

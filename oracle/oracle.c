@@ -317,6 +317,8 @@ static void linear(const float *x, int64_t t, int64_t k, const float *w, int64_t
     }
 }
 
+void orc_linear(const float *x, int64_t t, int64_t k, const float *w, int64_t n, float *y) { linear(x, t, k, w, n, y); }
+
 /* reference.rs:159-168: pairs (i, i + hd/2) for i < rope_dims/2. */
 static void rope(float *v, int64_t hd, int32_t pos, float theta, int64_t rope_dims) {
     int64_t half = hd / 2;

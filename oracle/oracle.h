@@ -20,6 +20,7 @@
  *                       wanted rows, decoded prefixes)
  *   state bytes / key   crates/omg-wgpu/src/engine.rs:510-580 (GRWS1),
  *                       :625-641 (FNV-1a), :1967-1974 (state_rows)
+ *   encoder path        laya.c (crates/omg-wgpu/src/laya.rs hidden + score)
  *   readout math        crates/omg-core/src/math.rs:5-67,
  *                       crates/omg-core/src/readout.rs:30-43,124-146,
  *                       crates/omg-core/src/plan.rs:223-303 (fold)
@@ -126,6 +127,32 @@ void orc_pointer_logits(int64_t d, int64_t dp, const float *w_q, const float *b_
  * logit per original option (EXCLUDED_LOGIT where never asked). */
 void orc_fold_mean(int64_t k, int64_t nruns, const int64_t *orders, const float *logits,
                    float excluded, float *out);
+
+/* ---- bidirectional encoder (laya.c: crates/omg-wgpu/src/laya.rs) ---- */
+typedef struct {
+    int32_t vocab, d, layers, heads, ff, window, head_layers, type_emb, act_hidden, act_out;
+    int32_t sliding[ORC_MAX_LAYERS];
+    float theta_global, theta_local, eps;
+} orc_laya_config;
+typedef struct orc_laya orc_laya;
+orc_laya *orc_laya_new(const orc_laya_config *cfg);
+void orc_laya_free(orc_laya *m);
+int orc_laya_set(orc_laya *m, const char *name, int dtype, int64_t rows, int64_t cols, const uint8_t *data,
+                 const uint8_t *scales);
+int orc_laya_missing(const orc_laya *m, char *buf, size_t len);
+/* x after the head layers at rows[0..nrows) of a packed batch; meta = 4
+ * int32 per token (position, sequence, first row, last row + 1). */
+int orc_laya_hidden(const orc_laya *m, const uint32_t *ids, const int32_t *meta, const int32_t *qtypes, int64_t t,
+                    const int64_t *rows, int64_t nrows, float *out);
+/* The host scorer on one sequence's rows ([CLS], then each marker). */
+void orc_laya_score(const orc_laya *m, const float *rows, int64_t nmarkers, float *logits, float *act);
+/* Pieces, exported for their own pins. */
+void orc_layer_norm(const float *x, int64_t n, const float *w, const float *b, float eps, float *y);
+float orc_erf(float x);
+float orc_gelu_erf(float x);
+void orc_rope_bi(float *v, int32_t pos, float theta, float scale);
+/* y[t][n] = x[t][k] . w[n][k], f32 (reference.rs:150-157). */
+void orc_linear(const float *x, int64_t t, int64_t k, const float *w, int64_t n, float *y);
 
 #ifdef __cplusplus
 }

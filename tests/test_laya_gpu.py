@@ -1,0 +1,336 @@
+"""The bidirectional encoder path (crates/omg-wgpu/src/laya.rs) on the GPU.
+
+Kernel level, through the C ABI: the [q | k | v] projection's epilogue
+(bias, RoPE of rope_bi.wgsl, q scale, the per-head f16 layout) against a
+CPU projection with the same f16 rounding points; the attention kernel
+against a float64 softmax over the same f16 Q/K/V with attention_bi.wgsl's
+visibility (same sequence, |row difference| <= window), on ragged sequence
+layouts; the erf-GELU gated GEMM and the bias + ReLU GEMM.
+
+Engine level: hidden rows (rel 1e-2; the reference's own forward test
+allows 2e-2, crates/omg-wgpu/tests/reference.rs:380-431) and scorer
+outputs against the CPU oracle (oracle/laya.c) on tiny configs and on the mmBERT-base shapes of
+BASELINE.json configs[3] with two layers; the full configs[3] pass (64
+requests x 3 questions of 256 tokens) by the properties the pass must have:
+a sequence's rows do not depend on the other sequences of the batch
+(bit-equal), finite outputs, and the oracle on a sample of its sequences
+through all 22 layers."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import grande_amd as g
+import oracle
+from grande_amd import laya as ly
+from grande_amd.engine import attention_bi
+from tests.common import rel_diff
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def dev(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def qweight(rng, n, k, dtype, scale=1.0, name="w"):
+    v = (rng.uniform(-1, 1, (n, k)) * scale).astype(np.float32)
+    if dtype == g.F16:
+        t = g.QTensor(name, g.F16, (n, k), v.astype(np.float16).view(np.uint8).ravel().copy(), np.zeros(0, np.uint8))
+    else:
+        data, scales = oracle.quantize(dtype, v)
+        t = g.QTensor(name, dtype, (n, k), data, scales)
+    return t, t.to_f32().astype(np.float16).astype(np.float32)
+
+
+def pack_meta(lengths):
+    meta = []
+    at = 0
+    for si, n in enumerate(lengths):
+        for i in range(n):
+            meta += [i, si, at, at + n]
+        at += n
+    return np.array(meta, np.int32).reshape(-1, 4)
+
+
+def rope_table(theta: float, rows: int) -> np.ndarray:
+    inv = np.power(np.float32(theta), -np.arange(0, 64, 2, dtype=np.float32) / np.float32(64)).astype(np.float32)
+    ang = np.arange(rows, dtype=np.float32)[:, None] * inv[None, :]
+    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
+def vt_col32(k):
+    return 8 * ((k % 16) // 4) + 4 * (k // 16) + k % 4
+
+
+def unpack_vt(vt: np.ndarray, heads: int, tpad: int) -> np.ndarray:
+    """[heads][tpad/32][64][32] (key columns by vt_col32) -> [heads][tpad][64]."""
+    v = vt.reshape(heads, tpad // 32, 64, 32)
+    cols = np.array([vt_col32(k) for k in range(32)])
+    return v[:, :, :, cols].transpose(0, 1, 3, 2).reshape(heads, tpad, 64)
+
+
+@pytest.mark.parametrize("lengths,heads,rope,dtype", [([5, 31, 33, 1, 64], 2, True, g.Q8), ([256, 256], 12, True, g.Q8),
+                                                      ([100, 3], 4, False, g.F16), ([70], 1, True, g.Q4),
+                                                      ([200] * 3, 12, False, g.Q8)])
+def test_qkv_heads_epilogue(lengths, heads, rope, dtype):
+    rng = np.random.default_rng(sum(lengths) * heads)
+    t, d = sum(lengths), 64 * heads
+    tpad = (t + 63) // 64 * 64
+    x = rng.uniform(-1, 1, (t, d)).astype(np.float16)
+    wt, wd = qweight(rng, 3 * d, d, dtype, 0.15)
+    bias = (rng.uniform(-1, 1, 3 * d) * 0.2).astype(np.float16)
+    meta = pack_meta(lengths)
+    table = rope_table(10000.0, 512)
+    w = g.DeviceWeight(wt)
+    q = torch.zeros(heads * tpad * 64, dtype=torch.float16, device="cuda")
+    k = torch.zeros_like(q)
+    vt = torch.zeros_like(q)
+    xd, bd, md, rd = dev(x), dev(bias), dev(meta), dev(table)
+    qscale = 0.125 if rope else 1.0
+    w.qkv_heads(xd.data_ptr(), d, t, bd.data_ptr(), rd.data_ptr() if rope else None, md.data_ptr() if rope else None,
+                qscale, tpad, q.data_ptr(), k.data_ptr(), vt.data_ptr())
+    torch.cuda.synchronize()
+    y = x.astype(np.float32) @ wd.T + bias.astype(np.float32)
+    y = y.reshape(t, 3, heads, 64)
+    if rope:
+        cs = table[meta[:, 0]]  # [t][32][2]
+        for s in (0, 1):
+            a, b = y[:, s, :, :32].copy(), y[:, s, :, 32:].copy()
+            c, sn = cs[:, None, :, 0], cs[:, None, :, 1]
+            y[:, s, :, :32] = a * c - b * sn
+            y[:, s, :, 32:] = b * c + a * sn
+    y[:, 0] *= qscale
+    got_q = q.cpu().numpy().reshape(heads, tpad, 64)[:, :t].astype(np.float32)
+    got_k = k.cpu().numpy().reshape(heads, tpad, 64)[:, :t].astype(np.float32)
+    got_v = unpack_vt(vt.cpu().numpy(), heads, tpad)[:, :t].astype(np.float32)
+    for got, sec in ((got_q, 0), (got_k, 1), (got_v, 2)):
+        exp = y[:, sec].transpose(1, 0, 2)
+        assert rel_diff(got, exp) < 2e-3, f"section {sec}"
+
+
+def attention_ref(q, k, v, meta, window):
+    """float64 softmax(q . k) v over the visible keys of each row."""
+    heads, t = q.shape[0], meta.shape[0]
+    out = np.zeros((t, heads * 64))
+    for i in range(t):
+        lo, hi = meta[i, 2], meta[i, 3]
+        if window:
+            lo, hi = max(lo, i - window), min(hi, i + window + 1)
+        for h in range(heads):
+            s = k[h, lo:hi].astype(np.float64) @ q[h, i].astype(np.float64)
+            p = np.exp(s - s.max())
+            out[i, h * 64:(h + 1) * 64] = (p / p.sum()) @ v[h, lo:hi].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("lengths,heads,window", [([5, 31, 33, 1, 64, 100], 2, 0), ([5, 31, 33, 1, 64, 100], 2, 4),
+                                                  ([256, 256, 256], 12, 64), ([256, 256], 3, 0), ([512], 1, 64),
+                                                  ([1], 1, 0), ([37, 91, 128, 7], 2, 16)])
+def test_attention_bi(lengths, heads, window):
+    rng = np.random.default_rng(sum(lengths) + heads + window)
+    t = sum(lengths)
+    tpad = (t + 63) // 64 * 64
+    q = np.zeros((heads, tpad, 64), np.float16)
+    k = np.zeros_like(q)
+    v = np.zeros_like(q)
+    q[:, :t] = rng.normal(0, 0.6, (heads, t, 64))
+    k[:, :t] = rng.normal(0, 0.6, (heads, t, 64))
+    v[:, :t] = rng.normal(0, 1, (heads, t, 64))
+    # V^T tiles with the kernel's key order
+    cols = np.array([vt_col32(kk) for kk in range(32)])
+    vt = np.zeros((heads, tpad // 32, 64, 32), np.float16)
+    vt[:, :, :, cols] = v.reshape(heads, tpad // 32, 32, 64).transpose(0, 1, 3, 2)
+    meta = pack_meta(lengths)
+    out = torch.zeros((t, heads * 64), dtype=torch.float16, device="cuda")
+    qd, kd, vd, md = dev(q), dev(k), dev(vt), dev(meta)
+    attention_bi(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), md.data_ptr(), heads, t, tpad, window, out.data_ptr())
+    torch.cuda.synchronize()
+    exp = attention_ref(q[:, :t], k[:, :t], v[:, :t], meta, window)
+    got = out.cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    assert np.max(np.abs(got - exp)) < 8e-3, f"max |d| {np.max(np.abs(got - exp))}"
+
+
+def gelu_erf(x):
+    from math import erf
+    return 0.5 * x * (1.0 + np.vectorize(erf)(x / np.sqrt(2.0)))
+
+
+@pytest.mark.parametrize("m,n,k", [(77, 96, 96), (600, 1152, 768), (2048, 1152, 768), (130, 200, 64)])
+def test_gemm_geglu_erf(m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    x = rng.uniform(-1, 1, (m, k)).astype(np.float16)
+    tg, gd = qweight(rng, n, k, g.Q8, 1.0, "gate")
+    tu, ud = qweight(rng, n, k, g.Q8, 1.0, "up")
+    wg, wu = g.DeviceWeight(tg), g.DeviceWeight(tu)
+    act = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+    xd = dev(x)
+    wg.gemm_geglu_erf(wu, xd.data_ptr(), k, m, act.data_ptr(), n)
+    torch.cuda.synchronize()
+    xf = x.astype(np.float64)
+    exp = gelu_erf(xf @ gd.T) * (xf @ ud.T)
+    got = act.cpu().numpy().astype(np.float64)
+    assert np.max(np.abs(got - exp) / np.maximum(np.abs(exp), 1.0)) < 2e-3
+
+
+@pytest.mark.parametrize("m,n,k", [(77, 96, 96), (600, 3072, 768), (1000, 640, 64)])
+def test_gemm_bias_relu(m, n, k):
+    rng = np.random.default_rng(m * 3 + n + k)
+    x = rng.uniform(-1, 1, (m, k)).astype(np.float16)
+    t, wd = qweight(rng, n, k, g.Q8, 1.0)
+    bias = rng.uniform(-2, 2, n).astype(np.float16)
+    w = g.DeviceWeight(t)
+    y = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+    xd, bd = dev(x), dev(bias)
+    w.gemm_bias_relu(xd.data_ptr(), k, m, bd.data_ptr(), y.data_ptr(), n)
+    torch.cuda.synchronize()
+    exp = np.maximum(x.astype(np.float64) @ wd.T + bias.astype(np.float64), 0.0)
+    got = y.cpu().numpy().astype(np.float64)
+    assert np.max(np.abs(got - exp) / np.maximum(np.abs(exp), 1.0)) < 2e-3
+    assert (got >= 0).all()
+
+
+# ------------------------------------------------------------- engine level
+
+def tiny(**over) -> str:
+    kw = dict(vocab=300, d=128, layers=3, heads=2, ff=192, local_attention=8, head_layers=2,
+              act_costs={"ask": 1.0, "wait": 0.5}, cls=1, sep=2, mask=4, pad=0)
+    kw.update(over)
+    return ly.laya_config_json(**kw)
+
+
+def random_seqs(rng, vocab, n, lo, hi, mask=4, cls=1, sep=2):
+    seqs = []
+    for i in range(n):
+        length = int(rng.integers(lo, hi + 1))
+        ids = rng.integers(5, vocab, length).tolist()
+        ids[0], ids[-1] = cls, sep
+        k = int(rng.integers(1, 4)) if length > 4 else 1
+        markers = sorted(rng.choice(np.arange(1, max(2, length - 1)), size=min(k, max(1, length - 2)),
+                                    replace=False).tolist())
+        for m in markers:
+            ids[m] = mask
+        seqs.append(ly.Sequence(ids, markers, int(rng.integers(0, 3))))
+    return seqs
+
+
+def engine_and_oracle(cfg, seed, dtype, capacity, max_rows):
+    w = ly.synth_weights(cfg, seed, dtype, dtype)
+    eng = ly.LayaEngine.new(w, capacity, max_rows)
+    return eng, oracle.Laya(cfg, list(w.tensors()))
+
+
+@pytest.mark.parametrize("dtype", [g.Q8, g.Q4, g.F16])
+def test_tiny_hidden_and_scores_match_oracle(dtype):
+    cfg = tiny()
+    eng, orc = engine_and_oracle(cfg, 11, dtype, 1024, 64)
+    rng = np.random.default_rng(3)
+    seqs = random_seqs(rng, 300, 9, 3, 120)
+    got = eng.hidden(seqs)
+    exp = orc.hidden([(s.ids, s.markers, s.qtype) for s in seqs])
+    worst = max(rel_diff(a, b) for a, b in zip(got, exp))
+    assert worst < 1e-2, worst
+    outs = eng.evaluate(seqs)
+    for s, o, e in zip(seqs, outs, exp):
+        lg, act = orc.score(e)
+        assert o.logits.shape == (len(s.markers),)
+        assert np.max(np.abs(o.logits - lg)) < 2e-2 * max(1.0, float(np.max(np.abs(lg))))
+        assert o.act_probability is not None and abs(o.act_probability - act) < 2e-2
+
+
+def test_sequence_rows_do_not_depend_on_the_batch():
+    cfg = tiny(layers=4, local_attention=16)
+    w = ly.synth_weights(cfg, 5, g.Q8, g.Q8)
+    eng = ly.LayaEngine.new(w, 2048, 64)
+    rng = np.random.default_rng(9)
+    seqs = random_seqs(rng, 300, 12, 2, 150)
+    together = eng.hidden(seqs)
+    for i in (0, 5, 11):
+        alone = eng.hidden([seqs[i]])
+        assert np.array_equal(alone[0], together[i]), f"sequence {i}"
+    rev = eng.hidden(seqs[::-1])
+    for a, b in zip(rev, together[::-1]):
+        assert np.array_equal(a, b)
+
+
+def test_no_head_layers_and_no_type_embedding():
+    cfg = tiny(head_layers=0, type_emb=False, act_costs=None)
+    eng, orc = engine_and_oracle(cfg, 2, g.Q8, 512, 32)
+    seqs = random_seqs(np.random.default_rng(4), 300, 4, 10, 60)
+    got = eng.hidden(seqs)
+    exp = orc.hidden([(s.ids, s.markers, s.qtype) for s in seqs])
+    assert max(rel_diff(a, b) for a, b in zip(got, exp)) < 1e-2
+    assert all(o.act_probability is None for o in eng.evaluate(seqs))
+
+
+def test_request_errors():
+    cfg = tiny()
+    w = ly.synth_weights(cfg, 1, g.Q8, g.Q8)
+    eng = ly.LayaEngine.new(w, 256, 8)
+    with pytest.raises(g.OmgError, match="empty"):
+        eng.hidden([ly.Sequence([], [], 0)])
+    with pytest.raises(g.OmgError, match="capacity"):
+        eng.hidden([ly.Sequence([1] * 200, [3], 0), ly.Sequence([1] * 100, [3], 0)])
+    with pytest.raises(g.OmgError, match="marker"):
+        eng.hidden([ly.Sequence([1, 4, 2], [7], 0)])
+    with pytest.raises(g.OmgError, match="vocabulary"):
+        eng.hidden([ly.Sequence([1, 4000, 2], [1], 0)])
+    with pytest.raises(g.OmgError, match="question type"):
+        eng.hidden([ly.Sequence([1, 4, 2], [1], 3)])
+    with pytest.raises(g.OmgError, match="rows"):
+        eng.hidden([ly.Sequence([1, 4, 4, 4, 4, 4, 4, 4, 4, 2], list(range(1, 9)), 0)])
+    eng.warmup()
+
+
+def c4_seqs(rng, requests, questions, seq_len, vocab):
+    seqs = []
+    for r in range(requests * questions):
+        ids = rng.integers(5, vocab, seq_len).tolist()
+        ids[0], ids[-1] = 1, 2
+        m = int(rng.integers(8, seq_len - 8))
+        ids[m] = 4
+        seqs.append(ly.Sequence(ids, [m], r % 3))
+    return seqs
+
+
+def c4_config(**over) -> str:
+    m = dict(ly.MMBERT_BASE)
+    m.update(over)
+    return ly.laya_config_json(**m, head_layers=2, act_costs={"ask": 1.0, "escalate": 2.0}, cls=1, sep=2, mask=4, pad=0)
+
+
+def test_c4_shapes_two_layers_match_oracle():
+    """configs[3]'s shapes (d 768, 12 heads of 64, ff 1152, window 64,
+    56,000-token vocabulary, Q8) with two encoder layers (global, local)."""
+    cfg = c4_config(layers=2)
+    eng, orc = engine_and_oracle(cfg, 0x5EED, g.Q8, 4 * 256, 8)
+    seqs = c4_seqs(np.random.default_rng(1), 1, 3, 256, 56_000)
+    got = eng.hidden(seqs)
+    exp = orc.hidden([(s.ids, s.markers, s.qtype) for s in seqs])
+    assert max(rel_diff(a, b) for a, b in zip(got, exp)) < 1e-2
+    for o, e in zip(eng.evaluate(seqs), exp):
+        lg, act = orc.score(e)
+        assert np.max(np.abs(o.logits - lg)) < 2e-2 * max(1.0, float(np.max(np.abs(lg))))
+
+
+def test_c4_full_pass_properties():
+    """64 requests x 3 questions of 256 tokens (49,152 tokens)
+    through all 22 layers; a sample of sequences checked by the oracle and
+    by isolation."""
+    spec = ly.C4
+    cfg = c4_config()
+    w = ly.synth_weights(cfg, 0x5EED, g.Q8, g.Q8)
+    n = spec["requests"] * spec["questions"]
+    eng = ly.LayaEngine.new(w, n * spec["seq_len"], 2 * n)
+    seqs = c4_seqs(np.random.default_rng(2), spec["requests"], spec["questions"], spec["seq_len"], 56_000)
+    outs = eng.evaluate(seqs)
+    assert len(outs) == n and all(np.isfinite(o.logits).all() for o in outs)
+    rows = eng.hidden(seqs)
+    sample = [0, 97, n - 1]
+    for i in sample:
+        assert np.array_equal(eng.hidden([seqs[i]])[0], rows[i]), f"sequence {i} isolation"
+    orc = oracle.Laya(cfg, list(w.tensors()))
+    exp = orc.hidden([(seqs[i].ids, seqs[i].markers, seqs[i].qtype) for i in sample[:1]])
+    assert rel_diff(rows[sample[0]], exp[0]) < 1e-2
