@@ -474,6 +474,10 @@ static void run(hipStream_t s, const GemmArgs& g) {
 //   narrow outputs (N <= 1280, the o and down projections): 64 x 64,
 //   96 x 64 from N = 768, four slots;
 //   wide outputs (the qkv projection): 128 x 64, 96 x 128 for K >= 4096.
+//   Long passes (M >= 8192, the encoder's 49,152-token batches; tile
+//   count is no constraint): 192 x 128, the best of the measured shapes
+//   for every linear of the mmBERT-base encoder; the q/k/v head scatter
+//   needs 64 weight rows per wave: 96 x 256.
 //   Gated: 160 x 128 weight rows (64 output columns; a 2,384-token pass
 //   of the 270M model is 480 tiles, at most two per CU, where 128-row
 //   tiles made 608 and left 96 CUs a third), 128 x 256 with three slots
@@ -483,9 +487,10 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
     const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
     if constexpr (EPI == EPI_QKV) {
         if (M <= 512) return run<QUANT, 2, 4, EPI, 4, 4>(s, g);
-        return run<QUANT, 8, 4, EPI, 2, 4>(s, g);
+        return run<QUANT, 6, 4, EPI, 2, 4>(s, g);
     } else if constexpr (EPI == EPI_F32 || EPI == EPI_RELU_F16) {
         if (M <= 512) return run<QUANT, 2, 1, EPI, 4, 2>(s, g);
+        if (M >= 8192) return run<QUANT, 12, 2, EPI, 2, 4>(s, g);
         if (N <= 1280) {
             if (N > 768) return run<QUANT, 6, 1, EPI, 4, 4>(s, g);
             return run<QUANT, 4, 1, EPI, 4, 4>(s, g);
@@ -495,6 +500,7 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
     } else {
         if (M <= 512) return run<QUANT, 4, 2, EPI, 2, 4>(s, g);
         if (N >= 8192) return run<QUANT, 8, 4, EPI, 3, 4>(s, g);
+        if (M >= 8192) return run<QUANT, 12, 2, EPI, 2, 4>(s, g);
         return run<QUANT, 10, 2, EPI, 2, 4>(s, g);
     }
 }
