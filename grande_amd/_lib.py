@@ -118,6 +118,8 @@ _SIGS = {
     "omg_laya_builder_free": (None, [_P]),
     "omg_laya_synth": (_P, [C.c_char_p, C.c_uint64, C.c_int, C.c_int]),
     "omg_laya_close": (None, [_P]),
+    "omg_laya_open_dir": (_P, [C.c_char_p, _P, C.c_size_t, C.c_size_t]),
+    "omg_laya_load_dir": (_P, [C.c_char_p, _P]),
     "omg_laya_config": (C.c_int, [_P, C.POINTER(omg_laya_config_t)]),
     "omg_laya_warmup": (C.c_int, [_P]),
     "omg_laya_hidden": (C.c_int, [_P, C.POINTER(omg_laya_seq), C.c_size_t, C.POINTER(C.c_float), C.c_size_t]),

@@ -543,6 +543,33 @@ omg_weights* omg_laya_synth(const char* config_json, uint64_t seed, int linear_d
     return out;
 }
 
+omg_weights* omg_laya_load_dir(const char* dir, const uint32_t* special_ids) {
+    omg_weights* out = nullptr;
+    guard([&] {
+        if (!dir) omg::fail(omg::E_INVALID, "null dir");
+        omg::LayaWeights lw = omg::load_laya_dir(dir, special_ids);
+        auto w = std::make_unique<omg_weights>();
+        w->tensors = std::move(lw.tensors);
+        w->index(lw.config.tensors());
+        out = w.release();
+    });
+    return out;
+}
+
+omg_laya* omg_laya_open_dir(const char* dir, const uint32_t* special_ids, size_t capacity, size_t max_rows) {
+    omg_laya* out = nullptr;
+    guard([&] {
+        if (!dir) omg::fail(omg::E_INVALID, "null dir");
+        omg::LayaWeights lw = omg::load_laya_dir(dir, special_ids);
+        omg::LayaBuilder b(lw.config);
+        for (const auto& kv : lw.tensors) b.push(kv.first, kv.second);
+        auto e = b.finish(int64_t(capacity), int64_t(max_rows));
+        e->warmup();
+        out = new omg_laya{std::move(e)};
+    });
+    return out;
+}
+
 void omg_laya_close(omg_laya* e) { delete e; }
 
 }  // extern "C"

@@ -256,6 +256,26 @@ LayaWeights synth_laya(const LayaConfig& cfg, uint64_t seed, Dtype linear, Dtype
     return w;
 }
 
+LayaWeights load_laya_dir(const std::string& dir, const uint32_t* special) {
+    Json v = Json::parse(read_file(dir + "/config.json"));
+    if (special) {
+        static const char* names[4] = {"cls_token", "sep_token", "mask_token", "pad_token"};
+        Json tok;
+        tok.kind = Json::Object;
+        for (int i = 0; i < 4; ++i) {
+            Json id;
+            id.kind = Json::Number;
+            id.num = double(special[i]);
+            tok.obj[names[i]] = id;
+        }
+        v.obj["laya_tokens"] = tok;
+    }
+    LayaWeights w;
+    w.config = LayaConfig::from_json(v);
+    w.tensors = read_manifest(dir);
+    return w;
+}
+
 // ----------------------------------------------------------------- builder
 
 LayaBuilder::LayaBuilder(LayaConfig cfg) : cfg_(std::move(cfg)) {

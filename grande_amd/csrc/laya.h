@@ -62,6 +62,12 @@ struct LayaWeights {
 // has no generator for this model.)
 LayaWeights synth_laya(const LayaConfig& cfg, uint64_t seed, Dtype linear, Dtype embed);
 
+// An exported directory (laya.rs:61-91 with tools/export_laya.py's layout:
+// config.json with laya_agent, manifest.json, *.bin).  `special` (cls,
+// sep, mask, pad), when given, replaces the config's laya_tokens: the
+// reference resolves those surface forms with its tokenizer.
+LayaWeights load_laya_dir(const std::string& dir, const uint32_t* special);
+
 // One question's sequence (laya.rs:468-476).
 struct LayaSeq {
     const uint32_t* ids;

@@ -331,6 +331,12 @@ Weights load_dir(const std::string& dir) {
     Weights w;
     w.config = Config::from_json(Json::parse(read_file(dir + "/config.json")));
     w.config.validate();
+    w.tensors = read_manifest(dir);
+    return w;
+}
+
+std::map<std::string, QTensor> read_manifest(const std::string& dir) {
+    std::map<std::string, QTensor> out;
     const Json man = Json::parse(read_file(dir + "/manifest.json"));
     if (man["files"].kind != Json::Array) fail(E_INVALID, "manifest.json: missing files");
     for (const Json& file : man["files"].arr) {
@@ -356,10 +362,10 @@ Weights load_dir(const std::string& dir) {
             if (int64_t(t.scales.size()) != want_scales)
                 fail(E_INVALID, name + ": " + std::to_string(t.scales.size()) + " scale bytes, expected " +
                                     std::to_string(want_scales));
-            w.tensors[name] = std::move(t);
+            out[name] = std::move(t);
         }
     }
-    return w;
+    return out;
 }
 
 }  // namespace omg

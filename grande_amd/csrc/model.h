@@ -89,6 +89,8 @@ Weights synth_weights(const Config& cfg, uint64_t seed, Dtype linear, Dtype embe
 // model.rs:742-795 + tools/export_wgpu_gguf.py: config.json + manifest.json
 // + *.bin.  Reads every catalogued tensor of an exported directory.
 Weights load_dir(const std::string& dir);
+// The tensors of an exported directory's manifest.json + *.bin files.
+std::map<std::string, QTensor> read_manifest(const std::string& dir);
 
 std::string read_file(const std::string& path);
 

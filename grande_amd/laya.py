@@ -91,6 +91,21 @@ def synth_weights(config: str, seed: int, linear: int, embed: int) -> Weights:
     return Weights(h, config)
 
 
+def _special(special):
+    if special is None:
+        return None
+    arr = (C.c_uint32 * 4)(*special)
+    return arr
+
+
+def load_dir(path, special=None) -> Weights:
+    """An exported directory's tensors (omg_laya_load_dir); `special` =
+    (cls, sep, mask, pad) ids replaces the config's laya_tokens."""
+    from pathlib import Path
+    h = L.handle(L.lib().omg_laya_load_dir(str(path).encode(), _special(special)))
+    return Weights(h, (Path(path) / "config.json").read_text())
+
+
 class _CSeqs:
     def __init__(self, seqs: Seq[Sequence]):
         self.keep = []
@@ -148,6 +163,11 @@ class LayaEngine:
         self.d, self.capacity, self.max_rows = cfg.d, cfg.capacity, cfg.max_rows
         self.act_out = cfg.act_out
         self.cls, self.sep, self.mask = cfg.cls, cfg.sep, cfg.mask
+
+    @classmethod
+    def open_dir(cls, path, capacity: int, max_rows: int, special=None) -> "LayaEngine":
+        """LayaBackend::load of an exported directory (omg_laya_open_dir)."""
+        return cls(L.handle(L.lib().omg_laya_open_dir(str(path).encode(), _special(special), capacity, max_rows)))
 
     @classmethod
     def new(cls, weights: Weights, capacity: int, max_rows: int) -> "LayaEngine":

@@ -272,6 +272,15 @@ void omg_laya_builder_free(omg_laya_builder *b);
  * sqrt(fan-in), embedding U(-1, 1), type embedding x 0.15, norm weights
  * 1 + U/2, biases U/50; the reference ships no generator for this model. */
 omg_weights *omg_laya_synth(const char *config_json, uint64_t seed, int linear_dtype, int embed_dtype);
+/* LayaBackend::load for an exported directory (laya/backend.rs:61-91,
+ * tools/export_laya.py): config.json (encoder config + laya_agent +
+ * laya_tokens), manifest.json, *.bin; the engine is warmed up
+ * (laya.rs:1126-1135).  special_ids (cls, sep, mask, pad), when not NULL,
+ * replace laya_tokens: the reference resolves their surface forms with
+ * the checkpoint's tokenizer, which stays with the caller. */
+omg_laya *omg_laya_open_dir(const char *dir, const uint32_t *special_ids, size_t capacity, size_t max_rows);
+/* The same directory's tensors as a host checkpoint. */
+omg_weights *omg_laya_load_dir(const char *dir, const uint32_t *special_ids);
 void omg_laya_close(omg_laya *e);
 int omg_laya_config(const omg_laya *e, omg_laya_config_t *out);
 /* LayaEngine::warmup (laya.rs:1126-1135). */

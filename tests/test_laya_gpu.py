@@ -334,3 +334,16 @@ def test_c4_full_pass_properties():
     orc = oracle.Laya(cfg, list(w.tensors()))
     exp = orc.hidden([(seqs[i].ids, seqs[i].markers, seqs[i].qtype) for i in sample[:1]])
     assert rel_diff(rows[sample[0]], exp[0]) < 1e-2
+
+
+def test_open_exported_directory(tmp_path):
+    """LayaBackend::load's exported-directory path: the engine opened from
+    disk gives the rows of the engine built from the same weights."""
+    cfg = tiny(layers=2)
+    w = ly.synth_weights(cfg, 17, g.Q8, g.Q8)
+    g.export_dir(w, tmp_path)
+    a = ly.LayaEngine.new(w, 512, 16)
+    b = ly.LayaEngine.open_dir(tmp_path, 512, 16)
+    seqs = random_seqs(np.random.default_rng(6), 300, 3, 20, 90)
+    for x, y in zip(a.hidden(seqs), b.hidden(seqs)):
+        assert np.array_equal(x, y)

@@ -141,3 +141,24 @@ def test_config_model_type_and_token_ids():
     del v["laya_tokens"]["mask_token"]
     with pytest.raises(g.OmgError, match="mask_token"):
         ly.LayaBuilder(json.dumps(v))
+
+
+def test_exported_directory_round_trip(tmp_path):
+    """tools/export_laya.py's layout (config.json with laya_agent,
+    manifest.json, *.bin) read back bit-exactly; special ids given by the
+    caller replace laya_tokens (the reference resolves them with its
+    tokenizer)."""
+    cfg = tiny(layers=2, head_layers=1)
+    w = ly.synth_weights(cfg, 13, g.Q8, g.Q4)
+    g.export_dir(w, tmp_path)
+    back = {t.name: t for t in ly.load_dir(tmp_path).tensors()}
+    for t in w.tensors():
+        b = back[t.name]
+        assert (b.dtype, b.shape) == (t.dtype, t.shape)
+        assert np.array_equal(b.data, t.data) and np.array_equal(b.scales, t.scales)
+    v = json.loads(cfg)
+    v["laya_tokens"] = {"cls_token": "[CLS]", "sep_token": "[SEP]", "mask_token": "[MASK]", "pad_token": "[PAD]"}
+    (tmp_path / "config.json").write_text(json.dumps(v))
+    with pytest.raises(g.OmgError, match="cls_token"):
+        ly.load_dir(tmp_path)
+    assert len(ly.load_dir(tmp_path, special=(1, 2, 4, 0))) == len(back)
