@@ -162,3 +162,29 @@ def test_exported_directory_round_trip(tmp_path):
     with pytest.raises(g.OmgError, match="cls_token"):
         ly.load_dir(tmp_path)
     assert len(ly.load_dir(tmp_path, special=(1, 2, 4, 0))) == len(back)
+
+
+def test_oracle_matches_transformers_modernbert():
+    """tests/golden/hf_modernbert.npz (make_hf_modernbert.py): transformers'
+    ModernBertModel, torch's TransformerEncoderLayer with the reference's
+    unscaled head attention, and the scorer as nn.Sequential, all in
+    float64 on the same seeded weights.  The oracle carries the GPU path's
+    f16 rounding points, hence 2e-3.  A planted mistake (window 5 instead
+    of 4 on the local layers) misses by far more."""
+    from pathlib import Path
+    z = np.load(Path(__file__).resolve().parent / "golden" / "hf_modernbert.npz")
+    seqs = [tuple(s) for s in json.loads(bytes(z["seqs"]).decode())]
+    for v in ("enc", "full"):
+        cfg = bytes(z[f"{v}_config"]).decode()
+        ts = list(ly.synth_weights(cfg, int(z["seed"][0]), g.Q8, g.Q8).tensors())
+        orc = oracle.Laya(cfg, ts)
+        rows = orc.hidden(seqs)
+        exp = z[f"{v}_rows"]
+        got = np.concatenate(rows)
+        assert np.abs(got - exp).max() / np.abs(exp).max() < 2e-3, v
+        logits = np.concatenate([orc.score(r)[0] for r in rows])
+        assert np.abs(logits - z[f"{v}_logits"]).max() < 2e-3, v
+        wrong = json.loads(cfg)
+        wrong["local_attention"] = 10
+        bad = np.concatenate(oracle.Laya(json.dumps(wrong), ts).hidden(seqs))
+        assert np.abs(bad - exp).max() / np.abs(exp).max() > 1e-2, v
