@@ -114,13 +114,14 @@ __device__ inline float gelu_tanh(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_ = 4>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_ = 4, int WM_ = 1>
 struct Cfg {
     static constexpr bool GATED = EPI == EPI_GELU_TANH || EPI == EPI_GELU_ERF;
     static constexpr int NW = NW_, T = NW * WAVE;
-    static constexpr int BM = 16 * MI;
+    static constexpr int WM = WM_, WN = NW / WM;       // waves along M and along N
+    static constexpr int BM = 16 * MI * WM;
     static constexpr int WR = 16 * NJ;                 // weight rows per wave
-    static constexpr int BNW = NW * WR;                // weight rows per tile
+    static constexpr int BNW = WN * WR;                // weight rows per tile
     static constexpr int BN = GATED ? BNW / 2 : BNW;   // output columns per tile
     static constexpr int X_CH = BM * 8, X_I = (X_CH + T - 1) / T;  // padded lanes go out of range
     static constexpr int W_CPR = QUANT == Q4_DT ? 2 : (QUANT == Q8_DT ? 4 : 8);
@@ -134,18 +135,22 @@ struct Cfg {
     static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
     static_assert(BN % 64 == 0 || !GATED, "a scale DMA instruction must stay in one matrix");
     static_assert(NS >= 2, "ring needs >= 2 slots");
+    static_assert(NW % WM == 0, "waves split evenly over M");
     static_assert(C <= 63, "vmcnt range");
     static_assert(EPI != EPI_QKV || WR == 64, "the Q/K/V epilogue gives each wave one 64-wide head");
 };
 
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_, int WM_>
 __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
-    using P = Cfg<QUANT, MI, NJ, EPI, NS, NW_>;
+    using P = Cfg<QUANT, MI, NJ, EPI, NS, NW_, WM_>;
     constexpr bool GATED = P::GATED;
     constexpr int NW = P::NW, BM = P::BM, BN = P::BN, WR = P::WR;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = int(threadIdx.x), lane = tid % WAVE;
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    // The wave's place in the tile: activation row blocks wm * MI .. + MI,
+    // weight rows of block column wn.
+    const int wn = wave % P::WN, wm = wave / P::WN;
 
     // Workgroups are dispatched round-robin over the 8 XCDs (each with its
     // own L2): workgroup b runs on XCD b % 8.  Give each XCD a contiguous run
@@ -259,9 +264,9 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     // Tile-local weight row of this wave's row block j.
     auto wrow_of = [&](int j) {
         if constexpr (GATED)
-            return j < NJ / 2 ? wave * (WR / 2) + 16 * j : BN + wave * (WR / 2) + 16 * (j - NJ / 2);
+            return j < NJ / 2 ? wn * (WR / 2) + 16 * j : BN + wn * (WR / 2) + 16 * (j - NJ / 2);
         else
-            return wave * WR + 16 * j;
+            return wn * WR + 16 * j;
     };
 
     floatx4 acc[MI][NJ];
@@ -294,7 +299,8 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int i = 0; i < MI; ++i) xf[ks][i] = *reinterpret_cast<const half8*>(X + i * 16 * G_ROW + foff[ks]);
+            for (int i = 0; i < MI; ++i)
+                xf[ks][i] = *reinterpret_cast<const half8*>(X + (wm * MI + i) * 16 * G_ROW + foff[ks]);
         uint32_t sc[NJ];
         uint2 code[2][NJ];  // Q4: .x only; Q8: both words
         half8 wf16[2][NJ];
@@ -344,7 +350,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
         // the tile edges are multiples of 64).  RoPE pairs dims (c, c + 32),
         // which sit in blocks j and j + 2 of the same lane.
         const QkvHeads& o = g.qkv;
-        const int64_t c0 = n0 + wave * WR;
+        const int64_t c0 = n0 + wn * WR;
         if (c0 >= N) return;
         const int sec = int(c0 / o.dq);
         const int64_t head = (c0 % o.dq) / 64;
@@ -356,7 +362,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
                 bias[j][r] = g.bias ? float(__builtin_bit_cast(half_t, g.bias[c0 + 16 * j + 4 * lg + r])) : 0.0f;
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
-            const int64_t m = m0 + i * 16 + lr;
+            const int64_t m = m0 + (wm * MI + i) * 16 + lr;
             if (m >= M) continue;
             float v[NJ][4];
 #pragma unroll
@@ -394,7 +400,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
         return;
     }
     constexpr int NO = GATED ? NJ / 2 : NJ;
-    const int64_t nw0 = n0 + (GATED ? wave * (WR / 2) : wave * WR);
+    const int64_t nw0 = n0 + (GATED ? wn * (WR / 2) : wn * WR);
     float cbias[EPI == EPI_RELU_F16 ? NO : 1][4];
     if constexpr (EPI == EPI_RELU_F16) {
 #pragma unroll
@@ -407,7 +413,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     }
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-        const int64_t m = m0 + i * 16 + lr;
+        const int64_t m = m0 + (wm * MI + i) * 16 + lr;
         if (m >= M) continue;
 #pragma unroll
         for (int j = 0; j < NO; ++j) {
@@ -447,19 +453,19 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     }
 }
 
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4, int WM = 1>
 static void run(hipStream_t s, const GemmArgs& g) {
-    using P = Cfg<QUANT, MI, NJ, EPI, NS, NW>;
+    using P = Cfg<QUANT, MI, NJ, EPI, NS, NW, WM>;
     static bool lds_set = false;
     if (!lds_set) {
-        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<QUANT, MI, NJ, EPI, NS, NW>),
+        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<QUANT, MI, NJ, EPI, NS, NW, WM>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
         lds_set = true;
     }
     const int64_t N = g.w0.rows;
     const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + P::BM - 1) / P::BM);
     const dim3 grid(unsigned((tiles + 7) / 8 * 8));
-    gemm_kernel<QUANT, MI, NJ, EPI, NS, NW><<<grid, dim3(P::T), P::LDS, s>>>(g);
+    gemm_kernel<QUANT, MI, NJ, EPI, NS, NW, WM><<<grid, dim3(P::T), P::LDS, s>>>(g);
     OMG_HIP(hipGetLastError());
 }
 
@@ -474,6 +480,9 @@ static void run(hipStream_t s, const GemmArgs& g) {
 //   narrow outputs (N <= 1280, the o and down projections): 64 x 64,
 //   96 x 64 from N = 768, four slots;
 //   wide outputs (the qkv projection): 128 x 64, 96 x 128 for K >= 4096.
+//   Tiles whose waves also split the activation rows (WM > 1: each wave
+//   reads fewer X fragments per MFMA) measured no faster at any of these
+//   shapes, so every dispatch keeps WM = 1.
 //   Long passes (M >= 8192, the encoder's 49,152-token batches; tile
 //   count is no constraint): 192 x 128, the best of the measured shapes
 //   for every linear of the mmBERT-base encoder; the q/k/v head scatter
