@@ -60,6 +60,8 @@ _SIGS = {
                                    C.c_size_t]),
     "omg_synth": (_P, [C.c_char_p, C.c_uint64, C.c_int, C.c_int]),
     "omg_load_dir": (_P, [C.c_char_p]),
+    "omg_load_gguf": (_P, [C.c_char_p]),
+    "omg_open_gguf": (_P, [C.c_char_p, C.c_size_t, C.c_size_t]),
     "omg_weights_count": (C.c_size_t, [_P]),
     "omg_weights_get": (C.c_int, [_P, C.c_size_t, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_int64),
                                   C.POINTER(C.c_size_t), C.POINTER(_P), C.POINTER(C.c_size_t), C.POINTER(_P),

@@ -156,6 +156,31 @@ omg_weights* omg_load_dir(const char* dir) {
     return out;
 }
 
+omg_weights* omg_load_gguf(const char* path) {
+    omg_weights* out = nullptr;
+    guard([&] {
+        if (!path) omg::fail(omg::E_INVALID, "null path");
+        auto w = std::make_unique<omg_weights>();
+        omg::Weights loaded = omg::load_gguf(path);
+        w->tensors = std::move(loaded.tensors);
+        w->index(loaded.config.tensors());
+        out = w.release();
+    });
+    return out;
+}
+
+omg_engine* omg_open_gguf(const char* path, size_t capacity, size_t max_rows) {
+    omg_engine* out = nullptr;
+    guard([&] {
+        if (!path) omg::fail(omg::E_INVALID, "null path");
+        omg::Weights w = omg::load_gguf(path);
+        omg::Builder b(w.config);
+        for (const auto& kv : w.tensors) b.push(kv.first, kv.second);
+        out = new omg_engine{b.finish(int64_t(capacity), int64_t(max_rows))};
+    });
+    return out;
+}
+
 size_t omg_weights_count(const omg_weights* w) { return w ? w->order.size() : 0; }
 
 int omg_weights_get(const omg_weights* w, size_t i, const char** name, int* dtype, int64_t* shape, size_t* ndim,

@@ -89,6 +89,11 @@ Weights synth_weights(const Config& cfg, uint64_t seed, Dtype linear, Dtype embe
 // model.rs:742-795 + tools/export_wgpu_gguf.py: config.json + manifest.json
 // + *.bin.  Reads every catalogued tensor of an exported directory.
 Weights load_dir(const std::string& dir);
+// A llama.cpp GGUF file (v2/v3, gemma3): its metadata as the text config
+// and its tensors in the catalogue's names, as
+// tools/export_wgpu_gguf.py:112-296 maps them (q / k / v fused).
+Weights load_gguf(const std::string& path);
+
 // The tensors of an exported directory's manifest.json + *.bin files.
 std::map<std::string, QTensor> read_manifest(const std::string& dir);
 

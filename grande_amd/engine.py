@@ -154,6 +154,11 @@ class Engine:
         """backend.rs:28-71 (an exported directory)."""
         return cls(L.handle(L.lib().omg_open_dir(str(path).encode(), capacity, max_rows)))
 
+    @classmethod
+    def open_gguf(cls, path: str | Path, capacity: int, max_rows: int) -> "Engine":
+        """A llama.cpp GGUF file read directly (omg_open_gguf)."""
+        return cls(L.handle(L.lib().omg_open_gguf(str(path).encode(), capacity, max_rows)))
+
     def close(self) -> None:
         lib = getattr(L, "_lib", None)
         if lib is not None and getattr(self, "_h", None):

@@ -128,6 +128,12 @@ class Weights:
         h = L.handle(L.lib().omg_load_dir(str(path).encode()))
         return cls(h, (Path(path) / "config.json").read_text())
 
+    @classmethod
+    def load_gguf(cls, path: str | Path) -> "Weights":
+        """A llama.cpp GGUF's tensors in the catalogue's names (omg_load_gguf);
+        `config` is None (Engine.open_gguf builds the engine from the file)."""
+        return cls(L.handle(L.lib().omg_load_gguf(str(path).encode())), None)
+
     def __del__(self):
         lib = getattr(L, "_lib", None)
         if lib is not None and getattr(self, "_h", None):

@@ -105,6 +105,12 @@ int omg_weights_get(const omg_weights *w, size_t i, const char **name, int *dtyp
                     size_t *ndim, const uint8_t **data, size_t *nbytes, const uint8_t **scales,
                     size_t *nscale_bytes);
 void omg_weights_free(omg_weights *w);
+/* A llama.cpp GGUF file (v2/v3, gemma3) read directly: the metadata and
+ * tensor mapping of tools/export_wgpu_gguf.py:112-296 (q / k / v fused per
+ * layer, Q8_0 / Q4_0 blocks split into codes and scales, f32 / bf16 to
+ * f16).  The reference reaches a GGUF through that export step; this reads
+ * the file itself. */
+omg_weights *omg_load_gguf(const char *path);
 /* Engine::new's loop over the catalogue (engine.rs:1341-1351). */
 int omg_builder_push_weights(omg_builder *b, const omg_weights *w);
 /* EngineBuilder::missing (engine.rs:875-885): newline-separated names into
@@ -117,6 +123,8 @@ void omg_builder_free(omg_builder *b);
 /* WgpuBackend::load for an exported directory: config.json + manifest.json
  * + *.bin (backend.rs:28-71, model.rs:742-795). */
 omg_engine *omg_open_dir(const char *dir, size_t capacity, size_t max_rows);
+/* An engine straight from a GGUF file (omg_load_gguf's tensors). */
+omg_engine *omg_open_gguf(const char *path, size_t capacity, size_t max_rows);
 void omg_close(omg_engine *e);
 int omg_config(const omg_engine *e, omg_config_t *out);
 /* Engine::warmup (engine.rs:1356-1366). */
