@@ -67,10 +67,15 @@ __device__ inline int vt_swz(int row) { return A_KT == 64 ? ((row >> 1) & 7) : (
 // (16 lanes on 16 consecutive rows at one logical chunk) hit distinct banks:
 //   K   [64 keys][HD]:  physical chunk = logical ^ (row & 15)  (32-chunk rows)
 //   V^T [HD][A_KT keys]:  physical chunk = logical ^ vt_swz(row)
+// Head dims above 256 split the output columns over HD / 256 workgroups
+// (blockIdx.z), each holding the full K tile and its 256 rows of V^T.
+template <int HD>
+constexpr int attn_col_splits() { return HD / 256; }
+
 template <int HD>
 struct AttnSmem {
     half_t k[2][A_KT * HD];
-    half_t v[2][HD * A_KT];
+    half_t v[2][(HD / attn_col_splits<HD>()) * A_KT];
 };
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
@@ -92,17 +97,21 @@ template <int HD>
 struct TileDma {
     static constexpr int KROW = HD / 8;                       // 16 B chunks per K row
     static constexpr int KINS = A_KT * HD / 8 / WAVE / A_NW;  // instructions per wave for K
-    static constexpr int VINS = HD * A_KT / 8 / WAVE / A_NW;
+    static constexpr int VINS = (HD / attn_col_splits<HD>()) * A_KT / 8 / WAVE / A_NW;
 };
 
 // One work item per workgroup: A_ROWS query rows (TPW tokens x HPG heads
 // per wave in QB blocks of 16 rows, A_NW waves) against key tiles [tb, te)
-// of the KV head blockIdx.y.
+// of the KV head blockIdx.y, output columns [256 z, 256 z + 256) for
+// z = blockIdx.z when HD > 256.
 template <int HD, int HPG>
 __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const int4* __restrict__ items) {
     using SM = AttnSmem<HD>;
     constexpr int DS = HD / 32;  // MFMA steps over the head dim
-    constexpr int CT = HD / 16;  // 16-wide output column tiles
+    constexpr int KG = DS < 8 ? DS : 8;  // K fragments in registers at once (per 16-key block)
+    constexpr int NCS = attn_col_splits<HD>();
+    constexpr int VD = HD / NCS;  // output columns of this workgroup
+    constexpr int CT = VD / 16;   // 16-wide output column tiles
     constexpr int QB = A_QB, TPQ = 16 / HPG;  // tokens per 16-row block
     constexpr int TPW = QB * TPQ, TPB = A_NW * TPW;
     constexpr float LOG2E = 1.4426950408889634f;
@@ -115,6 +124,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
     const int H = a.heads;
     const int g = int(blockIdx.y);
+    const int ch = NCS > 1 ? int(blockIdx.z) : 0;  // output column split
     const int64_t tok0 = int64_t(qtile) * TPB + wave * TPW;
     const int lr = lane % 16, G = lane / 16;
     const int u_lane = lr / HPG;  // the lane's token within each block
@@ -137,7 +147,8 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(sm.k[buf] + (wave * TD::KINS + i) * WAVE * 8),
                                                      16, o, k0 * HD * 2, 0, 0);
         }
-        const int vtile = (k0 / 64) * HD * 64 + k0 % 64;  // first element of the tile's V^T columns
+        // First element of the tile's V^T columns (rows of this column split).
+        const int vtile = (k0 / 64) * HD * 64 + k0 % 64 + ch * VD * 64;
 #pragma unroll
         for (int i = 0; i < TD::VINS; ++i) {
             const int slot = (wave * TD::VINS + i) * WAVE + lane;
@@ -204,18 +215,21 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             km_next = meta[(tile + 1) * A_KT + lane % A_KT];
         }
 
-        // All of the tile's K fragments are read at once (their LDS latency
-        // hides behind the mask ballots), then the QK products run with the
-        // accumulation chains interleaved.
+        // The tile's K fragments are read KG steps at a time (at HD 256 all
+        // at once: their LDS latency hides behind the mask ballots), then
+        // the QK products run with the accumulation chains interleaved.
         const half_t* K = sm.k[cur];
-        half8 kf[A_KB][DS];
+        half8 kf[A_KB][KG];
+        auto load_kf = [&](int sg) {
 #pragma unroll
-        for (int j = 0; j < A_KB; ++j)
+            for (int j = 0; j < A_KB; ++j)
 #pragma unroll
-            for (int s = 0; s < DS; ++s) {
-                const int pc = (s * 4 + G) ^ lr;  // row & 15 == lr
-                kf[j][s] = *reinterpret_cast<const half8*>(K + (j * 16 + lr) * HD + pc * 8);
-            }
+                for (int s = 0; s < KG; ++s) {
+                    const int pc = ((sg * KG + s) * 4 + G) ^ lr;  // row & 15 == lr
+                    kf[j][s] = *reinterpret_cast<const half8*>(K + (j * 16 + lr) * HD + pc * 8);
+                }
+        };
+        load_kf(0);
         __builtin_amdgcn_sched_barrier(0);
 
         // Which keys of the tile each of the wave's tokens sees: lane = key.
@@ -251,12 +265,17 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 #pragma unroll
             for (int j = 0; j < A_KB; ++j) sacc[b][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < DS; ++s)
+        for (int sg = 0; sg < DS / KG; ++sg) {
+            if (sg > 0) load_kf(sg);
 #pragma unroll
-            for (int j = 0; j < A_KB; ++j)
+            for (int s = 0; s < KG; ++s)
 #pragma unroll
-                for (int b = 0; b < QB; ++b)
-                    sacc[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][s], qf[b][s], sacc[b][j], 0, 0, 0);
+                for (int j = 0; j < A_KB; ++j)
+#pragma unroll
+                    for (int b = 0; b < QB; ++b)
+                        sacc[b][j] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][s], qf[b][sg * KG + s], sacc[b][j], 0, 0, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
 
         // The V^T fragments go out before the softmax, whose arithmetic then
@@ -361,14 +380,14 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             // Partial result of this chunk: O / l rounded to f16 exactly as
             // an unsplit tile's output, and the chunk's max and sum.
             const int64_t prow = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row;
-            half_t* op = a.part_o + prow * HD + G * 4;
+            half_t* op = a.part_o + prow * HD + ch * VD + G * 4;
 #pragma unroll
             for (int c = 0; c < CT; ++c) {
                 const half4 v = {half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
                                  half_t(o[b][c][3] * inv)};
                 *reinterpret_cast<half4*>(op + c * 16) = v;
             }
-            if (G == 0) {
+            if (G == 0 && ch == 0) {
                 a.part_ml[prow * 2] = m_run[b];
                 a.part_ml[prow * 2 + 1] = l;
             }
@@ -376,7 +395,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
         }
         const int64_t tq = tok0 + b * TPQ + u_lane;
         if (tq < a.t) {
-            half_t* dst = a.out + (tq * H + head) * HD + G * 4;
+            half_t* dst = a.out + (tq * H + head) * HD + ch * VD + G * 4;
 #pragma unroll
             for (int c = 0; c < CT; ++c) {
                 const half4 v = {half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
@@ -393,12 +412,14 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 // over the chunks the row saw anything in.  A row with one such chunk gets
 // that chunk's f16 output unchanged, exactly what an unsplit tile writes.
 // One wave per row (four rows per workgroup); lane l owns columns
-// 4l .. 4l + 3, so every partial row is one contiguous 512-byte wave load.
+// 256 q + 4l .. 256 q + 4l + 3 (q < HD / 256), so every 256 columns of a
+// partial row are one contiguous 512-byte wave load.
 // The statistics and partial rows of up to MAXC chunks are loaded together
 // (one round trip after the merge record).
 template <int HD>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const int4* __restrict__ merges) {
-    static_assert(HD == 4 * WAVE, "one half4 column group per lane");
+    static_assert(HD == 256 || HD == 512, "half4 column groups per lane");
+    constexpr int NQ = HD / 256;
     constexpr int MAXC = 8;  // chunks loaded per round
     const int4 mg = merges[blockIdx.x / (A_ROWS / 4)];
     const int qtile = mg.x, slot0 = mg.y, n = mg.z;
@@ -415,17 +436,24 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
     // Running merge over rounds of MAXC chunks (one round for n <= MAXC):
     // (M, L, acc) rescaled when a later round raises the max.
     float M = -INFINITY, L = 0.0f;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 acc[NQ];
+    half4 only[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        acc[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        only[q] = half4{};
+    }
     int seen = 0;
-    half4 only = {};
     for (int c0 = 0; c0 < n; c0 += MAXC) {
-        half4 v[MAXC];
+        half4 v[MAXC][NQ];
         float2 ml[MAXC];
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
             if (c0 + c < n) {
                 ml[c] = *reinterpret_cast<const float2*>(a.part_ml + base(c0 + c) * 2);
-                v[c] = *reinterpret_cast<const half4*>(a.part_o + base(c0 + c) * HD + lane * 4);
+#pragma unroll
+                for (int q = 0; q < NQ; ++q)
+                    v[c][q] = *reinterpret_cast<const half4*>(a.part_o + base(c0 + c) * HD + q * 256 + lane * 4);
             } else {
                 ml[c] = make_float2(-INFINITY, 0.0f);
             }
@@ -436,28 +464,38 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
         if (Mr == -INFINITY) continue;
         const float r = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mr);
         L *= r;
-        acc.x *= r;
-        acc.y *= r;
-        acc.z *= r;
-        acc.w *= r;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            acc[q].x *= r;
+            acc[q].y *= r;
+            acc[q].z *= r;
+            acc[q].w *= r;
+        }
         M = Mr;
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
             if (ml[c].x == -INFINITY) continue;
             ++seen;
-            only = v[c];
             const float w = ml[c].y * __builtin_amdgcn_exp2f(ml[c].x - M);
             L += w;
-            acc.x += float(v[c].x) * w;
-            acc.y += float(v[c].y) * w;
-            acc.z += float(v[c].z) * w;
-            acc.w += float(v[c].w) * w;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                only[q] = v[c][q];
+                acc[q].x += float(v[c][q].x) * w;
+                acc[q].y += float(v[c][q].y) * w;
+                acc[q].z += float(v[c][q].z) * w;
+                acc[q].w += float(v[c][q].w) * w;
+            }
         }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const half4 o = seen == 1 ? only
-                              : half4{half_t(acc.x * inv), half_t(acc.y * inv), half_t(acc.z * inv), half_t(acc.w * inv)};
-    *reinterpret_cast<half4*>(a.out + (tq * a.heads + head) * HD + lane * 4) = o;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const half4 o = seen == 1 ? only[q]
+                                  : half4{half_t(acc[q].x * inv), half_t(acc[q].y * inv), half_t(acc[q].z * inv),
+                                          half_t(acc[q].w * inv)};
+        *reinterpret_cast<half4*>(a.out + (tq * a.heads + head) * HD + q * 256 + lane * 4) = o;
+    }
 }
 
 void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk,
@@ -502,18 +540,30 @@ static void run_attention(hipStream_t s, const AttnArgs& a, const int4* items, i
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));
         attr_set = true;
     }
-    attention_kernel<HD, HPG><<<dim3(unsigned(nitems), unsigned(a.kv_heads)), dim3(A_THREADS), smem, s>>>(a, items);
+    attention_kernel<HD, HPG><<<dim3(unsigned(nitems), unsigned(a.kv_heads), unsigned(attn_col_splits<HD>())),
+                                dim3(A_THREADS), smem, s>>>(a, items);
     OMG_HIP(hipGetLastError());
 }
 
 void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems) {
     if (a.t <= 0 || nitems <= 0) return;
-    if (a.hd != 256) fail(E_INVALID, "attention: head_dim must be 256");
+    if (a.hd != 256 && a.hd != 512) fail(E_INVALID, "attention: head_dim must be 256 or 512");
     if (a.kv_heads <= 0 || a.heads % a.kv_heads) fail(E_INVALID, "attention: heads / kv_heads");
     const int hpg = a.heads / a.kv_heads;
     if (16 % hpg) fail(E_INVALID, "attention: query heads per KV head must divide 16");
     if (a.cap_pad % 64 || a.base + a.t > a.cap_pad) fail(E_INVALID, "attention: cache rows out of range");
     if (a.window < 0) fail(E_INVALID, "attention: negative window");
+    if (a.hd == 512) {
+        const size_t smem = sizeof(AttnSmem<512>);
+        switch (hpg) {
+            case 1: run_attention<512, 1>(s, a, items, nitems, smem); break;
+            case 2: run_attention<512, 2>(s, a, items, nitems, smem); break;
+            case 4: run_attention<512, 4>(s, a, items, nitems, smem); break;
+            case 8: run_attention<512, 8>(s, a, items, nitems, smem); break;
+            default: run_attention<512, 16>(s, a, items, nitems, smem); break;
+        }
+        return;
+    }
     const size_t smem = sizeof(AttnSmem<256>);
     switch (hpg) {
         case 1: run_attention<256, 1>(s, a, items, nitems, smem); break;
@@ -526,9 +576,13 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
 
 void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges) {
     if (a.t <= 0 || nmerges <= 0) return;
-    if (a.hd != 256) fail(E_INVALID, "attention_merge: head_dim must be 256");
-    attention_merge_kernel<256><<<dim3(unsigned(nmerges * (A_ROWS / 4)), unsigned(a.kv_heads)), dim3(256), 0, s>>>(
-        a, merges);
+    const dim3 grid(unsigned(nmerges * (A_ROWS / 4)), unsigned(a.kv_heads));
+    if (a.hd == 512)
+        attention_merge_kernel<512><<<grid, dim3(256), 0, s>>>(a, merges);
+    else if (a.hd == 256)
+        attention_merge_kernel<256><<<grid, dim3(256), 0, s>>>(a, merges);
+    else
+        fail(E_INVALID, "attention_merge: head_dim must be 256 or 512");
     OMG_HIP(hipGetLastError());
 }
 

@@ -31,6 +31,8 @@ struct omg_weights {
             auto it = tensors.find(spec.name);
             if (it != tensors.end()) order.push_back(&*it);
         }
+        auto table = tensors.find("per_layer_table");  // after the catalogue, as set_per_layer_table
+        if (table != tensors.end()) order.push_back(&*table);
     }
 };
 struct omg_laya_builder {

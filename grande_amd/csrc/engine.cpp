@@ -230,6 +230,8 @@ DevTensor upload_weight(const QTensor& t) {
 Builder::Builder(Config cfg) : cfg_(std::move(cfg)) {
     cfg_.validate();
     for (const TensorSpec& s : cfg_.tensors()) expected_[s.name] = s.shape;
+    // engine.rs:938-947 (set_per_layer_table): [vocab, layers x P].
+    if (cfg_.per_layer_dim > 0) expected_["per_layer_table"] = {cfg_.vocab, cfg_.per_layer_dim * cfg_.layers};
 }
 
 void Builder::push(const std::string& name, const QTensor& t) {
@@ -239,6 +241,12 @@ void Builder::push(const std::string& name, const QTensor& t) {
     const int64_t n = t.numel();
     if (int64_t(t.data.size()) != payload_bytes(t.dtype, n)) fail(E_INVALID, name + ": payload size mismatch");
     if (t.dtype != F16 && int64_t(t.scales.size()) != n / BLOCK * 2) fail(E_INVALID, name + ": scale size mismatch");
+    if (name.size() >= 9 && name.compare(name.size() - 9, 9, "out_scale") == 0) {
+        // A per-layer scalar (engine.rs:896-901), applied as is.
+        if (t.dtype != F16 || n != 1) fail(E_INVALID, name + ": expected one f16 value");
+        scalars_[name] = t.get(0);
+        return;
+    }
     if (t.shape.size() == 1) {
         // Norm weights are applied as (offset + w) in f32 (rmsnorm.wgsl:34-39).
         if (t.dtype != F16) fail(E_INVALID, name + ": 1-D tensors must be f16");
@@ -256,7 +264,7 @@ void Builder::push(const std::string& name, const QTensor& t) {
 std::vector<std::string> Builder::missing() const {
     std::vector<std::string> v;
     for (const auto& kv : expected_)
-        if (!linears_.count(kv.first) && !norms_.count(kv.first)) v.push_back(kv.first);
+        if (!linears_.count(kv.first) && !norms_.count(kv.first) && !scalars_.count(kv.first)) v.push_back(kv.first);
     return v;
 }
 
@@ -297,27 +305,47 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
         L.post_attn_norm = take_norm(n("post_attn_norm"));
         L.ffn_norm = take_norm(n("ffn_norm"));
         L.post_ffn_norm = take_norm(n("post_ffn_norm"));
+        if (c.per_layer_dim > 0) {
+            L.pl_gate = take_lin(n("pl_gate"));
+            L.pl_proj = take_lin(n("pl_proj"));
+            L.pl_norm = take_norm(n("pl_norm"));
+            L.out_scale = scalars_.at(n("out_scale"));
+        }
         E.layers_.push_back(std::move(L));
     }
-    // RoPE inverse frequencies theta^(-i / (hd/2)) (reference.rs:159-168),
-    // one table per attention type.
-    const int64_t hd = c.max_head_dim();
-    std::vector<float> fl(size_t(hd / 2)), fg(size_t(hd / 2));
-    for (int64_t i = 0; i < hd / 2; ++i) {
-        fl[size_t(i)] = std::pow(c.theta_local, -float(i) / float(hd / 2));
-        fg[size_t(i)] = std::pow(c.theta_global, -float(i) / float(hd / 2));
+    if (c.per_layer_dim > 0) {
+        E.pl_model_proj_ = take_lin("pl_model_proj");
+        E.pl_proj_norm_ = take_norm("pl_proj_norm");
+        E.pl_table_ = take_lin("per_layer_table");
     }
-    E.inv_freq_local_ = upload_bytes(fl.data(), fl.size() * 4);
-    E.inv_freq_global_ = upload_bytes(fg.data(), fg.size() * 4);
-    // Rotation (cos, sin) per position: positions stay below the capacity
-    // (every token of a pass has its own cache row).
+    // RoPE inverse frequencies theta^(-i / (hd/2)) (reference.rs:159-168)
+    // and the rotation (cos, sin) per position, one table per (layer type,
+    // head_dim): positions stay below the capacity (every token of a pass
+    // has its own cache row).
+    const int64_t hd = c.max_head_dim();
     const int64_t cap = capacity, d = c.d;
     E.rope_rows_ = cap;
-    E.rope_local_ = DevBuf(size_t(cap * (hd / 2)) * 8);
-    E.rope_global_ = DevBuf(size_t(cap * (hd / 2)) * 8);
-    launch_rope_table(E.stream_, E.inv_freq_local_.as<float>(), cap, hd / 2, E.rope_local_.as<float2>());
-    launch_rope_table(E.stream_, E.inv_freq_global_.as<float>(), cap, hd / 2, E.rope_global_.as<float2>());
-    OMG_HIP(hipStreamSynchronize(E.stream_));
+    {
+        std::vector<std::pair<bool, int64_t>> keys;
+        std::vector<DevBuf> freqs;
+        for (int64_t l = 0; l < c.layers; ++l) {
+            const std::pair<bool, int64_t> key{c.sliding[size_t(l)], c.head_dim[size_t(l)]};
+            auto it = std::find(keys.begin(), keys.end(), key);
+            if (it == keys.end()) {
+                const int64_t half = key.second / 2;
+                const float theta = key.first ? c.theta_local : c.theta_global;
+                std::vector<float> f(static_cast<size_t>(half));
+                for (int64_t i = 0; i < half; ++i) f[size_t(i)] = std::pow(theta, -float(i) / float(half));
+                freqs.push_back(upload_bytes(f.data(), f.size() * 4));
+                E.rope_tabs_.emplace_back(size_t(cap * half) * 8);
+                launch_rope_table(E.stream_, freqs.back().as<float>(), cap, half, E.rope_tabs_.back().as<float2>());
+                keys.push_back(key);
+                it = keys.end() - 1;
+            }
+            E.rope_of_.push_back(int(it - keys.begin()));
+        }
+        OMG_HIP(hipStreamSynchronize(E.stream_));
+    }
     E.ids_ = DevBuf(size_t(cap) * 4);
     E.meta_ = DevBuf(size_t(E.cap_pad_) * 16, true);
     E.x_ = DevBuf(size_t(cap * d) * 4);
@@ -333,6 +361,13 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.wanted_ = DevBuf(size_t(max_rows) * 4);
     E.labels_ = DevBuf(size_t(c.vocab) * 4);
     E.kv_stage_ = DevBuf(size_t(E.cap_pad_ * 2 * c.kv_heads * hd) * 2);
+    if (c.per_layer_dim > 0) {
+        const int64_t P = c.per_layer_dim;
+        E.x16_ = DevBuf(size_t(cap * d) * 2);
+        E.pli_ = DevBuf(size_t(cap * P * c.layers) * 4);
+        E.plg_ = DevBuf(size_t(cap * P) * 4);
+        E.pl16_ = DevBuf(size_t(cap * P) * 2);
+    }
     // Attention work: query tiles' key ranges are split at fixed multiples
     // of `chunk` key tiles: 256 keys on sliding layers (a range is at most
     // window + branch long), at least 512 keys and at most ~8 chunks over
@@ -518,7 +553,7 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         if (w.slots > part_slots_) {
             part_slots_ = w.slots;
             const size_t rows = size_t(part_slots_ * cfg_.kv_heads * attention_rows());
-            part_o_ = DevBuf(rows * size_t(cfg_.head_dim[0]) * 2);
+            part_o_ = DevBuf(rows * size_t(cfg_.max_head_dim()) * 2);
             part_ml_ = DevBuf(rows * 2 * 4);
         }
         n_items_[kind] = int64_t(w.items.size());
@@ -544,6 +579,19 @@ void Engine::forward(int64_t t, int64_t base) {
         launch_embed_norm(stream_, embed_.w, ids_.as<uint32_t>(), t, std::sqrt(float(d)),
                           layers_[0].attn_norm.as<float>(), c.eps, x_.as<float>(), hn_.as<half_t>());
     });
+    const int64_t P = c.per_layer_dim;
+    if (P > 0) {
+        // Per-layer inputs of every layer at once (engine.rs:1651-1666).
+        step("pl_in", [&] { launch_to_f16(stream_, x_.as<float>(), x16_.as<half_t>(), t * d); });
+        step("mm_pl_model_proj", [&] {
+            launch_gemm(stream_, x16_.as<half_t>(), d, pl_model_proj_.w, pli_.as<float>(), P * c.layers, t);
+        });
+        step("pl_combine", [&] {
+            launch_pl_combine(stream_, pl_table_.w, ids_.as<uint32_t>(), pl_proj_norm_.as<float>(), pli_.as<float>(),
+                              t, P, c.layers, c.eps, 1.0f / std::sqrt(float(d)), std::sqrt(float(P)),
+                              1.0f / std::sqrt(2.0f));
+        });
+    }
     for (int64_t l = 0; l < c.layers; ++l) {
         Layer& L = layers_[size_t(l)];
         const int64_t hd = c.head_dim[size_t(l)], qw = c.qkv_width(l), ff = c.ff[size_t(l)];
@@ -556,7 +604,7 @@ void Engine::forward(int64_t t, int64_t base) {
             q.meta = meta_.as<int32_t>();
             q.q_norm = L.q_norm.as<float>();
             q.k_norm = c.has_kv(l) ? L.k_norm.as<float>() : nullptr;
-            q.rope = (c.sliding[size_t(l)] ? rope_local_ : rope_global_).as<float2>();
+            q.rope = rope_tabs_[size_t(rope_of_[size_t(l)])].as<float2>();
             q.rope_rows = rope_rows_;
             q.rope_dims = c.rope_dims[size_t(l)];
             q.eps = c.eps;
@@ -607,9 +655,28 @@ void Engine::forward(int64_t t, int64_t base) {
         step("mm_down", [&] { launch_gemm(stream_, act_.as<half_t>(), ff, L.down.w, a_.as<float>(), d, t); });
         // The last layer's stream is normed at the wanted rows only (readout).
         const float* next = l + 1 < c.layers ? layers_[size_t(l + 1)].attn_norm.as<float>() : nullptr;
+        half_t* next_hn = next ? hn_.as<half_t>() : nullptr;
+        if (P == 0) {
+            step("norm", [&] {
+                launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), next,
+                                     next_hn, t, d, c.eps, 1.0f);
+            });
+            continue;
+        }
+        // Per-layer input block (engine.rs:1733-1750): the stream after the
+        // feed-forward, as f16, gates the layer's slice of the inputs.
         step("norm", [&] {
-            launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), next,
-                                 hn_.as<half_t>(), t, d, c.eps, 1.0f);
+            launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), nullptr,
+                                 x16_.as<half_t>(), t, d, c.eps, 1.0f);
+        });
+        step("mm_pl_gate", [&] { launch_gemm(stream_, x16_.as<half_t>(), d, L.pl_gate.w, plg_.as<float>(), P, t); });
+        step("pl_gate", [&] {
+            launch_pl_gate(stream_, plg_.as<float>(), pli_.as<float>(), pl16_.as<half_t>(), t, P, c.layers, l);
+        });
+        step("mm_pl_proj", [&] { launch_gemm(stream_, pl16_.as<half_t>(), P, L.pl_proj.w, a_.as<float>(), d, t); });
+        step("norm", [&] {
+            launch_residual_norm(stream_, a_.as<float>(), L.pl_norm.as<float>(), x_.as<float>(), next, next_hn, t, d,
+                                 c.eps, L.out_scale);
         });
     }
 }

@@ -121,6 +121,7 @@ class Builder {
     std::map<std::string, std::vector<int64_t>> expected_;
     std::map<std::string, DevTensor> linears_;
     std::map<std::string, DevBuf> norms_;  // f32, norm offset folded in
+    std::map<std::string, float> scalars_;  // per-layer output scales (engine.rs:896-901)
 };
 
 struct PassPlan {
@@ -182,12 +183,24 @@ class Engine {
     struct Layer {
         DevTensor qkv, o, gate, up, down;
         DevBuf attn_norm, q_norm, k_norm, post_attn_norm, ffn_norm, post_ffn_norm;
+        // per-layer inputs (Gemma 4)
+        DevTensor pl_gate, pl_proj;
+        DevBuf pl_norm;
+        float out_scale = 1.0f;
     };
     std::vector<Layer> layers_;
-    DevBuf inv_freq_local_, inv_freq_global_, rope_local_, rope_global_;
+    // Gemma 4 per-layer inputs: the [vocab, layers x P] token table stays in
+    // HBM and is gathered on the device.
+    DevTensor pl_model_proj_, pl_table_;
+    DevBuf pl_proj_norm_;
+    // RoPE (cos, sin) tables, one per (layer type, head_dim); rope_of_[l]
+    // indexes the layer's.
+    std::vector<DevBuf> rope_tabs_;
+    std::vector<int> rope_of_;
     int64_t rope_rows_ = 0;
     // workspace
     DevBuf ids_, meta_, x_, hn_, qkv_, q16_, attn_, a_, act_, rows_, logits_, wanted_, labels_, kv_stage_;
+    DevBuf x16_, pli_, plg_, pl16_;  // per-layer inputs: f16(x), [t][layers x P] f32, gate f32, gated f16
     // attention work lists of the current pass: [0] sliding layers, [1] global
     int attn_chunk_[2] = {0, 0};
     DevBuf attn_items_[2], attn_merges_[2], part_o_, part_ml_;

@@ -38,9 +38,21 @@ void repack_q4(const uint8_t* src, uint8_t* dst, int64_t n);
 // x[r] = deq(E[ids[r]]) * sqrt(d) (f32, bit-exact), hn[r] = f16(rmsnorm(x[r]) * w).
 void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, int64_t t,
                        float embed_scale, const float* w, float eps, float* x, half_t* hn);
-// y = rmsnorm(a[r]) * w1;  x[r] = (y + x[r]) * scale;  if w2: hn[r] = f16(rmsnorm(x[r]) * w2).
+// y = rmsnorm(a[r]) * w1;  x[r] = (y + x[r]) * scale;  if w2: hn[r] = f16(rmsnorm(x[r]) * w2),
+// else if hn: hn[r] = f16(x[r]).
 void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float* x, const float* w2,
                           half_t* hn, int64_t t, int64_t d, float eps, float scale);
+// Gemma 4 per-layer inputs (engine.rs:1651-1666, 1728-1750).  pl holds
+// f16(x) . pl_model_proj^T as [t][layers x P] and is replaced by
+// (rmsnorm(pl * proj_scale) * w + f16(table[ids[t], :]) * emb_scale) * out_scale.
+void launch_pl_combine(hipStream_t s, const DevWeight& table, const uint32_t* ids, const float* w, float* pl,
+                       int64_t t, int64_t P, int64_t layers, float eps, float proj_scale, float emb_scale,
+                       float out_scale);
+// out[t][j] = f16(gelu_tanh(g[t][j]) * pl[t][layer * P + j]).
+void launch_pl_gate(hipStream_t s, const float* g, const float* pl, half_t* out, int64_t t, int64_t P, int64_t layers,
+                    int64_t layer);
+// out = f16(x), n % 4 == 0.
+void launch_to_f16(hipStream_t s, const float* x, half_t* out, int64_t n);
 // Per token: q heads normed + roped + scaled into q16; on K/V layers, k
 // heads normed + roped and v heads (optionally normed) into the f16 cache.
 struct QkArgs {

@@ -116,9 +116,9 @@ void Config::validate() const {
         fail(E_INVALID, "query heads per KV head must divide 16");
     for (int64_t i = 0; i < layers; ++i) {
         const int64_t hd = head_dim[size_t(i)];
-        if (hd != 256)
+        if (hd != 256 && hd != 512)
             fail(E_INVALID, "layer " + std::to_string(i) + ": head_dim " + std::to_string(hd) +
-                                " (this engine's attention kernels are built for 256)");
+                                " (this engine's attention kernels are built for 256 and 512)");
         if (rope_dims[size_t(i)] > hd || rope_dims[size_t(i)] % 2)
             fail(E_INVALID, "layer " + std::to_string(i) + ": rope_dims " +
                                 std::to_string(rope_dims[size_t(i)]));
@@ -128,8 +128,8 @@ void Config::validate() const {
     if (d % 32 != 0) fail(E_INVALID, "hidden_size must be a multiple of 32");
     for (int64_t f : ff)
         if (f % 32 != 0 || f <= 0) fail(E_INVALID, "intermediate_size must be a positive multiple of 32");
-    if (per_layer_dim != 0)
-        fail(E_INVALID, "per-layer embedding inputs (Gemma 4 hidden_size_per_layer_input) are not built");
+    if (per_layer_dim < 0 || per_layer_dim % 32 != 0 || per_layer_dim > 1024)
+        fail(E_INVALID, "hidden_size_per_layer_input must be a multiple of 32, at most 1024");
     if (window < 0) fail(E_INVALID, "sliding_window must be >= 0");
 }
 
@@ -316,6 +316,8 @@ Weights synth_weights(const Config& cfg, uint64_t seed, Dtype linear, Dtype embe
             w.tensors[nm] = tensor(spec.shape, scale, linear);
         }
     }
+    // reference.rs:132-133: the per-layer token table comes after the catalogue.
+    if (cfg.per_layer_dim > 0) w.tensors["per_layer_table"] = tensor({cfg.vocab, cfg.per_layer_dim * cfg.layers}, 1.0f, linear);
     return w;
 }
 
@@ -339,31 +341,40 @@ std::map<std::string, QTensor> read_manifest(const std::string& dir) {
     std::map<std::string, QTensor> out;
     const Json man = Json::parse(read_file(dir + "/manifest.json"));
     if (man["files"].kind != Json::Array) fail(E_INVALID, "manifest.json: missing files");
+    // One manifest entry (model.rs:758-794) out of its file's bytes.
+    auto entry = [&](const Json& e, const std::string& bytes) {
+        QTensor t;
+        const std::string name = e["name"].s("");
+        t.dtype = parse_dtype(e["dtype"].s(""));
+        for (const Json& s : e["shape"].arr) t.shape.push_back(int64_t(s.u64(0)));
+        auto slice = [&](uint64_t off, uint64_t n) {
+            if (off + n > bytes.size())
+                fail(E_INVALID, name + ": byte range " + std::to_string(off) + ".." +
+                                    std::to_string(off + n) + " outside the file");
+            return std::vector<uint8_t>(bytes.begin() + long(off), bytes.begin() + long(off + n));
+        };
+        t.data = slice(e["offset"].u64(0), e["nbytes"].u64(0));
+        t.scales = slice(e["scales_offset"].u64(0), e["scales_nbytes"].u64(0));
+        const int64_t n = t.numel();
+        if (int64_t(t.data.size()) != payload_bytes(t.dtype, n))
+            fail(E_INVALID, name + ": " + std::to_string(t.data.size()) + " payload bytes, expected " +
+                                std::to_string(payload_bytes(t.dtype, n)));
+        const int64_t want_scales = t.dtype == F16 ? 0 : n / BLOCK * 2;
+        if (int64_t(t.scales.size()) != want_scales)
+            fail(E_INVALID, name + ": " + std::to_string(t.scales.size()) + " scale bytes, expected " +
+                                std::to_string(want_scales));
+        return t;
+    };
     for (const Json& file : man["files"].arr) {
         const std::string bytes = read_file(dir + "/" + file["path"].s(""));
-        for (const Json& e : file["tensors"].arr) {
-            QTensor t;
-            const std::string name = e["name"].s("");
-            t.dtype = parse_dtype(e["dtype"].s(""));
-            for (const Json& s : e["shape"].arr) t.shape.push_back(int64_t(s.u64(0)));
-            auto slice = [&](uint64_t off, uint64_t n) {
-                if (off + n > bytes.size())
-                    fail(E_INVALID, name + ": byte range " + std::to_string(off) + ".." +
-                                        std::to_string(off + n) + " outside the file");
-                return std::vector<uint8_t>(bytes.begin() + long(off), bytes.begin() + long(off + n));
-            };
-            t.data = slice(e["offset"].u64(0), e["nbytes"].u64(0));
-            t.scales = slice(e["scales_offset"].u64(0), e["scales_nbytes"].u64(0));
-            const int64_t n = t.numel();
-            if (int64_t(t.data.size()) != payload_bytes(t.dtype, n))
-                fail(E_INVALID, name + ": " + std::to_string(t.data.size()) + " payload bytes, expected " +
-                                    std::to_string(payload_bytes(t.dtype, n)));
-            const int64_t want_scales = t.dtype == F16 ? 0 : n / BLOCK * 2;
-            if (int64_t(t.scales.size()) != want_scales)
-                fail(E_INVALID, name + ": " + std::to_string(t.scales.size()) + " scale bytes, expected " +
-                                    std::to_string(want_scales));
-            out[name] = std::move(t);
-        }
+        for (const Json& e : file["tensors"].arr) out[e["name"].s("")] = entry(e, bytes);
+    }
+    // The per-layer token table, in a file of its own (backend.rs:50-57).
+    const Json& plt = man["per_layer_table"];
+    if (plt.kind == Json::Object) {
+        const std::string path = plt["path"].s("");
+        if (path.empty()) fail(E_INVALID, "manifest: per_layer_table has no path");
+        out["per_layer_table"] = entry(plt, read_file(dir + "/" + path));
     }
     return out;
 }

@@ -115,7 +115,18 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
             xv[j] = o;
         }
     }
-    if (!w2) return;
+    if (!w2) {
+        if (!hn) return;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int64_t q = lane + j * WAVE;
+            if (q < nq) {
+                const float4 v = xv[j];
+                *reinterpret_cast<half4*>(hn + row * d + 4 * q) = half4{half_t(v.x), half_t(v.y), half_t(v.z), half_t(v.w)};
+            }
+        }
+        return;
+    }
     const float inv2 = 1.0f / sqrtf(wave_sum(ss2) / float(d) + eps);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -146,6 +157,117 @@ void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float*
     OMG_HIP(hipGetLastError());
 }
 
+// ------------------------------------------------- per-layer inputs
+
+// pl_combine.wgsl: per (token, layer) slice of P elements of
+// proj = f16(x) . pl_model_proj^T (in place in `pl`),
+//   pl = (rmsnorm(proj / sqrt(d)) * w + f16(table[id, slice]) * sqrt(P)) / sqrt(2).
+// One wave per slice holding it in registers (NV float4 per lane).
+template <int DT, int NV>
+__global__ __launch_bounds__(256) void pl_combine_kernel(DevWeight table, const uint32_t* __restrict__ ids,
+                                                         const float* __restrict__ w, float* __restrict__ pl,
+                                                         int64_t t, int64_t P, int64_t layers, float eps,
+                                                         float proj_scale, float emb_scale, float out_scale) {
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    const int64_t slice = int64_t(blockIdx.x) * 4 + wave;  // token * layers + layer
+    if (slice >= t * layers) return;
+    const int64_t tok = slice / layers;
+    const int64_t nq = P / 4;
+    float* row = pl + slice * P;
+    float4 v[NV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t q = lane + j * WAVE;
+        if (q < nq) {
+            v[j] = *reinterpret_cast<const float4*>(row + 4 * q);
+            v[j].x *= proj_scale, v[j].y *= proj_scale, v[j].z *= proj_scale, v[j].w *= proj_scale;
+            ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / float(P) + eps);
+    const int64_t col0 = (slice - tok * layers) * P;
+    const int64_t id = ids[tok];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t q = lane + j * WAVE;
+        if (q < nq) {
+            float e[4];
+            load4_f32<DT>(table, id, col0 + 4 * q, e);
+            const float4 g = *reinterpret_cast<const float4*>(w + 4 * q);
+            const float vv[4] = {v[j].x, v[j].y, v[j].z, v[j].w}, gg[4] = {g.x, g.y, g.z, g.w};
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (vv[i] * inv * gg[i] + float(half_t(e[i])) * emb_scale) * out_scale;
+            *reinterpret_cast<float4*>(row + 4 * q) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
+void launch_pl_combine(hipStream_t s, const DevWeight& table, const uint32_t* ids, const float* w, float* pl,
+                       int64_t t, int64_t P, int64_t layers, float eps, float proj_scale, float emb_scale,
+                       float out_scale) {
+    if (t <= 0) return;
+    if (P % 4 != 0 || P > 1024) fail(E_INVALID, "pl_combine: per-layer width must be a multiple of 4, at most 1024");
+    if (table.cols != P * layers) fail(E_INVALID, "pl_combine: table width must be per-layer width x layers");
+    const int nv = int((P / 4 + WAVE - 1) / WAVE);
+    const dim3 grid(unsigned((t * layers + 3) / 4)), block(256);
+#define OMG_PLC(D, N) \
+    pl_combine_kernel<D, N><<<grid, block, 0, s>>>(table, ids, w, pl, t, P, layers, eps, proj_scale, emb_scale, out_scale)
+#define OMG_PLC_NV(D)                      \
+    switch (nv) {                          \
+        case 1: OMG_PLC(D, 1); break;      \
+        case 2: OMG_PLC(D, 2); break;      \
+        default: OMG_PLC(D, 4); break;     \
+    }
+    switch (table.dtype) {
+        case F16_DT: OMG_PLC_NV(F16_DT) break;
+        case Q8_DT: OMG_PLC_NV(Q8_DT) break;
+        default: OMG_PLC_NV(Q4_DT) break;
+    }
+#undef OMG_PLC_NV
+#undef OMG_PLC
+    OMG_HIP(hipGetLastError());
+}
+
+// pl_gate.wgsl: out[t][j] = f16(gelu_tanh(g[t][j]) * pl[t][layer * P + j]).
+__global__ __launch_bounds__(256) void pl_gate_kernel(const float* __restrict__ g, const float* __restrict__ pl,
+                                                      half_t* __restrict__ out, int64_t t, int64_t P,
+                                                      int64_t pl_stride, int64_t layer) {
+    const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= t * P) return;
+    const int64_t tok = i / P, j = i - tok * P;
+    const float4 gv = *reinterpret_cast<const float4*>(g + i);
+    const float4 pv = *reinterpret_cast<const float4*>(pl + tok * pl_stride + layer * P + j);
+    auto gelu = [](float x) { return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x))); };
+    *reinterpret_cast<half4*>(out + i) =
+        half4{half_t(gelu(gv.x) * pv.x), half_t(gelu(gv.y) * pv.y), half_t(gelu(gv.z) * pv.z), half_t(gelu(gv.w) * pv.w)};
+}
+
+void launch_pl_gate(hipStream_t s, const float* g, const float* pl, half_t* out, int64_t t, int64_t P, int64_t layers,
+                    int64_t layer) {
+    if (t <= 0) return;
+    if (P % 4 != 0 || layer < 0 || layer >= layers) fail(E_INVALID, "pl_gate: shape");
+    const int64_t n4 = t * P / 4;
+    pl_gate_kernel<<<dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, s>>>(g, pl, out, t, P, P * layers, layer);
+    OMG_HIP(hipGetLastError());
+}
+
+// out[i] = f16(x[i]), n % 4 == 0.
+__global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x, half_t* __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    *reinterpret_cast<half4*>(out + i) = half4{half_t(v.x), half_t(v.y), half_t(v.z), half_t(v.w)};
+}
+
+void launch_to_f16(hipStream_t s, const float* x, half_t* out, int64_t n) {
+    if (n <= 0) return;
+    if (n % 4 != 0) fail(E_INVALID, "to_f16: count must be a multiple of 4");
+    to_f16_kernel<<<dim3(unsigned((n / 4 + 255) / 256)), dim3(256), 0, s>>>(x, out, n);
+    OMG_HIP(hipGetLastError());
+}
+
 // -------------------------------------------------------------- qk prep
 
 // qk_prep.wgsl:66-114 in two kinds of blocks of one launch.
@@ -165,9 +287,11 @@ void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float*
 // sits in lane ^ 32.
 template <int HD>
 __global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int64_t vblocks, int qk_slots) {
-    constexpr int EPL = HD / WAVE;
+    constexpr int EPL = HD / WAVE;   // elements per lane: 4 (hd 256) or 8 (hd 512)
+    constexpr int NQ = EPL / 4;      // float4 per lane
     constexpr int HALF = HD / 2;
-    static_assert(EPL == 4 && HD == 256, "qk_prep: one float4 per lane, one dimension per thread");
+    constexpr int DPT = HD / 256;    // V^T dimensions per thread
+    static_assert(HD == 256 || HD == 512, "qk_prep: head_dim 256 or 512");
     const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
     const int e0 = lane * EPL;
     const int H = a.heads, KV = a.kv_heads;
@@ -179,48 +303,56 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int64_t vblocks,
         const int64_t lo = r0 > a.base ? r0 : a.base;
         const int64_t hi = r0 + 64 < a.base + a.t ? r0 + 64 : a.base + a.t;
         const bool whole = lo == r0 && hi == r0 + 64;
-        const int dim = int(threadIdx.x);
-        half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + tile) * HD + dim) * 64;
-        uint4 kept[8];
-        if (!whole) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) kept[c] = reinterpret_cast<const uint4*>(dst)[c];
-        }
         const float* src = a.qkv + int64_t(H + KV + head) * HD + e0;
-        float4 v[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             const int64_t row = r0 + 16 * wave + k;
-            v[k] = row >= lo && row < hi ? *reinterpret_cast<const float4*>(src + (row - a.base) * a.qkv_stride)
-                                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+            float4 v[NQ];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
+            for (int q = 0; q < NQ; ++q)
+                v[q] = row >= lo && row < hi
+                           ? *reinterpret_cast<const float4*>(src + (row - a.base) * a.qkv_stride + 4 * q)
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             float inv = 1.0f;
             if (a.v_norm) {
-                const float ss = v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+                float ss = 0.0f;
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) ss += v[q].x * v[q].x + v[q].y * v[q].y + v[q].z * v[q].z + v[q].w * v[q].w;
                 inv = 1.0f / sqrtf(wave_sum(ss) / float(HD) + a.eps);
             }
-            half4 h = {half_t(v[k].x * inv), half_t(v[k].y * inv), half_t(v[k].z * inv), half_t(v[k].w * inv)};
-            *reinterpret_cast<half4*>(&tile_rows[16 * wave + k][e0]) = h;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                half4 h = {half_t(v[q].x * inv), half_t(v[q].y * inv), half_t(v[q].z * inv), half_t(v[q].w * inv)};
+                *reinterpret_cast<half4*>(&tile_rows[16 * wave + k][e0 + 4 * q]) = h;
+            }
         }
         __syncthreads();
-        // Chunk (half hf, group m) holds keys 32hf + 4m + 0..3, then 32hf + 16 + 4m + 0..3.
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const int hf = c / 4, m = c % 4;
-            uint32_t h[8];
+        for (int dd = 0; dd < DPT; ++dd) {
+            const int dim = int(threadIdx.x) + 256 * dd;
+            half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + tile) * HD + dim) * 64;
+            uint4 kept[8];
+            if (!whole) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = 32 * hf + 16 * (j / 4) + 4 * m + j % 4;
-                h[j] = __builtin_bit_cast(uint16_t, tile_rows[key][dim]);
-                if (!whole && (r0 + key < lo || r0 + key >= hi)) {
-                    const uint32_t w = j / 2 == 0 ? kept[c].x : j / 2 == 1 ? kept[c].y : j / 2 == 2 ? kept[c].z : kept[c].w;
-                    h[j] = (w >> (16 * (j % 2))) & 0xffffu;
-                }
+                for (int c = 0; c < 8; ++c) kept[c] = reinterpret_cast<const uint4*>(dst)[c];
             }
-            const uint4 u = {h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
-            reinterpret_cast<uint4*>(dst)[c] = u;
+            // Chunk (half hf, group m) holds keys 32hf + 4m + 0..3, then 32hf + 16 + 4m + 0..3.
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const int hf = c / 4, m = c % 4;
+                uint32_t h[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int key = 32 * hf + 16 * (j / 4) + 4 * m + j % 4;
+                    h[j] = __builtin_bit_cast(uint16_t, tile_rows[key][dim]);
+                    if (!whole && (r0 + key < lo || r0 + key >= hi)) {
+                        const uint32_t w = j / 2 == 0 ? kept[c].x : j / 2 == 1 ? kept[c].y : j / 2 == 2 ? kept[c].z : kept[c].w;
+                        h[j] = (w >> (16 * (j % 2))) & 0xffffu;
+                    }
+                }
+                const uint4 u = {h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
+                reinterpret_cast<uint4*>(dst)[c] = u;
+            }
         }
         return;
     }
@@ -233,47 +365,57 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int64_t vblocks,
     const int head = is_q ? slot : slot - H;
     int pos = a.meta[4 * row];
     pos = pos < 0 ? 0 : (pos >= a.rope_rows ? int(a.rope_rows - 1) : pos);
-    const float4 v4 = *reinterpret_cast<const float4*>(a.qkv + tok * a.qkv_stride + int64_t(slot) * HD + e0);
-    const float4 w4 = *reinterpret_cast<const float4*>((is_q ? a.q_norm : a.k_norm) + e0);
+    const float* vsrc = a.qkv + tok * a.qkv_stride + int64_t(slot) * HD + e0;
+    const float* wsrc = (is_q ? a.q_norm : a.k_norm) + e0;
     const int d0 = e0 % HALF;
+    // (cos, sin) pairs of the lane's EPL dimensions: 2 * EPL floats.
     const float4* rt = reinterpret_cast<const float4*>(a.rope + int64_t(pos) * HALF + d0);
-    const float4 r01 = rt[0], r23 = rt[1];
-    const float cs[EPL] = {r01.x, r01.z, r23.x, r23.z}, sn[EPL] = {r01.y, r01.w, r23.y, r23.w};
-    const float v[EPL] = {v4.x, v4.y, v4.z, v4.w};
+    float v[EPL], w[EPL], cs[EPL], sn[EPL];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const float4 v4 = *reinterpret_cast<const float4*>(vsrc + 4 * q);
+        const float4 w4 = *reinterpret_cast<const float4*>(wsrc + 4 * q);
+        const float4 r01 = rt[2 * q], r23 = rt[2 * q + 1];
+        v[4 * q] = v4.x, v[4 * q + 1] = v4.y, v[4 * q + 2] = v4.z, v[4 * q + 3] = v4.w;
+        w[4 * q] = w4.x, w[4 * q + 1] = w4.y, w[4 * q + 2] = w4.z, w[4 * q + 3] = w4.w;
+        cs[4 * q] = r01.x, cs[4 * q + 1] = r01.z, cs[4 * q + 2] = r23.x, cs[4 * q + 3] = r23.z;
+        sn[4 * q] = r01.y, sn[4 * q + 1] = r01.w, sn[4 * q + 2] = r23.y, sn[4 * q + 3] = r23.w;
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) ss += v[i] * v[i];
     const float inv = 1.0f / sqrtf(wave_sum(ss) / float(HD) + a.eps);
-    const float y[EPL] = {v[0] * inv * w4.x, v[1] * inv * w4.y, v[2] * inv * w4.z, v[3] * inv * w4.w};
     float o[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-        const float partner = __shfl_xor(y[i], 32, WAVE);
+        const float y = v[i] * inv * w[i];
+        const float partner = __shfl_xor(y, 32, WAVE);
         if (d0 + i < a.rope_dims / 2)
-            o[i] = e0 < HALF ? y[i] * cs[i] - partner * sn[i] : y[i] * cs[i] + partner * sn[i];
+            o[i] = e0 < HALF ? y * cs[i] - partner * sn[i] : y * cs[i] + partner * sn[i];
         else
-            o[i] = y[i];
+            o[i] = y;
     }
-    if (is_q) {
-        half4 h = {half_t(o[0] * a.q_scale), half_t(o[1] * a.q_scale), half_t(o[2] * a.q_scale),
-                   half_t(o[3] * a.q_scale)};
-        *reinterpret_cast<half4*>(a.q16 + (tok * H + head) * HD + e0) = h;
-    } else {
-        half4 h = {half_t(o[0]), half_t(o[1]), half_t(o[2]), half_t(o[3])};
-        *reinterpret_cast<half4*>(a.kc + (int64_t(head) * a.cap_pad + row) * HD + e0) = h;
-    }
+    half_t* dst = is_q ? a.q16 + (tok * H + head) * HD + e0 : a.kc + (int64_t(head) * a.cap_pad + row) * HD + e0;
+    const float sc = is_q ? a.q_scale : 1.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+        *reinterpret_cast<half4*>(dst + 4 * q) = half4{half_t(o[4 * q] * sc), half_t(o[4 * q + 1] * sc),
+                                                       half_t(o[4 * q + 2] * sc), half_t(o[4 * q + 3] * sc)};
 }
 
 void launch_qk_prep(hipStream_t s, const QkArgs& a) {
     if (a.t <= 0) return;
     if (a.base + a.t > a.cap_pad || a.cap_pad % 64) fail(E_INVALID, "qk_prep: cache rows out of range");
-    if (a.hd != 256) fail(E_INVALID, "qk_prep: head_dim must be 256");
+    if (a.hd != 256 && a.hd != 512) fail(E_INVALID, "qk_prep: head_dim must be 256 or 512");
     if (a.rope_rows <= 0 || a.rope_dims > a.hd) fail(E_INVALID, "qk_prep: rope table");
     const int qk_slots = a.heads + (a.has_kv ? a.kv_heads : 0);
     const int64_t tiles = a.has_kv ? (a.base + a.t + 63) / 64 - a.base / 64 : 0;
     const int64_t vblocks = tiles * a.kv_heads;
     const int64_t blocks = vblocks + (a.t * qk_slots + 3) / 4;
-    qk_prep_kernel<256><<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(a, vblocks, qk_slots);
+    if (a.hd == 512)
+        qk_prep_kernel<512><<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(a, vblocks, qk_slots);
+    else
+        qk_prep_kernel<256><<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(a, vblocks, qk_slots);
     OMG_HIP(hipGetLastError());
 }
 

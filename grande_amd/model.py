@@ -55,6 +55,41 @@ def config_json(*, vocab: int, d: int, layers: int, heads: int, kv_heads: int, h
     return json.dumps(cfg)
 
 
+def gemma4_config_json(*, vocab: int, d: int, layers: int, heads: int, kv_heads: int, head_dim: int = 256,
+                       global_head_dim: int = 512, ff: int | list[int], window: int, sliding: list[bool],
+                       shared_kv_layers: int = 0, double_wide_mlp: bool = False, partial_rotary_global: float = 0.25,
+                       per_layer_dim: int = 0, softcap: float = 0.0, eps: float = 1e-6, theta_global: float = 1e6,
+                       theta_local: float = 1e4, bos: int = 2) -> str:
+    """A Gemma 4 text config (model.rs:95-210): global layers with their own
+    head_dim and partial RoPE, K/V shared by the last `shared_kv_layers`
+    layers, V normed, per-layer inputs of width `per_layer_dim`, norm
+    offset 0."""
+    cfg: dict = {
+        "model_type": "gemma4_text",
+        "vocab_size": vocab,
+        "hidden_size": d,
+        "num_hidden_layers": layers,
+        "num_attention_heads": heads,
+        "num_key_value_heads": kv_heads,
+        "head_dim": head_dim,
+        "global_head_dim": global_head_dim,
+        "intermediate_size": ff,
+        "use_double_wide_mlp": double_wide_mlp,
+        "num_kv_shared_layers": shared_kv_layers,
+        "sliding_window": window,
+        "layer_types": ["sliding_attention" if s else "full_attention" for s in sliding],
+        "rope_parameters": {
+            "full_attention": {"rope_theta": theta_global, "partial_rotary_factor": partial_rotary_global},
+            "sliding_attention": {"rope_theta": theta_local},
+        },
+        "hidden_size_per_layer_input": per_layer_dim,
+        "final_logit_softcapping": softcap,
+        "rms_norm_eps": eps,
+        "bos_token_id": bos,
+    }
+    return json.dumps(cfg)
+
+
 # BASELINE.json configs: Gemma-3-shaped decoders with the vocabulary pruned
 # to 25,000 rows.
 GEMMA3_270M = dict(vocab=25_000, d=640, layers=18, heads=4, kv_heads=1, head_dim=256, ff=2048, window=512)
@@ -162,13 +197,16 @@ class Weights:
 def export_dir(weights: Weights, path: str | Path) -> None:
     """Write the exported-directory layout (tools/export_wgpu_gguf.py:43-95):
     config.json, one .bin per file group (scales run, then codes, 4-byte
-    aligned), manifest.json."""
+    aligned), manifest.json; a Gemma 4 per-layer token table goes to
+    per_layer_table.bin under the manifest's own per_layer_table entry
+    (model.rs:744-750)."""
     out = Path(path)
     out.mkdir(parents=True, exist_ok=True)
     (out / "config.json").write_text(weights.config)
     groups: dict[str, list[QTensor]] = {}
     for t in weights.tensors():
-        key = t.name.split(".")[0] + "." + t.name.split(".")[1] if t.name.startswith("blk.") else "embed"
+        key = t.name.split(".")[0] + "." + t.name.split(".")[1] if t.name.startswith("blk.") else \
+            ("per_layer_table" if t.name == "per_layer_table" else "embed")
         groups.setdefault(key, []).append(t)
     files = []
     for key, ts in groups.items():
@@ -191,4 +229,8 @@ def export_dir(weights: Weights, path: str | Path) -> None:
                 e["offset"], e["nbytes"] = put(t.data.tobytes())
                 entries.append(e)
         files.append({"path": fname, "tensors": entries})
-    (out / "manifest.json").write_text(json.dumps({"files": files}, indent=1))
+    man: dict = {"files": [f for f in files if f["path"] != "per_layer_table.bin"]}
+    for f in files:
+        if f["path"] == "per_layer_table.bin":
+            man["per_layer_table"] = dict(f["tensors"][0], path=f["path"])
+    (out / "manifest.json").write_text(json.dumps(man, indent=1))

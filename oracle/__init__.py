@@ -40,7 +40,8 @@ class orc_config(C.Structure):
                 ("sliding", C.c_int32 * MAX_LAYERS), ("kv_source", C.c_int32 * MAX_LAYERS),
                 ("rope_dims", C.c_int32 * MAX_LAYERS), ("eps", C.c_float), ("window", C.c_int32),
                 ("theta_global", C.c_float), ("theta_local", C.c_float), ("query_scale", C.c_float),
-                ("norm_offset", C.c_float), ("v_norm", C.c_int32), ("softcap", C.c_float), ("bos", C.c_int32)]
+                ("norm_offset", C.c_float), ("v_norm", C.c_int32), ("softcap", C.c_float), ("bos", C.c_int32),
+                ("per_layer_dim", C.c_int32)]
 
 
 class orc_laya_config(C.Structure):
@@ -157,30 +158,55 @@ def get(dtype: int, data: np.ndarray, scales: np.ndarray, n: int) -> np.ndarray:
 # --------------------------------------------------------------- model
 
 def config_from_json(text: str) -> orc_config:
-    """The subset of model.rs:66-210 the oracle needs (Gemma 3 text)."""
+    """model.rs:66-210: Gemma 3 text configs, and Gemma 4 (global layers
+    with their own head_dim and partial RoPE, K/V shared by the last
+    num_kv_shared_layers from the last earlier layer of their type, V
+    normed, per-layer inputs)."""
     v = json.loads(text)
     v = v.get("text_config", v)
     L = int(v["num_hidden_layers"])
+    gemma4 = v.get("model_type", "gemma3_text") in ("gemma4_text", "gemma4")
     if "layer_types" in v:
         sliding = [t == "sliding_attention" for t in v["layer_types"]]
     else:
         k = int(v.get("_sliding_window_pattern", 6))
-        sliding = [(i + 1) % k != 0 for i in range(L)]
-    hd = int(v["head_dim"])
+        sliding = [True if k == 0 else (i + 1) % k != 0 for i in range(L)]
+    rope = v.get("rope_parameters", {})
+    hd_local = int(v["head_dim"])
+    hd_global = int(v.get("global_head_dim", hd_local))
+    rot_local = float(rope.get("sliding_attention", {}).get("partial_rotary_factor", 1.0))
+    rot_global = float(rope.get("full_attention", {}).get("partial_rotary_factor", 1.0))
+    shared = int(v.get("num_kv_shared_layers", 0))
+    first_shared = L - shared
     ff = v["intermediate_size"]
-    ff = list(ff) if isinstance(ff, list) else [int(ff)] * L
+    if isinstance(ff, list):
+        ff = [int(x) for x in ff]
+    else:
+        dbl = bool(v.get("use_double_wide_mlp", False))
+        ff = [2 * int(ff) if dbl and i >= first_shared else int(ff) for i in range(L)]
     c = orc_config()
     c.vocab, c.d, c.layers = int(v["vocab_size"]), int(v["hidden_size"]), L
     c.heads, c.kv_heads = int(v["num_attention_heads"]), int(v["num_key_value_heads"])
     for i in range(L):
-        c.head_dim[i], c.ff[i], c.sliding[i], c.kv_source[i], c.rope_dims[i] = hd, ff[i], int(sliding[i]), i, hd
+        hd = hd_local if sliding[i] else hd_global
+        src = i
+        if i >= first_shared:
+            src = next(j for j in range(first_shared - 1, -1, -1) if sliding[j] == sliding[i])
+        c.head_dim[i], c.ff[i], c.sliding[i], c.kv_source[i] = hd, ff[i], int(sliding[i]), src
+        c.rope_dims[i] = int(hd * (rot_local if sliding[i] else rot_global))
     c.eps = float(v.get("rms_norm_eps", 1e-6))
     c.window = int(v.get("sliding_window", 512))
-    c.theta_global = float(v.get("rope_theta", 1e6))
-    c.theta_local = float(v.get("rope_local_base_freq", 1e4))
-    c.query_scale = float(np.float32(v.get("query_pre_attn_scalar", hd)) ** np.float32(-0.5))
-    c.norm_offset = float(v.get("omg_norm_offset", 1.0))
-    c.v_norm, c.softcap, c.bos = 0, float(v.get("final_logit_softcapping", 0.0)), int(v.get("bos_token_id", 2))
+    c.theta_global = float(rope.get("full_attention", {}).get("rope_theta", v.get("rope_theta", 1e6)))
+    c.theta_local = float(rope.get("sliding_attention", {}).get("rope_theta", v.get("rope_local_base_freq", 1e4)))
+    if gemma4:
+        c.query_scale, c.v_norm = 1.0, 1
+        c.norm_offset = float(v.get("omg_norm_offset", 0.0))
+    else:
+        c.query_scale = float(np.float32(v.get("query_pre_attn_scalar", hd_local)) ** np.float32(-0.5))
+        c.v_norm = 0
+        c.norm_offset = float(v.get("omg_norm_offset", 1.0))
+    c.softcap, c.bos = float(v.get("final_logit_softcapping", 0.0) or 0.0), int(v.get("bos_token_id", 2))
+    c.per_layer_dim = int(v.get("hidden_size_per_layer_input", 0))
     return c
 
 

@@ -172,16 +172,21 @@ enum {
     T_UP,
     T_DOWN,
     T_POST_FFN_NORM,
+    T_PL_GATE,
+    T_PL_PROJ,
+    T_PL_NORM,
+    T_OUT_SCALE,
     T_COUNT
 };
 static const char *LAYER_NAMES[T_COUNT] = {"attn_norm", "qkv", "q_norm", "k_norm",
                                            "o", "post_attn_norm", "ffn_norm", "gate",
-                                           "up", "down", "post_ffn_norm"};
+                                           "up", "down", "post_ffn_norm", "pl_gate",
+                                           "pl_proj", "pl_norm", "out_scale"};
 
 struct orc_model {
     orc_config cfg;
     int gpu;
-    orc_tensor embed, final_norm;
+    orc_tensor embed, final_norm, pl_model_proj, pl_proj_norm, per_layer_table;
     orc_tensor layer[ORC_MAX_LAYERS][T_COUNT];
 };
 
@@ -210,6 +215,9 @@ void orc_model_free(orc_model *m) {
     if (!m) return;
     tensor_free(&m->embed);
     tensor_free(&m->final_norm);
+    tensor_free(&m->pl_model_proj);
+    tensor_free(&m->pl_proj_norm);
+    tensor_free(&m->per_layer_table);
     for (int l = 0; l < ORC_MAX_LAYERS; l++)
         for (int k = 0; k < T_COUNT; k++) tensor_free(&m->layer[l][k]);
     free(m);
@@ -219,13 +227,20 @@ static orc_tensor *lookup(orc_model *m, const char *name, int *is_linear) {
     *is_linear = 0;
     if (!strcmp(name, "embed")) return &m->embed;
     if (!strcmp(name, "final_norm")) return &m->final_norm;
+    if (!strcmp(name, "pl_model_proj")) {
+        *is_linear = 1;
+        return &m->pl_model_proj;
+    }
+    if (!strcmp(name, "pl_proj_norm")) return &m->pl_proj_norm;
+    if (!strcmp(name, "per_layer_table")) return &m->per_layer_table;
     int l;
     char rest[64];
     if (sscanf(name, "blk.%d.%63s", &l, rest) != 2) return NULL;
     if (l < 0 || l >= m->cfg.layers) return NULL;
     for (int k = 0; k < T_COUNT; k++) {
         if (!strcmp(rest, LAYER_NAMES[k])) {
-            *is_linear = (k == T_QKV || k == T_O || k == T_GATE || k == T_UP || k == T_DOWN);
+            *is_linear = (k == T_QKV || k == T_O || k == T_GATE || k == T_UP || k == T_DOWN || k == T_PL_GATE ||
+                          k == T_PL_PROJ);
             return &m->layer[l][k];
         }
     }
@@ -265,9 +280,14 @@ int orc_model_missing(const orc_model *m, char *buf, size_t len) {
     } while (0)
     if (!m->embed.present) MISS("embed");
     if (!m->final_norm.present) MISS("final_norm");
+    const int pl = m->cfg.per_layer_dim > 0;
+    if (pl && !m->pl_model_proj.present) MISS("pl_model_proj");
+    if (pl && !m->pl_proj_norm.present) MISS("pl_proj_norm");
+    if (pl && !m->per_layer_table.present) MISS("per_layer_table");
     for (int l = 0; l < m->cfg.layers; l++) {
         for (int k = 0; k < T_COUNT; k++) {
             if (k == T_K_NORM && !has_kv(&m->cfg, l)) continue;
+            if (k >= T_PL_GATE && !pl) continue;
             if (!m->layer[l][k].present) {
                 char nm[64];
                 snprintf(nm, sizeof nm, "blk.%d.%s", l, LAYER_NAMES[k]);
@@ -383,6 +403,34 @@ int orc_forward(const orc_model *m, const uint32_t *ids, const int32_t *pos, con
     float sc = sqrtf((float)d);
     for (int64_t i = 0; i < t; i++)
         for (int64_t k = 0; k < d; k++) x[i * d + k] = m->embed.w[(int64_t)ids[i] * d + k] * sc;
+    /* Per-layer inputs [t][layers x P], reference.rs:190-215. */
+    const int64_t P = c->per_layer_dim, PL = P * c->layers;
+    float *pli = NULL;
+    if (P > 0) {
+        pli = (float *)malloc((size_t)(t * PL) * 4);
+        float *xr = (float *)malloc((size_t)(t * d) * 4);
+        memcpy(xr, x, (size_t)(t * d) * 4);
+        if (m->gpu) round_rows(xr, t * d);
+        float *proj = (float *)malloc((size_t)(t * PL) * 4);
+        linear(xr, t, d, m->pl_model_proj.w, PL, proj);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < t; i++) {
+            float slice[1024], nv[1024];
+            for (int l = 0; l < c->layers; l++) {
+                for (int64_t j = 0; j < P; j++) slice[j] = proj[i * PL + l * P + j] / sqrtf((float)d);
+                rmsnorm(slice, P, m->pl_proj_norm.w, c->eps, c->norm_offset, nv);
+                for (int64_t j = 0; j < P; j++) {
+                    /* engine.rs:1370-1381 gathers the table rows as f16 */
+                    float tv = m->per_layer_table.w[(int64_t)ids[i] * PL + l * P + j];
+                    if (m->gpu) tv = r16(tv);
+                    const float e = tv * sqrtf((float)P);
+                    pli[i * PL + l * P + j] = (nv[j] + e) / sqrtf(2.0f);
+                }
+            }
+        }
+        free(xr);
+        free(proj);
+    }
 
     for (int l = 0; l < c->layers; l++) {
         const orc_tensor *L = m->layer[l];
@@ -489,7 +537,29 @@ int orc_forward(const orc_model *m, const uint32_t *ids, const int32_t *pos, con
             rmsnorm(a + i * d, d, L[T_POST_FFN_NORM].w, c->eps, c->norm_offset, tmp);
             for (int64_t k = 0; k < d; k++) x[i * d + k] += tmp[k];
         }
+        if (P > 0) {
+            /* reference.rs:323-341: x += rmsnorm(pl_proj . (gelu(x . pl_gate) * pli[l])); x *= out_scale. */
+            float *xr = (float *)malloc((size_t)(t * d) * 4);
+            float *gp = (float *)malloc((size_t)(t * P) * 4);
+            memcpy(xr, x, (size_t)(t * d) * 4);
+            if (m->gpu) round_rows(xr, t * d);
+            linear(xr, t, d, L[T_PL_GATE].w, P, gp);
+            for (int64_t i = 0; i < t; i++)
+                for (int64_t j = 0; j < P; j++) gp[i * P + j] = gelu(gp[i * P + j]) * pli[i * PL + l * P + j];
+            if (m->gpu) round_rows(gp, t * P);
+            linear(gp, t, P, L[T_PL_PROJ].w, d, a);
+            const float scale = L[T_OUT_SCALE].w[0];
+#pragma omp parallel for schedule(static)
+            for (int64_t i = 0; i < t; i++) {
+                float tmp[8192];
+                rmsnorm(a + i * d, d, L[T_PL_NORM].w, c->eps, c->norm_offset, tmp);
+                for (int64_t k = 0; k < d; k++) x[i * d + k] = (x[i * d + k] + tmp[k]) * scale;
+            }
+            free(xr);
+            free(gp);
+        }
     }
+    free(pli);
     norm_rows(x, t, d, &m->final_norm, c->eps, c->norm_offset, hidden);
     for (int l = 0; l < c->layers; l++) {
         free(kstore[l]);

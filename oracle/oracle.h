@@ -54,6 +54,7 @@ typedef struct {
     int32_t v_norm;
     float softcap;
     int32_t bos;
+    int32_t per_layer_dim; /* Gemma 4 per-layer inputs (0 = none) */
 } orc_config;
 
 /* ---- scalars ---- */

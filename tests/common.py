@@ -28,6 +28,18 @@ def gguf_tiny(heads: int = 4, kv_heads: int = 1, **over) -> str:
     return g.config_json(**kw)
 
 
+def gemma4_tiny(heads: int = 4, kv_heads: int = 1, **over) -> str:
+    """reference.rs:66-104: vocab 64, d 64, 4 layers, head_dim 256 / 512
+    (sliding / global), ff 96, 96, 192, 192, layers 2 and 3 reading the K/V
+    of layers 0 and 1, RoPE on 256 / 128 dims, window 5, V norm, per-layer
+    inputs of 32, softcap 30; (heads, kv_heads) = (8, 2) is the GQA variant."""
+    kw = dict(vocab=64, d=64, layers=4, heads=heads, kv_heads=kv_heads, head_dim=256, global_head_dim=512, ff=96,
+              double_wide_mlp=True, shared_kv_layers=2, window=5, sliding=[True, False, True, False],
+              partial_rotary_global=0.25, per_layer_dim=32, softcap=30.0)
+    kw.update(over)
+    return g.gemma4_config_json(**kw)
+
+
 def build(cfg: str, seed: int, linear: int, embed: int, capacity: int = 64, max_rows: int = 16,
           oracle_models: bool = True):
     """(engine, plain f32 oracle, GPU-rounding oracle, weights) on identical

@@ -156,3 +156,37 @@ def test_export_dir_round_trip(tmp_path):
     for x, y in zip(a, b):
         assert x.dtype == y.dtype and x.shape == y.shape
         assert np.array_equal(x.data, y.data) and np.array_equal(x.scales, y.scales)
+
+
+def test_gemma4_export_dir_round_trip(tmp_path):
+    """A Gemma 4 checkpoint's per-layer token table travels in
+    per_layer_table.bin under the manifest's per_layer_table entry
+    (model.rs:744-750) and reads back unchanged."""
+    import json
+    from tests.common import gemma4_tiny
+    cfg = gemma4_tiny()
+    w = g.Weights.synth(cfg, 23, g.Q4, g.Q8)
+    ts = {t.name: t for t in w.tensors()}
+    assert ts["per_layer_table"].shape == (64, 4 * 32) and list(ts)[-1] == "per_layer_table"
+    g.export_dir(w, tmp_path)
+    man = json.loads((tmp_path / "manifest.json").read_text())
+    assert man["per_layer_table"]["path"] == "per_layer_table.bin"
+    assert all(f["path"] != "per_layer_table.bin" for f in man["files"])
+    back = {t.name: t for t in g.Weights.load_dir(tmp_path).tensors()}
+    assert set(back) == set(ts)
+    for k, t in ts.items():
+        assert np.array_equal(t.data, back[k].data) and np.array_equal(t.scales, back[k].scales), k
+
+
+@pytest.mark.parametrize("edit,match", [
+    (lambda c: c.update(global_head_dim=384), "head_dim"),
+    (lambda c: c.update(hidden_size_per_layer_input=48), "per_layer_input"),
+    (lambda c: c.update(num_kv_shared_layers=4), "num_kv_shared_layers"),
+])
+def test_gemma4_config_validation(edit, match):
+    import json
+    from tests.common import gemma4_tiny
+    c = json.loads(gemma4_tiny())
+    edit(c)
+    with pytest.raises(L.OmgError, match=match):
+        g.EngineBuilder(json.dumps(c))
