@@ -3,7 +3,8 @@
 Every oracle function is checked against something other than a retyping
 of its own formula: the reference's own unit-test answers, published test
 vectors, an independent implementation (numpy's IEEE binary16, Hugging Face
-transformers' Gemma 3 in float64 via tests/golden/hf_gemma3.npz), closed
+transformers' Gemma 3 and Gemma 4 in float64 via tests/golden/hf_gemma3.npz
+and hf_gemma4.npz), closed
 forms, or answers worked out by hand from the reference's definitions.
 """
 from __future__ import annotations
@@ -20,6 +21,7 @@ import oracle
 from tests.common import rel_diff
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "hf_gemma3.npz"
+GOLDEN4 = Path(__file__).resolve().parent / "golden" / "hf_gemma4.npz"
 
 
 # ----------------------------------------------------------- f16 rounding
@@ -147,8 +149,8 @@ def test_q4_known_codes():
 
 # -------------------------------------------------------------- forward
 
-def golden_cases():
-    z = np.load(GOLDEN)
+def golden_cases(path=GOLDEN):
+    z = np.load(path)
     names = sorted({k.split("/")[0] for k in z.files})
     for n in names:
         cfg = z[n + "/config"].tobytes().decode()
@@ -182,6 +184,65 @@ def test_forward_matches_hf_gemma3(case):
     # the GPU rounding points (f16 operands) stay within f16 precision
     got16 = oracle.Model(cfg, ts, gpu_rounding=True).forward(ids, pos, seq)
     assert rel_diff(got16, hidden) < 2e-3
+
+
+@pytest.mark.parametrize("case", [c[0] for c in golden_cases(GOLDEN4)])
+def test_forward_matches_hf_gemma4(case):
+    """Gemma 4 (reference.rs:66-104 shapes): head_dim 512 global layers with
+    partial RoPE, shared K/V, V norm, per-layer inputs and output scalars,
+    against transformers' Gemma4TextModel in float64 (whose RMSNorm runs
+    in float32, hence the looser bound)."""
+    n, cfg, seed, lin, emb, request, hidden = next(c for c in golden_cases(GOLDEN4) if c[0] == case)
+    ts = list(g.Weights.synth(cfg, seed, lin, emb).tensors())
+    ids, pos, seq = flat_request(request)
+    got = oracle.Model(cfg, ts).forward(ids, pos, seq)
+    assert got.shape == hidden.shape
+    assert rel_diff(got, hidden) < 3e-5, rel_diff(got, hidden)  # measured 5.7e-6 and 9.9e-6
+    got16 = oracle.Model(cfg, ts, gpu_rounding=True).forward(ids, pos, seq)
+    assert rel_diff(got16, hidden) < 2e-2
+
+
+def test_gemma4_forward_mistakes_would_be_caught():
+    """Planted mistakes in the Gemma 4 pieces miss the fixture by far more
+    than the tolerance: no per-layer inputs (table zeroed), K/V not shared
+    (the shared layers' own K/V: a config without sharing, the same weights
+    where they exist), full RoPE on the global layers."""
+    n, cfg, seed, lin, emb, request, hidden = next(golden_cases(GOLDEN4))
+    ts = list(g.Weights.synth(cfg, seed, lin, emb).tensors())
+    ids, pos, seq = flat_request(request)
+    zeroed = [g.QTensor(t.name, t.dtype, t.shape, np.zeros_like(t.data), np.zeros_like(t.scales))
+              if t.name == "per_layer_table" else t for t in ts]
+    assert rel_diff(oracle.Model(cfg, zeroed).forward(ids, pos, seq), hidden) > 1e-2
+    c = json.loads(cfg)
+    c["rope_parameters"]["full_attention"]["partial_rotary_factor"] = 1.0
+    assert rel_diff(oracle.Model(json.dumps(c), ts).forward(ids, pos, seq), hidden) > 1e-2
+    c = json.loads(cfg)
+    c["num_kv_shared_layers"], c["use_double_wide_mlp"], c["intermediate_size"] = 0, False, [96, 96, 192, 192]
+    by_name = {t.name: t for t in ts}
+    # The shared layers (2, 3) get their sources' (0, 1) K/V rows and k_norm.
+    extra = [(l, by_name[f"blk.{l}.qkv"], by_name[f"blk.{l - 2}.qkv"]) for l in (2, 3)]
+    rebuilt = []
+    for t in ts:
+        hit = next((e for e in extra if t.name == f"blk.{e[0]}.qkv"), None)
+        if hit is None:
+            rebuilt.append(t)
+            continue
+        l, q, src = hit
+        rows_q = q.shape[0]
+        per_row = q.data.size // rows_q
+        kv_rows = src.shape[0] - rows_q
+        data = np.concatenate([q.data.reshape(rows_q, per_row), src.data.reshape(src.shape[0], per_row)[rows_q:]])
+        sp = q.scales.size // rows_q if q.scales.size else 0
+        scales = (np.concatenate([q.scales.reshape(rows_q, sp), src.scales.reshape(src.shape[0], sp)[rows_q:]])
+                  if sp else q.scales)
+        rebuilt.append(g.QTensor(t.name, t.dtype, (rows_q + kv_rows, q.shape[1]), data.ravel(), scales.ravel()))
+        rebuilt.append(g.QTensor(f"blk.{l}.k_norm", by_name[f"blk.{l - 2}.k_norm"].dtype,
+                                 by_name[f"blk.{l - 2}.k_norm"].shape, by_name[f"blk.{l - 2}.k_norm"].data,
+                                 by_name[f"blk.{l - 2}.k_norm"].scales))
+    unshared = oracle.Model(json.dumps(c), rebuilt).forward(ids, pos, seq)
+    # Same K/V projections and norms as the source layers, but each layer
+    # projects its own input: the rows move well outside the bound.
+    assert rel_diff(unshared, hidden) > 1e-2
 
 
 def test_forward_mistakes_would_be_caught():
