@@ -10,7 +10,10 @@ the resident state, T = 384) and the API wall times (host upload and
 readback included) are reported beside it.
 
 `--config c4` measures BASELINE.json configs[3] instead: the Laya encoder
-path over 192 sequences of 256 tokens (see bench_encoder).
+path over 192 sequences of 256 tokens (see bench_encoder).  `--config e2b`
+measures the reference's published Gemma 4 workload (E2B-shaped Q4_0, 12
+questions over a 2,000-token state; see bench_gemma4) as cold and warm
+latency against the published figures.
 
 Prints one JSON line (see the repository's driver contract).
 """
@@ -96,6 +99,8 @@ def main() -> int:
 
     if args.config == "c4":
         return bench_encoder(args)
+    if args.config == "e2b":
+        return bench_gemma4(args)
 
     import grande_amd as g
     from grande_amd import BranchTokens, Group, Want
@@ -254,6 +259,132 @@ def encoder_pairs(n: int, window: int) -> int:
     if not window:
         return n * n
     return sum(min(n, i + window + 1) - max(0, i - window) for i in range(n))
+
+
+def gemma4_layer_shapes(mc) -> list[dict]:
+    """Per layer: sliding, head_dim, own K/V, ff (model.rs:95-210)."""
+    L, shared = mc["layers"], mc["shared_kv_layers"]
+    out = []
+    for i in range(L):
+        s = mc["sliding"][i]
+        out.append(dict(sliding=s, hd=mc["head_dim"] if s else mc["global_head_dim"], own_kv=i < L - shared,
+                        ff=mc["ff"] * (2 if mc["double_wide_mlp"] and i >= L - shared else 1)))
+    return out
+
+
+def pairs_one_layer(prefix: int, bts: list, window: int) -> int:
+    """Query-key pairs the block-causal mask admits on one layer (window 0
+    = global) for one state and branches of lengths `bts`."""
+    total = 0
+    for q in range(prefix):
+        total += min(q + 1, window) if window else q + 1
+    for bt in bts:
+        for j in range(bt):
+            qp = prefix + j
+            vis_prefix = prefix if not window else max(0, min(prefix, prefix - (qp - window + 1)))
+            total += vis_prefix + (j + 1 if not window else min(j + 1, window))
+    return total
+
+
+def bench_gemma4(args) -> int:
+    """The reference's published Gemma 4 workload (docs/comparison.md:92,
+    116): E2B-shaped Q4_0, one 2,000-token state and 12 question branches
+    (663 tokens), label readout at each branch's last position.  A step is
+    one cold pass (T = 2,663) with the inputs in HBM; the warm pass
+    (branches only on the resident state) beside it.  The published
+    figures are wall-clock on an Apple M4 GPU; `vs_baseline` divides this
+    latency by the cold one (lower is better)."""
+    import grande_amd as g
+    from grande_amd import BranchTokens, Group, Want
+
+    spec = g.GEMMA4_CONFIGS[args.config]
+    mc = spec["model"]
+    cfg = g.gemma4_config_json(**mc)
+    P, bts = spec["state"], spec["branch_tokens"]
+    T = P + sum(bts)
+    rng = np.random.default_rng(SEED)
+    prefix = rng.integers(0, mc["vocab"], P).tolist()
+    branches = [BranchTokens(rng.integers(0, mc["vocab"], bt).tolist(), [bt - 1]) for bt in bts]
+    labels = g.LABEL_IDS
+    t0 = time.perf_counter()
+    eng = g.Engine.new(g.Weights.synth(cfg, SEED, spec["dtype"], spec["dtype"]), T + 64, 64)
+    load_s = time.perf_counter() - t0
+    eng.evict_resident()
+    t = time.perf_counter()
+    cold_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    api_cold_ms = (time.perf_counter() - t) * 1e3
+    t = time.perf_counter()
+    warm_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    api_warm_ms = (time.perf_counter() - t) * 1e3
+    warm_equal_cold = max(float(np.max(np.abs(a.rows[0] - b.rows[0]))) for a, b in zip(cold_rows, warm_rows))
+
+    def timed(first_resident: bool, steps: int, warmup: int) -> float:
+        eng.prepare([Group(prefix, branches)], Want.LABELS, labels, first_resident=first_resident)
+        for _ in range(warmup):
+            eng.launch()
+        eng.sync()
+        t = time.perf_counter()
+        for _ in range(steps):
+            eng.launch()
+        eng.sync()
+        return (time.perf_counter() - t) / steps
+
+    eng.evict_resident()
+    cold_s = timed(False, args.steps, args.warmup)
+    eng.evaluate(prefix, branches, Want.LABELS, labels)
+    warm_s = timed(True, args.steps, args.warmup)
+    eng.profile(True)
+    timed(False, args.steps, 0)
+    prof = eng.profile_report()
+    eng.profile(False)
+
+    shapes = gemma4_layer_shapes(mc)
+    d, H, KV, Pl = mc["d"], mc["heads"], mc["kv_heads"], mc["per_layer_dim"]
+    flop = {"mm_qkv": 0.0, "mm_o": 0.0, "mm_gate_up": 0.0, "mm_down": 0.0, "attention": 0.0}
+    for s in shapes:
+        flop["mm_qkv"] += 2.0 * T * d * (H + (2 * KV if s["own_kv"] else 0)) * s["hd"]
+        flop["mm_o"] += 2.0 * T * d * H * s["hd"]
+        flop["mm_gate_up"] += 4.0 * T * d * s["ff"]
+        flop["mm_down"] += 2.0 * T * d * s["ff"]
+        flop["attention"] += 4.0 * H * s["hd"] * pairs_one_layer(P, bts, mc["window"] if s["sliding"] else 0)
+    kernels = {}
+    total_ms = sum(v[1] for v in prof.values())
+    for name, (n, ms) in prof.items():
+        entry = {"launches_per_step": n // args.steps, "avg_us": round(ms / n * 1e3, 2), "share": round(ms / total_ms, 4)}
+        if name in flop:
+            tf = flop[name] * args.steps / (ms * 1e-3) / 1e12
+            entry.update(tflops=round(tf, 1), mfma_frac=round(tf / PEAK_F16_TFLOPS, 4))
+        kernels[name] = entry
+    pub = spec["published_ms"]
+    out = {
+        "metric": "cold latency (Gemma 4 E2B-shaped Q4_0, 12 Qs, 2,000-token state, 2,663 tokens), 1 GPU",
+        "value": round(cold_s * 1e3, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(cold_s * 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(cold_s * 1e3 / pub["cold"], 6),
+        "dtype": "q4_0 weights, f16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded random-init weights and token ids)",
+        "config": {"workload": f"{args.config}: Gemma 4 E2B-shaped Q4_0 (35 layers, d 1536, head_dim 256/512, "
+                               "20 K/V-sharing layers, per-layer inputs 256), vocab 25k, state 2000 + 12 branches "
+                               "(663 tokens), 26-label readout", "tokens": T, "state_tokens": P, "branches": len(bts)},
+        "published_ms": pub,
+        "warm_ms": round(warm_s * 1e3, 4),
+        "warm_vs_published": round(warm_s * 1e3 / pub["warm"], 6),
+        "questions_per_s": round(len(bts) / cold_s, 2),
+        "cold_tok_per_s": round(T / cold_s, 1),
+        "api_ms": {"cold": round(api_cold_ms, 3), "warm": round(api_warm_ms, 3)},
+        "warm_vs_cold_max_abs_logit": warm_equal_cold,
+        "pass_tflops": round(sum(flop.values()) / cold_s / 1e12, 2),
+        "kernels": kernels,
+        "load_s": round(load_s, 2),
+    }
+    print(json.dumps(out))
+    return 0
 
 
 def bench_encoder(args) -> int:

@@ -7,8 +7,8 @@ kernels behind the C ABI in include/omg_hip.h (libomg_hip.so).
 from ._lib import OmgError
 from .engine import (BranchOutput, BranchTokens, DeviceWeight, Engine, EngineBuilder, Group, GroupOutput,
                      PrefixSource, Want, pack, state_check, state_key)
-from .model import (BASELINE_CONFIGS, F16, LABEL_IDS, Q4, Q8, QTensor, Weights, config_json, export_dir,
-                    gemma4_config_json, quantize)
+from .model import (BASELINE_CONFIGS, F16, GEMMA4_CONFIGS, LABEL_IDS, Q4, Q8, QTensor, Weights, config_json,
+                    export_dir, gemma4_config_json, quantize)
 
 __all__ = [
     "BASELINE_CONFIGS", "BranchOutput", "BranchTokens", "DeviceWeight", "Engine", "EngineBuilder", "F16", "Group",

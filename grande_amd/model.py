@@ -107,6 +107,22 @@ BASELINE_CONFIGS = {
     "c5": dict(model=GEMMA3_4B, dtype=Q4, state=8000, branches=208, branch_tokens=40),
 }
 
+# The reference's published Gemma 4 figures (docs/comparison.md:92,116):
+# E2B Q4_0, vocabulary pruned, 12 questions over a 2,000-token state, 2,663
+# tokens in all.  Shape as the E2B checkpoint's config: 35 layers of d 1,536,
+# 8 query heads over 1 K/V head, head_dim 256 (sliding, window 512) / 512
+# (global, every 5th layer, RoPE on a quarter), ff 6,144 (12,288 on the 20
+# layers that share K/V), per-layer inputs of 256, softcap 30; the pruned
+# vocabulary taken as 25,000 rows like the other configs.
+GEMMA4_E2B = dict(vocab=25_000, d=1536, layers=35, heads=8, kv_heads=1, head_dim=256, global_head_dim=512, ff=6144,
+                  double_wide_mlp=True, shared_kv_layers=20, window=512,
+                  sliding=[(i + 1) % 5 != 0 for i in range(35)], partial_rotary_global=0.25, per_layer_dim=256,
+                  softcap=30.0)
+GEMMA4_CONFIGS = {
+    "e2b": dict(model=GEMMA4_E2B, dtype=Q4, state=2000, branch_tokens=[56] * 3 + [55] * 9,
+                published_ms={"cold": 8100.0, "warm": 2030.0}),
+}
+
 # The 26 label tokens read at each branch's answer position: option letters
 # A..Z (omg-core readout.rs:11-15) mapped to fixed ids of the synthetic vocab.
 LABEL_IDS = list(range(256, 256 + 26))
