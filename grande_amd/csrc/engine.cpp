@@ -12,6 +12,11 @@
 #include <cstdio>
 #include <fstream>
 
+// Most split-K partials of one product (a_ holds this many).
+#ifndef OMG_KSPLIT
+#define OMG_KSPLIT 4
+#endif
+
 namespace omg {
 
 // ------------------------------------------------------------------ pack
@@ -353,7 +358,8 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.qkv_ = DevBuf(size_t(cap * c.max_qkv()) * 4);
     E.q16_ = DevBuf(size_t(cap * c.heads * hd) * 2);
     E.attn_ = DevBuf(size_t(cap * c.heads * hd) * 2);
-    E.a_ = DevBuf(size_t(cap * d) * 4);
+    // a_ holds up to OMG_KSPLIT split-K partials of the o / down products.
+    E.a_ = DevBuf(size_t(cap * d) * 4 * OMG_KSPLIT);
     E.act_ = DevBuf(size_t(cap * c.max_ff()) * 2);
     E.rows_ = DevBuf(size_t(max_rows * d) * 4);
     const int64_t width = std::max(c.vocab, d);
@@ -572,6 +578,20 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     }
 }
 
+// K splits of the deep o / down products (K >= 4096, output width n <=
+// 2048): one per 2048 of K, at most OMG_KSPLIT, whole 64-wide stages per
+// split.  Their tiles are few (a 96 x 128 tile grid over n <= 2048 columns
+// fills the 256 CUs only past ~2,000 rows) and each runs K / 64 stages in
+// series; the splits run side by side and the residual norm adds them.  A
+// function of the shape only, so a row's sums do not depend on the pass
+// (rows over a resident prefix stay bit-equal to a full pass).
+static int ksplit(int64_t k, int64_t n) {
+    if (k < 4096 || n > 2048) return 1;
+    int s = int(std::min<int64_t>(OMG_KSPLIT, k / 2048));
+    while (s > 1 && k % (64 * s) != 0) --s;
+    return s;
+}
+
 void Engine::forward(int64_t t, int64_t base) {
     const Config& c = cfg_;
     const int64_t d = c.d;
@@ -642,24 +662,28 @@ void Engine::forward(int64_t t, int64_t base) {
         if (n_merges_[kind] > 0)
             step("attention_merge",
                  [&] { launch_attention_merge(stream_, att, attn_merges_[kind].as<int4>(), n_merges_[kind]); });
+        const int so = ksplit(c.heads * hd, d), sd = ksplit(ff, d);
+        const int64_t pstride = capacity_ * d;
         step("mm_o", [&] {
-            launch_gemm(stream_, attn_.as<half_t>(), c.heads * hd, L.o.w, a_.as<float>(), d, t);
+            launch_gemm_splitk(stream_, attn_.as<half_t>(), c.heads * hd, L.o.w, a_.as<float>(), d, t, so, pstride);
         });
         step("norm", [&] {
             launch_residual_norm(stream_, a_.as<float>(), L.post_attn_norm.as<float>(), x_.as<float>(),
-                                 L.ffn_norm.as<float>(), hn_.as<half_t>(), t, d, c.eps, 1.0f);
+                                 L.ffn_norm.as<float>(), hn_.as<half_t>(), t, d, c.eps, 1.0f, so, pstride);
         });
         step("mm_gate_up", [&] {
             launch_gemm_geglu(stream_, hn_.as<half_t>(), d, L.gate.w, L.up.w, act_.as<half_t>(), ff, t);
         });
-        step("mm_down", [&] { launch_gemm(stream_, act_.as<half_t>(), ff, L.down.w, a_.as<float>(), d, t); });
+        step("mm_down", [&] {
+            launch_gemm_splitk(stream_, act_.as<half_t>(), ff, L.down.w, a_.as<float>(), d, t, sd, pstride);
+        });
         // The last layer's stream is normed at the wanted rows only (readout).
         const float* next = l + 1 < c.layers ? layers_[size_t(l + 1)].attn_norm.as<float>() : nullptr;
         half_t* next_hn = next ? hn_.as<half_t>() : nullptr;
         if (P == 0) {
             step("norm", [&] {
                 launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), next,
-                                     next_hn, t, d, c.eps, 1.0f);
+                                     next_hn, t, d, c.eps, 1.0f, sd, pstride);
             });
             continue;
         }
@@ -667,7 +691,7 @@ void Engine::forward(int64_t t, int64_t base) {
         // feed-forward, as f16, gates the layer's slice of the inputs.
         step("norm", [&] {
             launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), nullptr,
-                                 x16_.as<half_t>(), t, d, c.eps, 1.0f);
+                                 x16_.as<half_t>(), t, d, c.eps, 1.0f, sd, pstride);
         });
         step("mm_pl_gate", [&] { launch_gemm(stream_, x16_.as<half_t>(), d, L.pl_gate.w, plg_.as<float>(), P, t); });
         step("pl_gate", [&] {

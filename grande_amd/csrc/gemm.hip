@@ -68,6 +68,10 @@ struct GemmArgs {
     int64_t ldy;
     const uint16_t* bias;  // f16 per output column (EPI_RELU_F16; EPI_QKV, may be null)
     QkvHeads qkv;          // EPI_QKV
+    // Split K (EPI_F32): blockIdx.y = split z sums K range
+    // [z K / ksplit, (z + 1) K / ksplit) into y + z * part_stride.
+    int ksplit = 1;
+    int64_t part_stride = 0;
 };
 
 constexpr int RSRC_FLAGS = 0x00020000;  // raw (untyped) 32-bit buffer
@@ -163,7 +167,8 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     const int tile = (int(blockIdx.x) % 8) * per_xcd + int(blockIdx.x) / 8;
     if (tile >= ntiles) return;
     const int64_t n0 = int64_t(tile % ntn) * BN, m0 = int64_t(tile / ntn) * BM;
-    const int nk = int((K + G_BK - 1) / G_BK);
+    const int kbeg = int(blockIdx.y) * int(K / g.ksplit);  // this split's K range (multiples of G_BK)
+    const int nk = int((K / g.ksplit + G_BK - 1) / G_BK);
     const int K32 = int(K);
     const int64_t rows_m = M - m0 < BM ? M - m0 : BM;
     const int64_t rows_n = N - n0 < BN ? N - n0 : BN;
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     auto issue = [&](int s) {
         uint8_t* base = slot_base(s);
         const bool live = s < nk;
-        const int k0 = s * G_BK;
+        const int k0 = kbeg + s * G_BK;
         const int64_t xbytes = live ? rows_m * g.ldx * 2 : 0;
         // (Range checks cover the lane offset only: a row's offset plus the
         // stage offset stays inside the row, and rows past M are out of
@@ -436,7 +441,8 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
                     *reinterpret_cast<half4*>(static_cast<half_t*>(g.y) + m * g.ldy + n) =
                         half4{half_t(v[0]), half_t(v[1]), half_t(v[2]), half_t(v[3])};
                 } else {
-                    *reinterpret_cast<float4*>(static_cast<float*>(g.y) + m * g.ldy + n) =
+                    *reinterpret_cast<float4*>(static_cast<float*>(g.y) + int64_t(blockIdx.y) * g.part_stride +
+                                               m * g.ldy + n) =
                         make_float4(v[0], v[1], v[2], v[3]);
                 }
             } else {
@@ -446,7 +452,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
                     if constexpr (F16_OUT)
                         static_cast<half_t*>(g.y)[m * g.ldy + n + r] = half_t(v[r]);
                     else
-                        static_cast<float*>(g.y)[m * g.ldy + n + r] = v[r];
+                        static_cast<float*>(g.y)[int64_t(blockIdx.y) * g.part_stride + m * g.ldy + n + r] = v[r];
                 }
             }
         }
@@ -464,7 +470,7 @@ static void run(hipStream_t s, const GemmArgs& g) {
     }
     const int64_t N = g.w0.rows;
     const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + P::BM - 1) / P::BM);
-    const dim3 grid(unsigned((tiles + 7) / 8 * 8));
+    const dim3 grid(unsigned((tiles + 7) / 8 * 8), unsigned(g.ksplit));
     gemm_kernel<QUANT, MI, NJ, EPI, NS, NW, WM><<<grid, dim3(P::T), P::LDS, s>>>(g);
     OMG_HIP(hipGetLastError());
 }
@@ -543,6 +549,19 @@ void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w
     check(x, ldx, w, ldy, m);
     if (m == 0) return;
     dispatch_dtype<EPI_F32>(s, GemmArgs{x, ldx, m, w, w, y, ldy, nullptr, {}});
+}
+
+void launch_gemm_splitk(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
+                       int64_t m, int parts, int64_t part_stride) {
+    check(x, ldx, w, ldy, m);
+    if (parts < 1 || (parts > 1 && w.cols % (int64_t(G_BK) * parts) != 0))
+        fail(E_INVALID, "gemm_splitk: K must split into parts of whole 64-wide stages");
+    if (parts > 1 && part_stride < m * ldy) fail(E_INVALID, "gemm_splitk: partial outputs overlap");
+    if (m == 0) return;
+    GemmArgs g{x, ldx, m, w, w, y, ldy, nullptr, {}};
+    g.ksplit = parts;
+    g.part_stride = part_stride;
+    dispatch_dtype<EPI_F32>(s, g);
 }
 
 void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,

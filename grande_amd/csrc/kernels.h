@@ -39,9 +39,11 @@ void repack_q4(const uint8_t* src, uint8_t* dst, int64_t n);
 void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, int64_t t,
                        float embed_scale, const float* w, float eps, float* x, half_t* hn);
 // y = rmsnorm(a[r]) * w1;  x[r] = (y + x[r]) * scale;  if w2: hn[r] = f16(rmsnorm(x[r]) * w2),
-// else if hn: hn[r] = f16(x[r]).
+// else if hn: hn[r] = f16(x[r]).  With parts > 1, a[r] is the sum of the
+// split-K partials a[p * part_stride + r] in order p = 0, 1, ...
 void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float* x, const float* w2,
-                          half_t* hn, int64_t t, int64_t d, float eps, float scale);
+                          half_t* hn, int64_t t, int64_t d, float eps, float scale, int parts = 1,
+                          int64_t part_stride = 0);
 // Gemma 4 per-layer inputs (engine.rs:1651-1666, 1728-1750).  pl holds
 // f16(x) . pl_model_proj^T as [t][layers x P] and is replaced by
 // (rmsnorm(pl * proj_scale) * w + f16(table[ids[t], :]) * emb_scale) * out_scale.
@@ -109,6 +111,12 @@ struct QkvHeads {
 // y[M][N] (f32) = f16(X)[M][K] . deq(W)[N][K]^T, f32 accumulation.
 void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
                  int64_t m);
+// The same product with K split into `parts` ranges (K % (64 parts) == 0):
+// partial p (K range p) goes to y + p * part_stride; the sum is the
+// consumer's (launch_residual_norm).  More workgroups for narrow-N, deep-K
+// products; each partial's rows are independent of M.
+void launch_gemm_splitk(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
+                        int64_t m, int parts, int64_t part_stride);
 // act[M][F] (f16) = gelu(X . Wg^T) * (X . Wu^T); gelu_tanh, or the exact
 // (erf) form when `erf`.
 void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,

@@ -73,7 +73,8 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
                                                             float* __restrict__ x,
                                                             const float* __restrict__ w2,
                                                             half_t* __restrict__ hn, int64_t t,
-                                                            int64_t d, float eps, float scale) {
+                                                            int64_t d, float eps, float scale, int parts,
+                                                            int64_t part_stride) {
     const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
     const int64_t row = int64_t(blockIdx.x) * 4 + wave;
     if (row >= t) return;
@@ -86,6 +87,10 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
         const int64_t q = lane + j * WAVE;
         if (q < nq) {
             av[j] = *reinterpret_cast<const float4*>(ar + 4 * q);
+            for (int p = 1; p < parts; ++p) {
+                const float4 b = *reinterpret_cast<const float4*>(ar + p * part_stride + 4 * q);
+                av[j].x += b.x, av[j].y += b.y, av[j].z += b.z, av[j].w += b.w;
+            }
             xv[j] = *reinterpret_cast<const float4*>(xr + 4 * q);
             g1[j] = *reinterpret_cast<const float4*>(w1 + 4 * q);
             if (w2) g2[j] = *reinterpret_cast<const float4*>(w2 + 4 * q);
@@ -141,13 +146,16 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
 }
 
 void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float* x, const float* w2,
-                          half_t* hn, int64_t t, int64_t d, float eps, float scale) {
+                          half_t* hn, int64_t t, int64_t d, float eps, float scale, int parts,
+                          int64_t part_stride) {
     if (t <= 0) return;
     if (d % 4 != 0) fail(E_INVALID, "residual_norm: width must be a multiple of 4");
+    if (parts < 1 || (parts > 1 && (part_stride < t * d || part_stride % 4)))
+        fail(E_INVALID, "residual_norm: split-K partials");
     const int nv = int((d / 4 + WAVE - 1) / WAVE);
     const dim3 grid(unsigned((t + 3) / 4)), block(256);
 #define OMG_RN(N) \
-    case N: residual_norm_kernel<N><<<grid, block, 0, s>>>(a, w1, x, w2, hn, t, d, eps, scale); break;
+    case N: residual_norm_kernel<N><<<grid, block, 0, s>>>(a, w1, x, w2, hn, t, d, eps, scale, parts, part_stride); break;
     switch (nv) {
         OMG_RN(1) OMG_RN(2) OMG_RN(3) OMG_RN(4) OMG_RN(5) OMG_RN(6) OMG_RN(7) OMG_RN(8)
         OMG_RN(9) OMG_RN(10) OMG_RN(11) OMG_RN(12) OMG_RN(13) OMG_RN(14) OMG_RN(15) OMG_RN(16)
