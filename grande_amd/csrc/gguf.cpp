@@ -3,7 +3,7 @@
 // directory (metadata -> the HF-style text config Config::from_json reads;
 // q / k / v fused into one qkv tensor per layer; Q8_0 / Q4_0 blocks split
 // into codes and f16 scales; f32 / bf16 tensors to f16), done in C++ so a
-// GGUF loads without the export step.  Gemma 3 text models.
+// GGUF loads without the export step.  Gemma 3 and Gemma 4 text models.
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -139,7 +139,9 @@ Weights load_gguf(const std::string& path) {
     const size_t data0 = (r.at + align - 1) / align * align;
 
     const std::string arch = kv["general.architecture"].s("");
-    if (arch != "gemma3") fail(E_INVALID, "gguf: architecture " + arch + " (gemma3 supported)");
+    if (arch != "gemma3" && arch != "gemma4")
+        fail(E_INVALID, "gguf: architecture " + arch + " (gemma3 and gemma4 supported)");
+    const bool g4 = arch == "gemma4";
     auto g = [&](const std::string& k) -> const Json& {
         static const Json none;
         auto it = kv.find(arch + "." + k);
@@ -170,7 +172,7 @@ Weights load_gguf(const std::string& path) {
     {
         Json mt;
         mt.kind = Json::String;
-        mt.str = "gemma3_text";
+        mt.str = g4 ? "gemma4_text" : "gemma3_text";
         cfg.obj["model_type"] = mt;
     }
     setn("vocab_size", double(vocab));
@@ -211,7 +213,44 @@ Weights load_gguf(const std::string& path) {
     setn("rope_theta", need("rope.freq_base"));
     setn("rope_local_base_freq", g("rope.freq_base_swa").f64(10000.0));
     setn("final_logit_softcapping", g("final_logit_softcapping").f64(0.0));
-    setn("query_pre_attn_scalar", g("attention.query_pre_attn_scalar").f64(hd_swa));
+    if (g4) {
+        // export_wgpu_gguf.py:140-171: partial RoPE on the global layers is
+        // carried by rope_freqs (1.0 for rotated pairs, 1e30 for the rest);
+        // K/V sharing and the per-layer inputs by their own keys.
+        double rot_full = 1.0;
+        auto rf = infos.find("rope_freqs.weight");
+        if (rf != infos.end()) {
+            if (rf->second.type != G_F32) fail(E_INVALID, "gguf: rope_freqs.weight must be f32");
+            const int64_t n = rf->second.numel();
+            if (data0 + rf->second.offset + uint64_t(n) * 4 > file.size())
+                fail(E_INVALID, "gguf: rope_freqs.weight past the end of the file");
+            int64_t rotated = 0;
+            for (int64_t i = 0; i < n; ++i) {
+                float f;
+                std::memcpy(&f, file.data() + data0 + rf->second.offset + 4 * i, 4);
+                rotated += f < 1e10f;
+            }
+            rot_full = double(rotated) * 2.0 / hd_full;
+        }
+        Json rope;
+        rope.kind = Json::Object;
+        Json full, slide, x;
+        full.kind = slide.kind = Json::Object;
+        x.kind = Json::Number;
+        x.num = need("rope.freq_base");
+        full.obj["rope_theta"] = x;
+        x.num = rot_full;
+        full.obj["partial_rotary_factor"] = x;
+        x.num = g("rope.freq_base_swa").f64(10000.0);
+        slide.obj["rope_theta"] = x;
+        rope.obj["full_attention"] = full;
+        rope.obj["sliding_attention"] = slide;
+        cfg.obj["rope_parameters"] = rope;
+        setn("num_kv_shared_layers", g("attention.shared_kv_layers").f64(0.0));
+        setn("hidden_size_per_layer_input", g("embedding_length_per_layer_input").f64(0.0));
+    } else {
+        setn("query_pre_attn_scalar", g("attention.query_pre_attn_scalar").f64(hd_swa));
+    }
     setn("bos_token_id", kv.count("tokenizer.ggml.bos_token_id") ? kv["tokenizer.ggml.bos_token_id"].num : 2.0);
     setn("omg_norm_offset", 0.0);
 
@@ -282,6 +321,14 @@ Weights load_gguf(const std::string& path) {
     const Config& c = w.config;
     w.tensors["embed"] = convert({"token_embd.weight"}, {vocab, d});
     w.tensors["final_norm"] = convert({"output_norm.weight"}, {d});
+    const int64_t pl = c.per_layer_dim;
+    if (pl > 0) {
+        w.tensors["pl_model_proj"] = convert({"per_layer_model_proj.weight"}, {pl * layers, d});
+        w.tensors["pl_proj_norm"] = convert({"per_layer_proj_norm.weight"}, {pl});
+        const int64_t rows = infos.count("per_layer_token_embd.weight") ? infos["per_layer_token_embd.weight"].shape[0] : 0;
+        if (rows != vocab) fail(E_INVALID, "gguf: per_layer_token_embd.weight rows must match the vocabulary");
+        w.tensors["per_layer_table"] = convert({"per_layer_token_embd.weight"}, {vocab, pl * layers});
+    }
     for (int64_t l = 0; l < layers; ++l) {
         const std::string b = "blk." + std::to_string(l) + ".";
         const int64_t hd = c.head_dim[size_t(l)], ffl = c.ff[size_t(l)];
@@ -302,6 +349,12 @@ Weights load_gguf(const std::string& path) {
         w.tensors[b + "up"] = convert({b + "ffn_up.weight"}, {ffl, d});
         w.tensors[b + "down"] = convert({b + "ffn_down.weight"}, {d, ffl});
         w.tensors[b + "post_ffn_norm"] = convert({b + "post_ffw_norm.weight"}, {d});
+        if (pl > 0) {
+            w.tensors[b + "pl_gate"] = convert({b + "inp_gate.weight"}, {pl, d});
+            w.tensors[b + "pl_proj"] = convert({b + "proj.weight"}, {d, pl});
+            w.tensors[b + "pl_norm"] = convert({b + "post_norm.weight"}, {d});
+            w.tensors[b + "out_scale"] = convert({b + "layer_output_scale.weight"}, {1});
+        }
     }
     (void)version;
     return w;

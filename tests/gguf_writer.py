@@ -1,5 +1,6 @@
-"""A GGUF v3 writer for the tests: a Gemma 3 checkpoint in llama.cpp's
-tensor names and metadata keys (the ones tools/export_wgpu_gguf.py reads),
+"""A GGUF v3 writer for the tests: a Gemma 3 or Gemma 4 checkpoint in
+llama.cpp's tensor names and metadata keys (the ones
+tools/export_wgpu_gguf.py reads),
 written from a host checkpoint of this library (q / k / v split back out of
 the fused qkv tensor, Q8_0 / Q4_0 codes and scales interleaved into GGUF
 blocks).  There is no gguf package in the image; the format is GGUF v3 as
@@ -66,12 +67,18 @@ def write_gemma3(path: str | Path, config_text: str, weights: g.Weights, f32_nor
     GGUF stores Gemma 3 norms); 1-D tensors are written as f32 (or bf16 for
     the llama.cpp names in `bf16`)."""
     cfg = json.loads(config_text)
+    g4 = cfg.get("model_type") == "gemma4_text"
+    arch = "gemma4" if g4 else "gemma3"
     ts = {t.name: t for t in weights.tensors()}
     L, d, H, KV = cfg["num_hidden_layers"], cfg["hidden_size"], cfg["num_attention_heads"], cfg["num_key_value_heads"]
-    hd = cfg["head_dim"]
     types = cfg.get("layer_types")
     swa = [t == "sliding_attention" for t in types] if types else \
         [(i + 1) % cfg.get("_sliding_window_pattern", 6) != 0 for i in range(L)]
+    hd_swa = cfg["head_dim"]
+    hd_full = cfg.get("global_head_dim", hd_swa)
+    shared = cfg.get("num_kv_shared_layers", 0)
+    pl = cfg.get("hidden_size_per_layer_input", 0)
+    ffs = [ts[f"blk.{l}.gate"].shape[0] for l in range(L)]
     tensors: list[tuple[str, list[int], int, bytes]] = []
 
     def add(name, t: g.QTensor, shape, rows=None):
@@ -90,15 +97,29 @@ def write_gemma3(path: str | Path, config_text: str, weights: g.Weights, f32_nor
 
     add("token_embd.weight", ts["embed"], ts["embed"].shape)
     add("output_norm.weight", ts["final_norm"], [d])
+    if pl:
+        add("per_layer_model_proj.weight", ts["pl_model_proj"], [pl * L, d])
+        add("per_layer_proj_norm.weight", ts["pl_proj_norm"], [pl])
+        add("per_layer_token_embd.weight", ts["per_layer_table"], list(ts["per_layer_table"].shape))
+    if g4:
+        # partial RoPE of the global layers: 1.0 for rotated pairs, 1e30 for the rest
+        rot = cfg["rope_parameters"]["full_attention"].get("partial_rotary_factor", 1.0)
+        f = np.full(hd_full // 2, 1e30, np.float32)
+        f[: int(rot * hd_full) // 2] = 1.0
+        tensors.append(("rope_freqs.weight", [hd_full // 2], GG_F32, f.tobytes()))
     for l in range(L):
         b = f"blk.{l}."
+        hd = hd_swa if swa[l] else hd_full
+        own = l < L - shared
         add(b + "attn_norm.weight", ts[b + "attn_norm"], [d])
         qkv = ts[b + "qkv"]
         add(b + "attn_q.weight", qkv, [H * hd, d], (0, H * hd))
-        add(b + "attn_k.weight", qkv, [KV * hd, d], (H * hd, (H + KV) * hd))
-        add(b + "attn_v.weight", qkv, [KV * hd, d], ((H + KV) * hd, (H + 2 * KV) * hd))
+        if own:
+            add(b + "attn_k.weight", qkv, [KV * hd, d], (H * hd, (H + KV) * hd))
+            add(b + "attn_v.weight", qkv, [KV * hd, d], ((H + KV) * hd, (H + 2 * KV) * hd))
         add(b + "attn_q_norm.weight", ts[b + "q_norm"], [hd])
-        add(b + "attn_k_norm.weight", ts[b + "k_norm"], [hd])
+        if own:
+            add(b + "attn_k_norm.weight", ts[b + "k_norm"], [hd])
         add(b + "attn_output.weight", ts[b + "o"], [d, H * hd])
         add(b + "post_attention_norm.weight", ts[b + "post_attn_norm"], [d])
         add(b + "ffn_norm.weight", ts[b + "ffn_norm"], [d])
@@ -107,6 +128,11 @@ def write_gemma3(path: str | Path, config_text: str, weights: g.Weights, f32_nor
         add(b + "ffn_up.weight", ts[b + "up"], [ff, d])
         add(b + "ffn_down.weight", ts[b + "down"], [d, ff])
         add(b + "post_ffw_norm.weight", ts[b + "post_ffn_norm"], [d])
+        if pl:
+            add(b + "inp_gate.weight", ts[b + "pl_gate"], [pl, d])
+            add(b + "proj.weight", ts[b + "pl_proj"], [d, pl])
+            add(b + "post_norm.weight", ts[b + "pl_norm"], [d])
+            add(b + "layer_output_scale.weight", ts[b + "out_scale"], [1])
 
     head = bytearray(b"GGUF") + struct.pack("<I", 3)
     kvs = bytearray()
@@ -117,20 +143,33 @@ def write_gemma3(path: str | Path, config_text: str, weights: g.Weights, f32_nor
         _kv(kvs, key, vtype, value)
         n_kv += 1
 
-    kv("general.architecture", STR, "gemma3")
+    a = arch + "."
+    kv("general.architecture", STR, arch)
     kv("general.alignment", U32, 32)
-    kv("gemma3.block_count", U32, L)
-    kv("gemma3.embedding_length", U32, d)
-    kv("gemma3.attention.head_count", U32, H)
-    kv("gemma3.attention.head_count_kv", U32, KV)
-    kv("gemma3.attention.key_length", U32, hd)
-    kv("gemma3.feed_forward_length", U32, cfg["intermediate_size"])
-    kv("gemma3.attention.sliding_window", U32, cfg["sliding_window"])
-    kv("gemma3.attention.sliding_window_pattern", ARR, (BOOL, swa))
-    kv("gemma3.attention.layer_norm_rms_epsilon", F32, cfg.get("rms_norm_eps", 1e-6))
-    kv("gemma3.rope.freq_base", F32, cfg.get("rope_theta", 1e6))
-    kv("gemma3.rope.freq_base_swa", F32, cfg.get("rope_local_base_freq", 1e4))
-    kv("gemma3.attention.query_pre_attn_scalar", U32, int(cfg.get("query_pre_attn_scalar", hd)))
+    kv(a + "block_count", U32, L)
+    kv(a + "embedding_length", U32, d)
+    kv(a + "attention.head_count", U32, H)
+    kv(a + "attention.head_count_kv", U32, KV)
+    kv(a + "attention.key_length", U32, hd_full)
+    if g4:
+        kv(a + "attention.key_length_swa", U32, hd_swa)
+        kv(a + "feed_forward_length", ARR, (I32, ffs))
+    else:
+        kv(a + "feed_forward_length", U32, cfg["intermediate_size"])
+    kv(a + "attention.sliding_window", U32, cfg["sliding_window"])
+    kv(a + "attention.sliding_window_pattern", ARR, (BOOL, swa))
+    kv(a + "attention.layer_norm_rms_epsilon", F32, cfg.get("rms_norm_eps", 1e-6))
+    if g4:
+        rp = cfg["rope_parameters"]
+        kv(a + "rope.freq_base", F32, rp["full_attention"]["rope_theta"])
+        kv(a + "rope.freq_base_swa", F32, rp["sliding_attention"]["rope_theta"])
+        kv(a + "attention.shared_kv_layers", U32, shared)
+        kv(a + "embedding_length_per_layer_input", U32, pl)
+        kv(a + "final_logit_softcapping", F32, cfg.get("final_logit_softcapping", 0.0))
+    else:
+        kv(a + "rope.freq_base", F32, cfg.get("rope_theta", 1e6))
+        kv(a + "rope.freq_base_swa", F32, cfg.get("rope_local_base_freq", 1e4))
+        kv(a + "attention.query_pre_attn_scalar", U32, int(cfg.get("query_pre_attn_scalar", hd_swa)))
     kv("tokenizer.ggml.bos_token_id", U32, cfg.get("bos_token_id", 2))
     kv("tokenizer.ggml.tokens", ARR, (STR, [f"t{i}" for i in range(8)]))
     infos = bytearray()

@@ -1,4 +1,4 @@
-"""GGUF loading (omg_load_gguf): a llama.cpp Gemma 3 file read directly,
+"""GGUF loading (omg_load_gguf): a llama.cpp Gemma 3 or Gemma 4 file read directly,
 mapped as tools/export_wgpu_gguf.py:112-296 maps it; the files are written
 by tests/gguf_writer.py from seeded checkpoints.  CPU only: the tensors
 must come back bit-equal to the checkpoint they were written from (f32
@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import grande_amd as g
-from tests.common import gguf_tiny
+from tests.common import gemma4_tiny, gguf_tiny
 from tests.gguf_writer import write_gemma3
 
 
@@ -20,6 +20,27 @@ def test_gguf_tensors_round_trip(tmp_path, dtype):
     path = tmp_path / "m.gguf"
     write_gemma3(path, cfg, w)
     back = {t.name: t for t in g.Weights.load_gguf(path).tensors()}
+    orig = {t.name: t for t in w.tensors()}
+    assert sorted(back) == sorted(orig)
+    for name, t in orig.items():
+        b = back[name]
+        assert (b.dtype, tuple(b.shape)) == (t.dtype, tuple(t.shape)), name
+        assert np.array_equal(b.data, t.data) and np.array_equal(b.scales, t.scales), name
+
+
+@pytest.mark.parametrize("dtype", [g.Q8, g.Q4, g.F16])
+@pytest.mark.parametrize("heads,kv", [(4, 1), (8, 2)])
+def test_gguf_gemma4_tensors_round_trip(tmp_path, dtype, heads, kv):
+    """A gemma4 GGUF (export_wgpu_gguf.py:140-290): shared-K/V layers
+    without k / v tensors, head_dim 512 global layers whose partial RoPE
+    rides in rope_freqs, per-layer ff lengths, the per-layer input tensors
+    and token table, per-layer output scalars."""
+    cfg = gemma4_tiny(heads, kv)
+    w = g.Weights.synth(cfg, 3, dtype, dtype)
+    path = tmp_path / "m4.gguf"
+    write_gemma3(path, cfg, w)
+    loaded = g.Weights.load_gguf(path)
+    back = {t.name: t for t in loaded.tensors()}
     orig = {t.name: t for t in w.tensors()}
     assert sorted(back) == sorted(orig)
     for name, t in orig.items():
@@ -68,6 +89,23 @@ def test_engine_from_gguf_matches_engine_from_checkpoint(tmp_path):
     a = g.Engine.new(w, 128, 16)
     b = g.Engine.open_gguf(path, 128, 16)
     rng = np.random.default_rng(1)
+    prefix = rng.integers(0, 64, 30).tolist()
+    branches = [g.BranchTokens(rng.integers(0, 64, 7).tolist(), [6]) for _ in range(3)]
+    for x, y in zip(a.evaluate(prefix, branches, g.Want.HIDDEN), b.evaluate(prefix, branches, g.Want.HIDDEN)):
+        assert np.array_equal(x.rows[0], y.rows[0])
+
+
+@pytest.mark.gpu
+def test_engine_from_gemma4_gguf_matches_engine_from_checkpoint(tmp_path):
+    """Gemma 4: the engine opened from the GGUF (config from its metadata)
+    gives bit-equal rows to the engine built from the checkpoint."""
+    cfg = gemma4_tiny(8, 2)
+    w = g.Weights.synth(cfg, 8, g.Q4, g.Q8)
+    path = tmp_path / "m4.gguf"
+    write_gemma3(path, cfg, w)
+    a = g.Engine.new(w, 128, 16)
+    b = g.Engine.open_gguf(path, 128, 16)
+    rng = np.random.default_rng(2)
     prefix = rng.integers(0, 64, 30).tolist()
     branches = [g.BranchTokens(rng.integers(0, 64, 7).tolist(), [6]) for _ in range(3)]
     for x, y in zip(a.evaluate(prefix, branches, g.Want.HIDDEN), b.evaluate(prefix, branches, g.Want.HIDDEN)):
