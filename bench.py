@@ -31,6 +31,7 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+METRIC = "questions/sec + state prefill tok/s (Gemma-3-270M Q4_0, 2k state, 12 Qs), 1 GPU"
 PEAK_F16_TFLOPS = 2500.0   # MI355X dense FP16/BF16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 SEED = 0x5EED
@@ -107,6 +108,9 @@ def main() -> int:
 
     spec = g.BASELINE_CONFIGS[args.config]
     mc = spec["model"]
+    wname = {g.Q4: "q4_0", g.Q8: "q8_0", g.F16: "f16"}[spec["dtype"]]
+    size = {640: "270M", 1152: "1B", 2560: "4B"}.get(mc["d"], f"d{mc['d']}")
+    shape = f"Gemma-3-{size}-shaped {wname.upper()}"
     cfg = g.config_json(**mc)
     P, NB, BT = spec["state"], spec["branches"], spec["branch_tokens"]
     T = P + NB * BT
@@ -117,7 +121,7 @@ def main() -> int:
 
     t0 = time.perf_counter()
     weights = g.Weights.synth(cfg, SEED, spec["dtype"], spec["dtype"])
-    eng = g.Engine.new(weights, T + 64, 64)
+    eng = g.Engine.new(weights, T + 64, max(64, NB))
     load_s = time.perf_counter() - t0
 
     # API passes (host ids in, label logits out): cold, then warm on the
@@ -181,7 +185,7 @@ def main() -> int:
     total_flop = sum(flops.values()) * mc["layers"]
 
     out = {
-        "metric": "questions/sec + state prefill tok/s (Gemma-3-270M Q4_0, 2k state, 12 Qs), 1 GPU",
+        "metric": METRIC if args.config == "c2" else f"questions/sec ({args.config}: {shape}), 1 GPU",
         "value": round(NB / cold_s, 2),
         "unit": "questions/s",
         "n_gpus": 1,
@@ -191,9 +195,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights, f16 MFMA, f32 accumulate",
+        "dtype": f"{wname} weights, f16 MFMA, f32 accumulate",
         "data": "synthetic (seeded random-init weights and token ids)",
-        "config": {"workload": f"{args.config}: Gemma-3-270M-shaped Q4_0, vocab 25k, state {P} + {NB}x{BT} branches, "
+        "config": {"workload": f"{args.config}: {shape}, vocab 25k, state {P} + {NB}x{BT} branches, "
                                "26-label readout", "tokens": T, "state_tokens": P, "branches": NB,
                    "branch_tokens": BT},
         "cold_tok_per_s": round(T / cold_s, 1),

@@ -578,15 +578,18 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     }
 }
 
-// K splits of the deep o / down products (K >= 4096, output width n <=
-// 2048): one per 2048 of K, at most OMG_KSPLIT, whole 64-wide stages per
-// split.  Their tiles are few (a 96 x 128 tile grid over n <= 2048 columns
-// fills the 256 CUs only past ~2,000 rows) and each runs K / 64 stages in
-// series; the splits run side by side and the residual norm adds them.  A
-// function of the shape only, so a row's sums do not depend on the pass
-// (rows over a resident prefix stay bit-equal to a full pass).
+// K splits of the deep o / down products (output width n <= 2048): one
+// per 2048 of K, at most OMG_KSPLIT, whole 64-wide stages per split.
+// Their tiles are few and each runs K / 64 stages in series; the splits
+// run side by side and the residual norm adds them.  Widths up to 1280 get
+// 64-column tiles (twice the workgroups of the 128-column tiles above), so
+// they split from K 8192, wider ones from K 4096 (measured: Gemma 4 E2B's
+// K 4096 / 6144 / 12288 at n 1536 gain on cold and warm passes, the 1B's
+// K 6912 at n 1152 loses 3% cold).  A function of the shape only, so a
+// row's sums do not depend on the pass (rows over a resident prefix stay
+// bit-equal to a full pass).
 static int ksplit(int64_t k, int64_t n) {
-    if (k < 4096 || n > 2048) return 1;
+    if (n > 2048 || k < (n > 1280 ? 4096 : 8192)) return 1;
     int s = int(std::min<int64_t>(OMG_KSPLIT, k / 2048));
     while (s > 1 && k % (64 * s) != 0) --s;
     return s;

@@ -279,3 +279,17 @@ def test_open_dir_loads_an_exported_directory(tmp_path):
     ra = a.evaluate(prefix, branches, Want.HIDDEN)[0].rows[0]
     rb = b.evaluate(prefix, branches, Want.HIDDEN)[0].rows[0]
     assert np.array_equal(ra, rb)
+
+
+def test_split_k_products_match_cpu_reference():
+    """The deep o / down products that split K (output width 1536 > 1280,
+    K 4096: down in 2 ranges summed by the residual norm) against the
+    oracle, and rows over the resident prefix still bit-equal."""
+    cfg = gguf_tiny(vocab=64, d=1536, layers=2, ff=4096, sliding=[True, False])
+    check_hidden(cfg, 5, g.Q4, g.Q8)
+    eng, _, _, _ = build(cfg, 5, g.Q4, g.Q8, oracle_models=False)
+    full = eng.evaluate(PREFIX, BRANCHES, Want.HIDDEN)
+    again = eng.evaluate(PREFIX, BRANCHES, Want.HIDDEN)
+    assert eng.prefix_source() == PrefixSource.RESIDENT
+    for a, b in zip(full, again):
+        assert all(np.array_equal(x, y) for x, y in zip(a.rows, b.rows))
