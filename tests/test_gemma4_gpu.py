@@ -161,3 +161,21 @@ def test_gemma4_open_dir_loads_the_per_layer_table(tmp_path):
     for x, y in zip(a, b):
         for r, s in zip(x.rows, y.rows):
             assert np.array_equal(r, s)
+
+
+@pytest.mark.parametrize("heads,kv", [(2, 2), (4, 2), (8, 1), (16, 1)])
+def test_gemma4_every_head_grouping(heads, kv):
+    """Every query-heads-per-K/V-head grouping of the head_dim 256 and 512
+    kernels (1, 2, 8, 16 per group; 4 is covered above), on a prefix long
+    enough for split key ranges, with q / k norms scaled down (see soften)."""
+    rng = np.random.default_rng(6)
+    prefix = rng.integers(0, 64, 300).tolist()
+    branches = [BranchTokens(rng.integers(0, 64, 21).tolist(), [0, 20]) for _ in range(2)]
+    cfg = gemma4_tiny(heads, kv)
+    ts = soften(list(g.Weights.synth(cfg, 29, g.Q4, g.Q8).tensors()))
+    out = engine_of(cfg, ts, 512).evaluate(prefix, branches, Want.HIDDEN)
+    for gpu_rounding, tol in ((False, 2e-2), (True, 6e-3)):
+        exp = oracle_rows(oracle.Model(cfg, ts, gpu_rounding=gpu_rounding), prefix, branches)
+        worst = max(rel_diff(r, e) for o, ex in zip(out, exp) for r, e in zip(o.rows, ex))
+        print(f"gpu_rounding={gpu_rounding}: rel diff {worst:.2e}")
+        assert worst < tol
