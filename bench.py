@@ -125,7 +125,11 @@ def main() -> int:
     load_s = time.perf_counter() - t0
 
     # API passes (host ids in, label logits out): cold, then warm on the
-    # resident state, then a state save / evict / restore round trip.
+    # resident state, then a state save / evict / restore round trip.  One
+    # untimed cold and warm pair first: the first launch of each kernel
+    # loads its code object.
+    eng.evaluate(prefix, branches, Want.LABELS, labels)
+    eng.evaluate(prefix, branches, Want.LABELS, labels)
     eng.evict_resident()
     t = time.perf_counter()
     cold_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
@@ -313,6 +317,8 @@ def bench_gemma4(args) -> int:
     t0 = time.perf_counter()
     eng = g.Engine.new(g.Weights.synth(cfg, SEED, spec["dtype"], spec["dtype"]), T + 64, 64)
     load_s = time.perf_counter() - t0
+    eng.evaluate(prefix, branches, Want.LABELS, labels)  # untimed: first launches load code objects
+    eng.evaluate(prefix, branches, Want.LABELS, labels)
     eng.evict_resident()
     t = time.perf_counter()
     cold_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
