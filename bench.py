@@ -138,6 +138,9 @@ def main() -> int:
     warm_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
     api_warm_ms = (time.perf_counter() - t) * 1e3
     assert eng.prefix_source() == g.PrefixSource.RESIDENT
+    # (one untimed save and restore first: their first calls load the
+    # gather / scatter kernels and touch the pinned staging pages)
+    eng.restore_state(eng.save_state(prefix, "bench"), "bench")
     t = time.perf_counter()
     state = eng.save_state(prefix, "bench")
     save_ms = (time.perf_counter() - t) * 1e3

@@ -307,13 +307,9 @@ int omg_save_state(omg_engine* e, const uint32_t* prefix, size_t n, const char* 
                    size_t* len) {
     return guard([&] {
         if (!bytes || !len || (n && !prefix)) omg::fail(omg::E_INVALID, "null argument");
-        const omg::SavedState s = eng(e).save_state(prefix, int64_t(n));
-        const std::vector<uint8_t> b = s.to_bytes(model_id ? model_id : eng(e).model_id());
-        uint8_t* p = static_cast<uint8_t*>(std::malloc(b.size() ? b.size() : 1));
-        if (!p) omg::fail(omg::E_INVALID, "out of host memory");
-        std::memcpy(p, b.data(), b.size());
+        const auto [p, size] = eng(e).save_state_bytes(prefix, int64_t(n), model_id ? model_id : eng(e).model_id());
         *bytes = p;
-        *len = b.size();
+        *len = size;
     });
 }
 

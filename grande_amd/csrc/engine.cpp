@@ -412,6 +412,12 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     OMG_HIP(hipHostMalloc(&E.h_in_, E.h_in_bytes_, hipHostMallocDefault));
     E.h_out_bytes_ = size_t(max_rows * width) * 4;
     OMG_HIP(hipHostMalloc(&E.h_out_, E.h_out_bytes_, hipHostMallocDefault));
+    for (int64_t l = 0; l < c.layers; ++l) {
+        if (!c.has_kv(l)) continue;
+        const auto [r0, r1] = E.state_rows(l, capacity);
+        E.h_state_bytes_ += size_t((r1 - r0) * 2 * c.kv_heads * c.head_dim[size_t(l)] * 2);
+    }
+    if (E.h_state_bytes_) OMG_HIP(hipHostMalloc(&E.h_state_, E.h_state_bytes_, hipHostMallocDefault));
     OMG_HIP(hipDeviceSynchronize());
     return e;
 }
@@ -425,6 +431,7 @@ Engine::~Engine() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (h_in_) (void)hipHostFree(h_in_);
     if (h_out_) (void)hipHostFree(h_out_);
+    if (h_state_) (void)hipHostFree(h_state_);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -818,22 +825,79 @@ SavedState Engine::save_state_at(const uint32_t* prefix, int64_t p, int64_t row0
     if (row0 + p > capacity_) fail(E_INVALID, "state rows outside the cache");
     SavedState s;
     s.prefix.assign(prefix, prefix + p);
+    stage_state(p, row0);
+    size_t off = 0;
+    for (int64_t l = 0; l < c.layers; ++l) {
+        if (!c.has_kv(l)) continue;
+        const auto [r0, r1] = state_rows(l, p);
+        const size_t n = size_t((r1 - r0) * 2 * c.kv_heads * c.head_dim[size_t(l)] * 2);
+        const uint8_t* src = static_cast<const uint8_t*>(h_state_) + off;
+        s.layers.push_back(SavedState::Layer{uint32_t(l), uint32_t(r0), std::vector<uint8_t>(src, src + n)});
+        off += n;
+    }
+    return s;
+}
+
+std::pair<uint8_t*, size_t> Engine::save_state_bytes(const uint32_t* prefix, int64_t p, const std::string& model_id) {
+    const Config& c = cfg_;
+    if (p > capacity_) fail(E_INVALID, "state rows outside the cache");
+    const size_t staged = stage_state(p, 0);
+    int64_t nl = 0;
+    for (int64_t l = 0; l < c.layers; ++l) nl += c.has_kv(l);
+    const size_t len = 6 + 4 + model_id.size() + 4 + 4 * size_t(p) + 4 + 12 * size_t(nl) + staged;
+    uint8_t* out = static_cast<uint8_t*>(std::malloc(len));
+    if (!out) fail(E_INVALID, "out of host memory");
+    uint8_t* w = out;
+    auto u32 = [&](uint32_t v) {
+        for (int i = 0; i < 4; ++i) *w++ = uint8_t(v >> (8 * i));
+    };
+    const char magic[6] = {'G', 'R', 'W', 'S', '1', '\0'};
+    std::memcpy(w, magic, 6);
+    w += 6;
+    u32(uint32_t(model_id.size()));
+    std::memcpy(w, model_id.data(), model_id.size());
+    w += model_id.size();
+    u32(uint32_t(p));
+    for (int64_t i = 0; i < p; ++i) u32(prefix[i]);
+    u32(uint32_t(nl));
+    size_t off = 0;
+    for (int64_t l = 0; l < c.layers; ++l) {
+        if (!c.has_kv(l)) continue;
+        const auto [r0, r1] = state_rows(l, p);
+        const size_t n = size_t((r1 - r0) * 2 * c.kv_heads * c.head_dim[size_t(l)] * 2);
+        u32(uint32_t(l));
+        u32(uint32_t(r0));
+        u32(uint32_t(n));
+        std::memcpy(w, static_cast<const uint8_t*>(h_state_) + off, n);
+        w += n;
+        off += n;
+    }
+    return {out, len};
+}
+
+size_t Engine::stage_state(int64_t p, int64_t row0) {
+    const Config& c = cfg_;
     sync();
+    // Every layer's rows are gathered into the device stage and copied to
+    // the pinned staging buffer in stream order (a layer's gather waits for
+    // the previous copy), then synchronised once.
+    size_t off = 0;
     for (int64_t l = 0; l < c.layers; ++l) {
         if (!c.has_kv(l)) continue;
         const auto [r0, r1] = state_rows(l, p);
         const int64_t hd = c.head_dim[size_t(l)];
-        const int64_t row_bytes = 2 * c.kv_heads * hd * 2;
-        SavedState::Layer L{uint32_t(l), uint32_t(r0), std::vector<uint8_t>(size_t((r1 - r0) * row_bytes))};
-        if (r1 > r0) {
+        const size_t n = size_t((r1 - r0) * 2 * c.kv_heads * hd * 2);
+        if (off + n > h_state_bytes_) fail(E_STATE, "state larger than the staging buffer");
+        if (n) {
             launch_kv_gather(stream_, kc_[size_t(l)].as<half_t>(), vt_[size_t(l)].as<half_t>(), cap_pad_,
                              int(c.kv_heads), int(hd), row0 + r0, r1 - r0, kv_stage_.as<half_t>());
-            OMG_HIP(hipMemcpyAsync(L.bytes.data(), kv_stage_.p, L.bytes.size(), hipMemcpyDeviceToHost, stream_));
-            OMG_HIP(hipStreamSynchronize(stream_));
+            OMG_HIP(hipMemcpyAsync(static_cast<uint8_t*>(h_state_) + off, kv_stage_.p, n, hipMemcpyDeviceToHost,
+                                   stream_));
         }
-        s.layers.push_back(std::move(L));
+        off += n;
     }
-    return s;
+    OMG_HIP(hipStreamSynchronize(stream_));
+    return off;
 }
 
 void Engine::restore_state(const SavedState& s) {
@@ -856,15 +920,30 @@ void Engine::restore_state(const SavedState& s) {
                               std::to_string(L.row0) + ", expected " + std::to_string((r1 - r0) * row_bytes) +
                               " at " + std::to_string(r0));
     }
+    // All layers' rows into the pinned staging buffer, then per layer a
+    // copy to the device stage and the scatter into the cache, in stream
+    // order (a layer's copy waits for the previous scatter); one sync.
+    size_t total = 0;
+    for (const SavedState::Layer& L : s.layers) total += L.bytes.size();
+    if (total > h_state_bytes_) fail(E_STATE, "state larger than the staging buffer");
+    size_t off = 0;
+    for (const SavedState::Layer& L : s.layers) {
+        std::memcpy(static_cast<uint8_t*>(h_state_) + off, L.bytes.data(), L.bytes.size());
+        off += L.bytes.size();
+    }
+    off = 0;
     for (const SavedState::Layer& L : s.layers) {
         const int64_t l = L.layer, hd = c.head_dim[size_t(l)];
         const auto [r0, r1] = state_rows(l, p);
-        if (r1 <= r0) continue;
-        OMG_HIP(hipMemcpyAsync(kv_stage_.p, L.bytes.data(), L.bytes.size(), hipMemcpyHostToDevice, stream_));
-        launch_kv_scatter(stream_, kc_[size_t(l)].as<half_t>(), vt_[size_t(l)].as<half_t>(), cap_pad_,
-                          int(c.kv_heads), int(hd), r0, r1 - r0, kv_stage_.as<half_t>());
-        OMG_HIP(hipStreamSynchronize(stream_));
+        if (r1 > r0) {
+            OMG_HIP(hipMemcpyAsync(kv_stage_.p, static_cast<const uint8_t*>(h_state_) + off, L.bytes.size(),
+                                   hipMemcpyHostToDevice, stream_));
+            launch_kv_scatter(stream_, kc_[size_t(l)].as<half_t>(), vt_[size_t(l)].as<half_t>(), cap_pad_,
+                              int(c.kv_heads), int(hd), r0, r1 - r0, kv_stage_.as<half_t>());
+        }
+        off += L.bytes.size();
     }
+    OMG_HIP(hipStreamSynchronize(stream_));
     std::vector<int32_t> meta(size_t(4 * p));
     for (int64_t i = 0; i < p; ++i) {
         meta[size_t(4 * i)] = int32_t(i);

@@ -144,6 +144,10 @@ class Engine {
 
     void set_state_cache(size_t bytes, const std::string& dir, const std::string& model_id);
     SavedState save_state(const uint32_t* prefix, int64_t n) { return save_state_at(prefix, n, 0); }
+    // The same state serialised straight from the pinned staging buffer as
+    // GRWS1 bytes (SavedState::to_bytes's layout) into one malloc'd block
+    // the caller frees with std::free.
+    std::pair<uint8_t*, size_t> save_state_bytes(const uint32_t* prefix, int64_t n, const std::string& model_id);
     void restore_state(const SavedState& s);
     bool is_resident(const uint32_t* prefix, int64_t n) const;
     int prefix_source() const { return last_source_; }
@@ -167,6 +171,9 @@ class Engine {
     int restore_from_cache(const uint32_t* prefix, int64_t n);
     void remember(const uint32_t* prefix, int64_t n, int64_t row0);
     SavedState save_state_at(const uint32_t* prefix, int64_t n, int64_t row0);
+    // Gather the K/V rows of a state of p tokens (cache rows from row0) into
+    // h_state_, layer after layer, and synchronise; returns the bytes staged.
+    size_t stage_state(int64_t p, int64_t row0);
     std::pair<int64_t, int64_t> state_rows(int64_t layer, int64_t p) const;
     Packed pack_checked(const GroupIn* groups, int64_t n, int64_t first, bool resident) const;
     void upload(const Packed& pk, const uint32_t* labels, int64_t nlabels);
@@ -212,6 +219,10 @@ class Engine {
     size_t h_in_bytes_ = 0;
     void* h_out_ = nullptr;
     size_t h_out_bytes_ = 0;
+    // pinned staging of a whole state's K/V rows (save / restore), sized
+    // at finish for a state of `capacity` tokens
+    void* h_state_ = nullptr;
+    size_t h_state_bytes_ = 0;
     // resident prefix / state cache (engine.rs:483-496)
     std::optional<std::vector<uint32_t>> resident_;
     int last_source_ = SRC_NONE;

@@ -159,6 +159,9 @@ def test_state_cache_restores_exactly(tmp_path):
         assert all(np.array_equal(x, y) for x, y in zip(full_a[0].rows, disk_a[0].rows))
         name = f"{g.state_key('test', a):016x}.state"
         assert (tmp_path / "states" / name).exists()
+        # The API's bytes (serialised from the pinned staging buffer) and the
+        # cache's file (SavedState::to_bytes) are the same GRWS1 bytes.
+        assert (tmp_path / "states" / name).read_bytes() == eng.save_state(a, "test")
 
 
 def test_branches_do_not_see_each_other():
