@@ -229,11 +229,17 @@ def main() -> int:
         model = oracle.Model(cfg, list(weights.tensors()))
         ids, pos, seq = oracle.pack_single(prefix, branches)
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        # Whole cold passes, repeated until about 10 s of CPU work (at most 30 passes).
         t = time.perf_counter()
-        hidden = model.forward(ids, pos, seq)
-        rows = np.stack([hidden[P + i * BT + BT - 1] for i in range(NB)])
-        cpu_logits = model.logits(rows)[:, labels]
-        cpu_s = time.perf_counter() - t
+        passes = 0
+        while True:
+            hidden = model.forward(ids, pos, seq)
+            rows = np.stack([hidden[P + i * BT + BT - 1] for i in range(NB)])
+            cpu_logits = model.logits(rows)[:, labels]
+            passes += 1
+            if time.perf_counter() - t >= 10.0 or passes >= 30:
+                break
+        cpu_s = (time.perf_counter() - t) / passes
         dp, argmax_same = 0.0, True
         for i in range(NB):
             pg = oracle.softmax(cold_rows[i].rows[0])
@@ -241,9 +247,9 @@ def main() -> int:
             dp = max(dp, float(np.max(np.abs(pg - pc))))
             argmax_same &= int(np.argmax(pg)) == int(np.argmax(pc))
         out["cpu_baseline"] = {"value": round(NB / cpu_s, 4), "unit": "questions/s", "cores": threads,
-                               "kind": "port", "sample": f"one full cold pass of the same workload ({T} tokens, "
+                               "kind": "port", "sample": f"{passes} full cold passes of the same workload ({T} tokens, "
                                f"{mc['layers']} layers) + label readout, f32 C restatement of the reference CPU "
-                               f"forward, OpenMP", "seconds": round(cpu_s, 3),
+                               f"forward, OpenMP; value from the mean pass", "seconds": round(cpu_s * passes, 3),
                                "gpu_speedup": round(cpu_s / cold_s, 1)}
         out["parity"] = {"max_abs_dprob_after_softmax": dp, "argmax_identical": bool(argmax_same), "tol": 2e-2}
     print(json.dumps(out))
