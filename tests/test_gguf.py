@@ -110,3 +110,31 @@ def test_engine_from_gemma4_gguf_matches_engine_from_checkpoint(tmp_path):
     branches = [g.BranchTokens(rng.integers(0, 64, 7).tolist(), [6]) for _ in range(3)]
     for x, y in zip(a.evaluate(prefix, branches, g.Want.HIDDEN), b.evaluate(prefix, branches, g.Want.HIDDEN)):
         assert np.array_equal(x.rows[0], y.rows[0])
+
+
+def test_gguf_mutated_headers_fail_cleanly(tmp_path):
+    """Random byte changes in the header, metadata and tensor infos, and
+    truncations: every file either loads or is refused with OmgError (the
+    parser bounds-checks every read against the file)."""
+    import random
+    cfg = gemma4_tiny()
+    w = g.Weights.synth(cfg, 3, g.Q8, g.Q8)
+    src = tmp_path / "src.gguf"
+    write_gemma3(src, cfg, w)
+    raw = src.read_bytes()
+    rnd = random.Random(11)
+    refused = 0
+    for i in range(150):
+        b = bytearray(raw)
+        for _ in range(rnd.randint(1, 4)):
+            pos = rnd.randrange(min(len(b), 6000))
+            b[pos] = rnd.choice([0, 0xFF, rnd.randrange(256)])
+        if rnd.random() < 0.2:
+            b = b[: rnd.randrange(len(b))]
+        p = tmp_path / "m.gguf"
+        p.write_bytes(bytes(b))
+        try:
+            g.Weights.load_gguf(p)
+        except g.OmgError:
+            refused += 1
+    assert refused > 0

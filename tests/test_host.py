@@ -190,3 +190,27 @@ def test_gemma4_config_validation(edit, match):
     edit(c)
     with pytest.raises(L.OmgError, match=match):
         g.EngineBuilder(json.dumps(c))
+
+
+def test_state_bytes_mutations_fail_cleanly():
+    """GRWS1 parsing (SavedState::from_bytes) of randomly changed or cut
+    bytes: parsed or refused with OmgError, never a crash."""
+    import random
+    import struct
+    rnd = random.Random(5)
+    refused = 0
+    for i in range(400):
+        b = b"GRWS1\0" + struct.pack("<I", 1) + b"m" + struct.pack("<I", 3) + struct.pack("<III", 1, 2, 3)
+        b += struct.pack("<I", 2)
+        for layer in range(2):
+            b += struct.pack("<III", layer, 0, 16) + bytes(16)
+        b = bytearray(b)
+        for _ in range(rnd.randint(1, 3)):
+            b[rnd.randrange(len(b))] = rnd.choice([0, 0xFF, rnd.randrange(256)])
+        if rnd.random() < 0.3:
+            b = b[: rnd.randrange(len(b) + 1)]
+        try:
+            g.state_check(bytes(b), "m")
+        except L.OmgError:
+            refused += 1
+    assert refused > 0
