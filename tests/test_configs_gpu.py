@@ -164,3 +164,53 @@ def test_c5_shapes_two_layers_match_cpu_reference():
     assert max(rel_diff(h, r) for h, r in zip(hid, rows)) < 2e-2
     assert max(rel_diff(h, r) for h, r in zip(hid, rows16)) < 4e-3
     assert_readout(got, plain.logits(rows)[:, LABELS], "c5 two layers")
+
+
+def test_e2b_full_pass_properties():
+    """The Gemma 4 E2B-shaped model of bench.py --config e2b at full size
+    (35 layers, head_dim 256 / 512, 20 K/V-sharing double-wide layers,
+    per-layer inputs, split-K down products): 2,000-token state + 12
+    branches; the warm pass and a save -> evict -> restore give bit-equal
+    label logits, all finite and inside the softcap."""
+    spec = g.GEMMA4_CONFIGS["e2b"]
+    mc = spec["model"]
+    cfg = g.gemma4_config_json(**mc)
+    rng = np.random.default_rng(SEED)
+    prefix = rng.integers(0, mc["vocab"], spec["state"]).tolist()
+    branches = [BranchTokens(rng.integers(0, mc["vocab"], bt).tolist(), [bt - 1]) for bt in spec["branch_tokens"]]
+    eng = g.Engine.new(g.Weights.synth(cfg, SEED, spec["dtype"], spec["dtype"]), 2000 + 663 + 64, 16)
+    cold = eng.evaluate(prefix, branches, Want.LABELS, LABELS)
+    warm = eng.evaluate(prefix, branches, Want.LABELS, LABELS)
+    assert eng.prefix_source() == g.PrefixSource.RESIDENT
+    assert all(np.array_equal(a.rows[0], b.rows[0]) for a, b in zip(cold, warm))
+    state = eng.save_state(prefix, "e2b")
+    eng.evict_resident()
+    eng.restore_state(state, "e2b")
+    again = eng.evaluate(prefix, branches, Want.LABELS, LABELS)
+    assert all(np.array_equal(a.rows[0], b.rows[0]) for a, b in zip(cold, again))
+    z = np.stack([b.rows[0] for b in cold])
+    assert np.isfinite(z).all() and np.abs(z).max() < 30.0
+
+
+def test_e2b_shapes_five_layers_match_cpu_reference():
+    """The E2B shapes (d 1536, 8 query heads over 1 K/V head, ff 6144 /
+    12288, head_dim 512 global layer, per-layer inputs of 256) through the
+    oracle, with five layers (sliding, sliding, global, sliding, global),
+    the last two sharing the K/V of layers 1 and 2 with double-wide
+    feed-forwards and split-K down products."""
+    mc = dict(g.GEMMA4_CONFIGS["e2b"]["model"], layers=5, shared_kv_layers=2,
+              sliding=[True, True, False, True, False])
+    cfg = g.gemma4_config_json(**mc)
+    rng = np.random.default_rng(3)
+    prefix = rng.integers(0, mc["vocab"], 40).tolist()
+    branches = [BranchTokens(rng.integers(0, mc["vocab"], 9).tolist(), [8]) for _ in range(3)]
+    from tests.test_gemma4_gpu import engine_of, soften
+    # q / k norms scaled down: a smooth softmax, so that the comparison is
+    # not dominated by amplified rounding (see soften)
+    ts = soften(list(g.Weights.synth(cfg, SEED, g.Q4, g.Q4).tensors()))
+    hid = np.stack([b.rows[0] for b in engine_of(cfg, ts, 128, 8).evaluate(prefix, branches, Want.HIDDEN)])
+    rows = oracle_wanted_rows(oracle.Model(cfg, ts), prefix, branches)
+    rows16 = oracle_wanted_rows(oracle.Model(cfg, ts, gpu_rounding=True), prefix, branches)
+    worst, worst16 = max(rel_diff(h, r) for h, r in zip(hid, rows)), max(rel_diff(h, r) for h, r in zip(hid, rows16))
+    print(f"rel diff vs f32 oracle {worst:.2e}, vs f16-rounding oracle {worst16:.2e}")
+    assert worst < 2e-2 and worst16 < 6e-3
