@@ -311,26 +311,44 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int64_t vblocks,
         const int64_t lo = r0 > a.base ? r0 : a.base;
         const int64_t hi = r0 + 64 < a.base + a.t ? r0 + 64 : a.base + a.t;
         const bool whole = lo == r0 && hi == r0 + 64;
+        // The destination's current contents first (a tile only partly in
+        // this pass keeps its other keys' columns), then all 16 rows of the
+        // wave, so every load is in flight before the first use.
+        uint4 kept[DPT][8];
+        if (!whole) {
+#pragma unroll
+            for (int dd = 0; dd < DPT; ++dd) {
+                const int dim = int(threadIdx.x) + 256 * dd;
+                const half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + tile) * HD + dim) * 64;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) kept[dd][c] = reinterpret_cast<const uint4*>(dst)[c];
+            }
+        }
         const float* src = a.qkv + int64_t(H + KV + head) * HD + e0;
+        float4 v[16][NQ];
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             const int64_t row = r0 + 16 * wave + k;
-            float4 v[NQ];
 #pragma unroll
             for (int q = 0; q < NQ; ++q)
-                v[q] = row >= lo && row < hi
-                           ? *reinterpret_cast<const float4*>(src + (row - a.base) * a.qkv_stride + 4 * q)
-                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                v[k][q] = row >= lo && row < hi
+                              ? *reinterpret_cast<const float4*>(src + (row - a.base) * a.qkv_stride + 4 * q)
+                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
             float inv = 1.0f;
             if (a.v_norm) {
                 float ss = 0.0f;
 #pragma unroll
-                for (int q = 0; q < NQ; ++q) ss += v[q].x * v[q].x + v[q].y * v[q].y + v[q].z * v[q].z + v[q].w * v[q].w;
+                for (int q = 0; q < NQ; ++q)
+                    ss += v[k][q].x * v[k][q].x + v[k][q].y * v[k][q].y + v[k][q].z * v[k][q].z + v[k][q].w * v[k][q].w;
                 inv = 1.0f / sqrtf(wave_sum(ss) / float(HD) + a.eps);
             }
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
-                half4 h = {half_t(v[q].x * inv), half_t(v[q].y * inv), half_t(v[q].z * inv), half_t(v[q].w * inv)};
+                half4 h = {half_t(v[k][q].x * inv), half_t(v[k][q].y * inv), half_t(v[k][q].z * inv),
+                           half_t(v[k][q].w * inv)};
                 *reinterpret_cast<half4*>(&tile_rows[16 * wave + k][e0 + 4 * q]) = h;
             }
         }
@@ -339,11 +357,6 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int64_t vblocks,
         for (int dd = 0; dd < DPT; ++dd) {
             const int dim = int(threadIdx.x) + 256 * dd;
             half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + tile) * HD + dim) * 64;
-            uint4 kept[8];
-            if (!whole) {
-#pragma unroll
-                for (int c = 0; c < 8; ++c) kept[c] = reinterpret_cast<const uint4*>(dst)[c];
-            }
             // Chunk (half hf, group m) holds keys 32hf + 4m + 0..3, then 32hf + 16 + 4m + 0..3.
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -354,7 +367,8 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkArgs a, int64_t vblocks,
                     const int key = 32 * hf + 16 * (j / 4) + 4 * m + j % 4;
                     h[j] = __builtin_bit_cast(uint16_t, tile_rows[key][dim]);
                     if (!whole && (r0 + key < lo || r0 + key >= hi)) {
-                        const uint32_t w = j / 2 == 0 ? kept[c].x : j / 2 == 1 ? kept[c].y : j / 2 == 2 ? kept[c].z : kept[c].w;
+                        const uint4 kc = kept[dd][c];
+                        const uint32_t w = j / 2 == 0 ? kc.x : j / 2 == 1 ? kc.y : j / 2 == 2 ? kc.z : kc.w;
                         h[j] = (w >> (16 * (j % 2))) & 0xffffu;
                     }
                 }
