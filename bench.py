@@ -3,8 +3,10 @@
 Workload (the metric's configuration): a
 Gemma-3-270M-shaped decoder with seeded Q4_0 weights and a 25,000-row
 vocabulary, one 2,000-token state plus 12 question branches of 32 tokens
-in one block-causal pass, label readout (26 label logits) at each branch's
-last position.  A step is one cold pass (state + branches, T = 2,384) with
+in one block-causal pass, label readout at each branch's last position:
+the 26 label logits and the log-sum-exp of the full 25,000-wide row, what
+the reference's Readout::distribution takes from the row
+(crates/omg-core/src/readout.rs:124-146).  A step is one cold pass (state + branches, T = 2,384) with
 the token ids and metadata already in HBM; the warm pass (branches only on
 the resident state, T = 384) and the API wall times (host upload and
 readback included) are reported beside it.
@@ -128,14 +130,14 @@ def main() -> int:
     # resident state, then a state save / evict / restore round trip.  One
     # untimed cold and warm pair first: the first launch of each kernel
     # loads its code object.
-    eng.evaluate(prefix, branches, Want.LABELS, labels)
-    eng.evaluate(prefix, branches, Want.LABELS, labels)
+    eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
+    eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     eng.evict_resident()
     t = time.perf_counter()
-    cold_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    cold_rows = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     api_cold_ms = (time.perf_counter() - t) * 1e3
     t = time.perf_counter()
-    warm_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    warm_rows = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     api_warm_ms = (time.perf_counter() - t) * 1e3
     assert eng.prefix_source() == g.PrefixSource.RESIDENT
     # (one untimed save and restore first: their first calls load the
@@ -148,12 +150,12 @@ def main() -> int:
     t = time.perf_counter()
     eng.restore_state(state, "bench")
     restore_ms = (time.perf_counter() - t) * 1e3
-    restored_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    restored_rows = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     restored_equal = all(np.array_equal(a.rows[0], b.rows[0]) for a, b in zip(warm_rows, restored_rows))
     warm_equal_cold = max(float(np.max(np.abs(a.rows[0] - b.rows[0]))) for a, b in zip(cold_rows, warm_rows))
 
     def timed(first_resident: bool, steps: int, warmup: int) -> float:
-        eng.prepare([Group(prefix, branches)], Want.LABELS, labels, first_resident=first_resident)
+        eng.prepare([Group(prefix, branches)], Want.LABELS_LSE, labels, first_resident=first_resident)
         for _ in range(warmup):
             eng.launch()
         eng.sync()
@@ -165,7 +167,7 @@ def main() -> int:
 
     eng.evict_resident()
     cold_s = timed(False, args.steps, args.warmup)
-    eng.evaluate(prefix, branches, Want.LABELS, labels)  # leaves the state resident
+    eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)  # leaves the state resident
     warm_s = timed(True, args.steps, args.warmup)
 
     # Per-kernel HIP-event times over a second timed region of cold steps.
@@ -205,7 +207,7 @@ def main() -> int:
         "dtype": f"{wname} weights, f16 MFMA, f32 accumulate",
         "data": "synthetic (seeded random-init weights and token ids)",
         "config": {"workload": f"{args.config}: {shape}, vocab 25k, state {P} + {NB}x{BT} branches, "
-                               "26-label readout", "tokens": T, "state_tokens": P, "branches": NB,
+                               "26 label logits + full-row log-sum-exp readout", "tokens": T, "state_tokens": P, "branches": NB,
                    "branch_tokens": BT},
         "cold_tok_per_s": round(T / cold_s, 1),
         "warm_ms": round(warm_s * 1e3, 4),
@@ -235,23 +237,30 @@ def main() -> int:
         while True:
             hidden = model.forward(ids, pos, seq)
             rows = np.stack([hidden[P + i * BT + BT - 1] for i in range(NB)])
-            cpu_logits = model.logits(rows)[:, labels]
+            cpu_logits = model.logits(rows)
+            lse = np.log(np.exp(cpu_logits - cpu_logits.max(1, keepdims=True)).sum(1)) + cpu_logits.max(1)
+            cpu_logits = np.concatenate([cpu_logits[:, labels], lse[:, None]], 1)
             passes += 1
             if time.perf_counter() - t >= 10.0 or passes >= 30:
                 break
         cpu_s = (time.perf_counter() - t) / passes
-        dp, argmax_same = 0.0, True
+        dp, dmass, argmax_same = 0.0, 0.0, True
+        cpu_full = model.logits(rows)
         for i in range(NB):
-            pg = oracle.softmax(cold_rows[i].rows[0])
-            pc = oracle.softmax(cpu_logits[i])
+            got = cold_rows[i].rows[0]
+            pg = oracle.softmax(got[:-1])
+            _, pc, mass_c = oracle.label_readout(cpu_full[i], labels)
+            mass_g = float(np.exp(oracle.log_sum_exp(got[:-1]) - float(got[-1])))
             dp = max(dp, float(np.max(np.abs(pg - pc))))
+            dmass = max(dmass, abs(mass_g - mass_c))
             argmax_same &= int(np.argmax(pg)) == int(np.argmax(pc))
         out["cpu_baseline"] = {"value": round(NB / cpu_s, 4), "unit": "questions/s", "cores": threads,
                                "kind": "port", "sample": f"{passes} full cold passes of the same workload ({T} tokens, "
                                f"{mc['layers']} layers) + label readout, f32 C restatement of the reference CPU "
                                f"forward, OpenMP; value from the mean pass", "seconds": round(cpu_s * passes, 3),
                                "gpu_speedup": round(cpu_s / cold_s, 1)}
-        out["parity"] = {"max_abs_dprob_after_softmax": dp, "argmax_identical": bool(argmax_same), "tol": 2e-2}
+        out["parity"] = {"max_abs_dprob_after_softmax": dp, "max_abs_dcandidate_mass": dmass,
+                         "argmax_identical": bool(argmax_same), "tol": 2e-2}
     print(json.dumps(out))
     return 0
 
@@ -326,19 +335,19 @@ def bench_gemma4(args) -> int:
     t0 = time.perf_counter()
     eng = g.Engine.new(g.Weights.synth(cfg, SEED, spec["dtype"], spec["dtype"]), T + 64, 64)
     load_s = time.perf_counter() - t0
-    eng.evaluate(prefix, branches, Want.LABELS, labels)  # untimed: first launches load code objects
-    eng.evaluate(prefix, branches, Want.LABELS, labels)
+    eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)  # untimed: first launches load code objects
+    eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     eng.evict_resident()
     t = time.perf_counter()
-    cold_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    cold_rows = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     api_cold_ms = (time.perf_counter() - t) * 1e3
     t = time.perf_counter()
-    warm_rows = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    warm_rows = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     api_warm_ms = (time.perf_counter() - t) * 1e3
     warm_equal_cold = max(float(np.max(np.abs(a.rows[0] - b.rows[0]))) for a, b in zip(cold_rows, warm_rows))
 
     def timed(first_resident: bool, steps: int, warmup: int) -> float:
-        eng.prepare([Group(prefix, branches)], Want.LABELS, labels, first_resident=first_resident)
+        eng.prepare([Group(prefix, branches)], Want.LABELS_LSE, labels, first_resident=first_resident)
         for _ in range(warmup):
             eng.launch()
         eng.sync()
@@ -350,7 +359,7 @@ def bench_gemma4(args) -> int:
 
     eng.evict_resident()
     cold_s = timed(False, args.steps, args.warmup)
-    eng.evaluate(prefix, branches, Want.LABELS, labels)
+    eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     warm_s = timed(True, args.steps, args.warmup)
     eng.profile(True)
     timed(False, args.steps, 0)
@@ -390,7 +399,7 @@ def bench_gemma4(args) -> int:
         "data": "synthetic (seeded random-init weights and token ids)",
         "config": {"workload": f"{args.config}: Gemma 4 E2B-shaped Q4_0 (35 layers, d 1536, head_dim 256/512, "
                                "20 K/V-sharing layers, per-layer inputs 256), vocab 25k, state 2000 + 12 branches "
-                               "(663 tokens), 26-label readout", "tokens": T, "state_tokens": P, "branches": len(bts)},
+                               "(663 tokens), 26 label logits + full-row log-sum-exp readout", "tokens": T, "state_tokens": P, "branches": len(bts)},
         "published_ms": pub,
         "warm_ms": round(warm_s * 1e3, 4),
         "warm_vs_published": round(warm_s * 1e3 / pub["warm"], 6),

@@ -11,7 +11,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libomg_hip.so"
 OK = 0
 E_INVALID, E_CAPACITY, E_DEVICE, E_STATE, E_IO, E_MISSING = -1, -2, -3, -4, -5, -6
 DTYPE_F16, DTYPE_Q8, DTYPE_Q4 = 0, 1, 2
-WANT_LOGITS, WANT_HIDDEN, WANT_LABELS = 0, 1, 2
+WANT_LOGITS, WANT_HIDDEN, WANT_LABELS, WANT_LABELS_LSE = 0, 1, 2, 3
 SRC_NONE, SRC_RESIDENT, SRC_RAM, SRC_DISK, SRC_DECODED = 0, 1, 2, 3, 4
 
 
@@ -89,7 +89,8 @@ _SIGS = {
     "omg_free_bytes": (None, [C.POINTER(C.c_uint8)]),
     "omg_quantize": (C.c_int, [C.c_int, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_uint8),
                                C.POINTER(C.c_uint8)]),
-    "omg_pack": (C.c_int, [C.POINTER(omg_group), C.c_size_t, C.c_size_t, C.c_int, C.POINTER(C.c_uint32),
+    "omg_pack": (C.c_int, [C.POINTER(omg_group), C.c_size_t, C.c_size_t, C.c_int, C.c_size_t, C.c_size_t,
+                           C.POINTER(C.c_uint32),
                            C.POINTER(C.c_int32), C.POINTER(C.c_int64), C.POINTER(C.c_size_t),
                            C.POINTER(C.c_size_t)]),
     "omg_state_key": (C.c_uint64, [C.c_char_p, C.POINTER(C.c_uint32), C.c_size_t]),
@@ -106,6 +107,7 @@ _SIGS = {
     "omg_dev_gemm": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
     "omg_dev_gemm_geglu": (C.c_int, [_P, _P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
     "omg_dev_embed_norm": (C.c_int, [_P, _P, C.c_int64, C.c_float, _P, C.c_float, _P, _P, _P]),
+    "omg_dev_label_readout": (C.c_int, [_P, _P, C.c_int64, _P, C.c_int64, C.c_float, _P, _P]),
     "omg_dev_gemm_geglu_erf": (C.c_int, [_P, _P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
     "omg_dev_gemm_bias_relu": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, _P, C.c_int64, _P]),
     "omg_dev_qkv_heads": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, _P, _P, C.c_float, C.c_int64, _P, _P, _P,

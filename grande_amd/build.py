@@ -25,7 +25,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", f"-I{INCL
 # Device code never uses packed-FP32 VALU instructions.
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
-SOURCES = ["gemm.hip", "attention.hip", "norm.hip", "laya.hip", "model.cpp", "gguf.cpp", "engine.cpp", "laya.cpp", "capi.cpp"]
+SOURCES = ["gemm.hip", "attention.hip", "norm.hip", "laya.hip", "model.cpp", "gguf.cpp", "state.cpp", "engine.cpp", "laya.cpp", "capi.cpp"]
 # Per-file device flags.  The GEMM and attention kernels keep their MFMA
 # accumulators in ordinary VGPRs: with the AGPR form the register allocator
 # shuffles them between loop iterations (v_accvgpr moves in the main loop).

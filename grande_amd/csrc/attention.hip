@@ -100,6 +100,18 @@ struct TileDma {
     static constexpr int VINS = (HD / attn_col_splits<HD>()) * A_KT / 8 / WAVE / A_NW;
 };
 
+// exp2(s log2(e) - m) for a whole-number m, as 2^frac(x) * 2^(floor(x) - m)
+// with x = s log2(e): the fraction and the exponent depend on the score
+// alone, so a probability taken against another whole-number max differs by
+// an exact power of two, and so does its f16 rounding (above f16's
+// subnormals).  Masked scores (-inf) give 0.
+__device__ inline float prob(float s, float m) {
+    constexpr float LOG2E = 1.4426950408889634f;
+    const float x = fmaxf(s * LOG2E, -16384.0f);
+    const float xi = floorf(x);
+    return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(x - xi), int(xi - m));
+}
+
 // One work item per workgroup: A_ROWS query rows (TPW tokens x HPG heads
 // per wave in QB blocks of 16 rows, A_NW waves) against key tiles [tb, te)
 // of the KV head blockIdx.y, output columns [256 z, 256 z + 256) for
@@ -329,9 +341,15 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             // f16 holds with the same relative precision.  A row that has
             // seen nothing yet keeps m = -inf; exponents are taken against 0
             // then, which gives exactly 0 for every -inf score.
+            // The max is kept at whole powers of two (ceil in log2 units):
+            // wherever the row's keys fall into tiles, its probabilities
+            // differ only by exact powers of two, which scale through the
+            // f16 rounding of P, the sums and the rescales without changing
+            // a bit, so a row's result does not depend on where its group
+            // sits in the cache (beyond f32 summation order).
             constexpr float TAU = 8.0f;
             const bool grow = mt > m_run[b] + TAU;
-            const float m_new = grow ? mt : m_run[b];
+            const float m_new = grow ? ceilf(mt) : m_run[b];
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             alpha[b] = grow ? __builtin_amdgcn_exp2f(m_run[b] - m_use) : 1.0f;
             // A row that had seen nothing still holds O = 0: no rescale.
@@ -342,8 +360,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
                 half2v pr[2];
 #pragma unroll
                 for (int r = 0; r < 4; r += 2) {
-                    pr[r / 2] = half2v{half_t(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][j][r], LOG2E, -m_use))),
-                                       half_t(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][j][r + 1], LOG2E, -m_use)))};
+                    pr[r / 2] = half2v{half_t(prob(sacc[b][j][r], m_use)), half_t(prob(sacc[b][j][r + 1], m_use))};
                     psum = __builtin_amdgcn_fdot2(pr[r / 2], half2v{half_t(1.0f), half_t(1.0f)}, psum, false);
                 }
                 pb[b][j / 2][(j % 2) * 4 + 0] = pr[0].x;
@@ -504,23 +521,65 @@ void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int
     w.merges.clear();
     const int hpg = heads / kv_heads, tpb = A_NW * A_QB * (16 / hpg);
     int slot = 0;
+    // A query tile's key range, one span per group among its tokens (in
+    // key order: groups are laid out one after another).  Padding rows
+    // between groups are left out of the ranges: they see nothing or other
+    // padding rows, and their outputs are never read.
+    struct Span {
+        int64_t row_lo, lo, hi;
+    };
+    std::vector<Span> spans;
+    std::vector<int4> pieces;
     for (int64_t q0 = 0, qt = 0; q0 < t; q0 += tpb, ++qt) {
-        int64_t lo = INT64_MAX, hi = 0;
+        spans.clear();
         for (int64_t i = q0; i < t && i < q0 + tpb; ++i) {
             const int32_t* m = meta + 4 * i;
+            if (m[1] < 0) continue;
             const int64_t l = int64_t(m[2]) + (window > 0 ? std::max<int64_t>(0, int64_t(m[0]) - window + 1) : 0);
-            lo = std::min(lo, l);
-            hi = std::max(hi, int64_t(m[3]));
+            if (spans.empty() || spans.back().row_lo != m[2]) spans.push_back({m[2], l, m[3]});
+            spans.back().lo = std::min(spans.back().lo, l);
+            spans.back().hi = std::max(spans.back().hi, int64_t(m[3]));
         }
-        const int t0 = int(lo / A_KT), t1 = int((hi + A_KT - 1) / A_KT);
-        if (chunk <= 0 || t1 - t0 <= 0 || (t0 / chunk) == ((t1 - 1) / chunk)) {
-            w.items.push_back({int(qt), t0, t1, -1});
+        if (spans.empty()) {
+            // Padding only: an empty key range writes zeros (finite values
+            // keep the padding rows' K / V finite, so the exact zeros that
+            // masked keys contribute stay zero).
+            w.items.push_back({int(qt), 0, 0, -1});
             continue;
         }
-        const int first = slot;
-        for (int c = t0 / chunk; c <= (t1 - 1) / chunk; ++c) {
-            w.items.push_back({int(qt), std::max(t0, c * chunk), std::min(t1, (c + 1) * chunk), slot++});
+        // Chunk boundaries count from each group's first key row when every
+        // group of the tile starts on a key tile (the engine aligns them),
+        // so a group's partials are the same wherever it sits in the cache;
+        // otherwise from cache row 0 over the tile's whole range.
+        bool aligned = true;
+        for (const Span& sp : spans) aligned = aligned && sp.row_lo % A_KT == 0;
+        if (!aligned) {
+            int64_t lo = INT64_MAX, hi = 0;
+            for (const Span& sp : spans) {
+                lo = std::min(lo, sp.lo);
+                hi = std::max(hi, sp.hi);
+            }
+            spans.assign(1, Span{0, lo, hi});
         }
+        pieces.clear();
+        for (const Span& sp : spans) {
+            const int org = int(sp.row_lo / A_KT);
+            const int t0 = int(sp.lo / A_KT), t1 = int((sp.hi + A_KT - 1) / A_KT);
+            if (t1 <= t0) continue;
+            if (chunk <= 0) {
+                pieces.push_back({int(qt), t0, t1, 0});
+                continue;
+            }
+            for (int c = (t0 - org) / chunk; c <= (t1 - 1 - org) / chunk; ++c)
+                pieces.push_back({int(qt), std::max(t0, org + c * chunk), std::min(t1, org + (c + 1) * chunk), 0});
+        }
+        if (pieces.size() == 1) {
+            w.items.push_back({int(qt), pieces[0].y, pieces[0].z, -1});
+            continue;
+        }
+        if (pieces.empty()) continue;
+        const int first = slot;
+        for (int4 pc : pieces) w.items.push_back({pc.x, pc.y, pc.z, slot++});
         w.merges.push_back({int(qt), first, slot - first, 0});
     }
     w.slots = slot;

@@ -340,13 +340,14 @@ int omg_quantize(int dtype, const float* values, size_t n, uint8_t* data, uint8_
     });
 }
 
-int omg_pack(const omg_group* groups, size_t ngroups, size_t first, int resident, uint32_t* ids,
-             int32_t* meta, int64_t* wanted, size_t* n_ids, size_t* n_wanted) {
+int omg_pack(const omg_group* groups, size_t ngroups, size_t first, int resident, size_t align, size_t rows,
+             uint32_t* ids, int32_t* meta, int64_t* wanted, size_t* n_ids, size_t* n_wanted) {
     return guard([&] {
         if (!n_ids || !n_wanted) omg::fail(omg::E_INVALID, "null sizes");
         if (first >= ngroups) omg::fail(omg::E_INVALID, "first group out of range");
         Groups g = convert(groups, ngroups);
-        const omg::Packed pk = omg::pack_groups(g.groups.data(), int64_t(ngroups), int64_t(first), resident != 0);
+        omg::Packed pk = omg::pack_groups(g.groups.data(), int64_t(ngroups), int64_t(first), resident != 0);
+        if (align > 1) pk = omg::align_groups(pk, int64_t(align), int64_t(rows));
         if (pk.ids.size() > *n_ids || pk.wanted.size() > *n_wanted)
             omg::fail(omg::E_CAPACITY, "omg_pack: output arrays too small");
         std::memcpy(ids, pk.ids.data(), pk.ids.size() * 4);
@@ -434,6 +435,30 @@ int omg_dev_gemm_geglu(const omg_weight* wg, const omg_weight* wu, const void* x
         if (!wg || !wu || !x_f16 || !act_f16) omg::fail(omg::E_INVALID, "null argument");
         omg::launch_gemm_geglu(static_cast<hipStream_t>(stream), static_cast<const omg::half_t*>(x_f16), ldx, wg->t.w,
                                wu->t.w, static_cast<omg::half_t*>(act_f16), ldact, m);
+    });
+}
+
+int omg_dev_label_readout(const omg_weight* embed, const float* rows, int64_t nrows, const uint32_t* labels,
+                          int64_t nlabels, float softcap, float* out, void* stream) {
+    return guard([&] {
+        if (!embed || !rows || !labels || !out) omg::fail(omg::E_INVALID, "null argument");
+        if (nrows <= 0 || nlabels <= 0) omg::fail(omg::E_INVALID, "label readout: no rows or no labels");
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        const int64_t vocab = embed->t.w.rows, nb = omg::logits_blocks(vocab);
+        // scratch: the full logits rows, then the per-workgroup partials
+        const size_t bytes = size_t(nrows * vocab) * 4 + size_t(nb * nrows) * 8;
+        void* scratch = nullptr;
+        OMG_HIP(hipMallocAsync(&scratch, bytes, s));
+        float* logits = static_cast<float*>(scratch);
+        float2* part = reinterpret_cast<float2*>(logits + nrows * vocab);
+        try {
+            omg::launch_logits(s, embed->t.w, rows, nrows, nullptr, vocab, softcap, logits, part);
+            omg::launch_label_lse(s, logits, nrows, vocab, part, nb, labels, nlabels, out);
+        } catch (...) {
+            (void)hipFreeAsync(scratch, s);
+            throw;
+        }
+        OMG_HIP(hipFreeAsync(scratch, s));
     });
 }
 

@@ -19,164 +19,6 @@
 
 namespace omg {
 
-// ------------------------------------------------------------------ pack
-
-Packed pack_groups(const GroupIn* groups, int64_t n, int64_t first, bool resident) {
-    Packed pk;
-    for (int64_t g = 0; g < n; ++g) {
-        pk.total += groups[g].prefix_len;
-        for (int64_t b = 0; b < groups[g].nbranches; ++b) pk.total += groups[g].branches[b].ntokens;
-    }
-    if (n == 0 || pk.total == 0) fail(E_INVALID, "empty request");
-    const int64_t p0 = groups[first].prefix_len;
-    pk.base = resident ? p0 : 0;
-    pk.ids.reserve(size_t(pk.total - pk.base));
-    pk.meta.reserve(size_t(4 * (pk.total - pk.base)));
-    auto push = [&](int64_t pos, int32_t seq, int64_t row_lo, uint32_t tok) {
-        const int64_t row = pk.base + int64_t(pk.ids.size());
-        pk.meta.push_back(int32_t(pos));
-        pk.meta.push_back(seq);
-        pk.meta.push_back(int32_t(row_lo));
-        pk.meta.push_back(int32_t(row + 1));
-        pk.ids.push_back(tok);
-    };
-    for (int64_t k = 0; k < n; ++k) {
-        const int64_t gi = k == 0 ? first : (k <= first ? k - 1 : k);
-        const GroupIn& g = groups[gi];
-        if (g.nbranches >= (int64_t(1) << SEQ_GROUP_SHIFT))
-            fail(E_CAPACITY, std::to_string(g.nbranches) + " branches in one group; the engine addresses at most " +
-                                 std::to_string((1 << SEQ_GROUP_SHIFT) - 1));
-        const int32_t seq_hi = int32_t(k << SEQ_GROUP_SHIFT);
-        const int64_t row_lo = k == 0 ? 0 : pk.base + int64_t(pk.ids.size());
-        if (!(k == 0 && pk.base > 0)) {
-            pk.decoded.push_back({gi, pk.base + int64_t(pk.ids.size())});
-            for (int64_t i = 0; i < g.prefix_len; ++i) push(i, seq_hi, row_lo, g.prefix[i]);
-        }
-        for (int64_t bi = 0; bi < g.nbranches; ++bi) {
-            const BranchIn& b = g.branches[bi];
-            const int64_t start = int64_t(pk.ids.size());
-            for (int64_t j = 0; j < b.ntokens; ++j)
-                push(g.prefix_len + j, seq_hi | int32_t(bi + 1), row_lo, b.tokens[j]);
-            for (int64_t s = 0; s < b.nwant; ++s) {
-                if (int64_t(b.want[s]) >= b.ntokens)
-                    fail(E_INVALID, "branch " + std::to_string(bi) + ": wanted position " + std::to_string(b.want[s]) +
-                                        " past its " + std::to_string(b.ntokens) + " tokens");
-                pk.wanted.push_back({gi, bi, s, start + int64_t(b.want[s])});
-            }
-        }
-    }
-    return pk;
-}
-
-// ----------------------------------------------------------------- state
-
-size_t SavedState::byte_len() const {
-    size_t n = prefix.size() * 4;
-    for (const Layer& l : layers) n += l.bytes.size();
-    return n;
-}
-
-static void put_u32(std::vector<uint8_t>& o, uint32_t v) {
-    for (int i = 0; i < 4; ++i) o.push_back(uint8_t(v >> (8 * i)));
-}
-
-std::vector<uint8_t> SavedState::to_bytes(const std::string& model_id) const {
-    std::vector<uint8_t> out;
-    out.reserve(byte_len() + 64 + model_id.size());
-    const char magic[6] = {'G', 'R', 'W', 'S', '1', '\0'};
-    out.insert(out.end(), magic, magic + 6);
-    put_u32(out, uint32_t(model_id.size()));
-    out.insert(out.end(), model_id.begin(), model_id.end());
-    put_u32(out, uint32_t(prefix.size()));
-    for (uint32_t t : prefix) put_u32(out, t);
-    put_u32(out, uint32_t(layers.size()));
-    for (const Layer& l : layers) {
-        put_u32(out, l.layer);
-        put_u32(out, l.row0);
-        put_u32(out, uint32_t(l.bytes.size()));
-        out.insert(out.end(), l.bytes.begin(), l.bytes.end());
-    }
-    return out;
-}
-
-SavedState SavedState::from_bytes(const uint8_t* b, size_t n, const std::string& model_id) {
-    size_t at = 0;
-    auto take = [&](size_t k) {
-        if (at + k > n) fail(E_STATE, "state file truncated");
-        const uint8_t* p = b + at;
-        at += k;
-        return p;
-    };
-    auto u32 = [&]() {
-        const uint8_t* p = take(4);
-        return uint32_t(p[0]) | uint32_t(p[1]) << 8 | uint32_t(p[2]) << 16 | uint32_t(p[3]) << 24;
-    };
-    if (std::memcmp(take(6), "GRWS1\0", 6) != 0) fail(E_STATE, "not a omg state file");
-    const uint32_t idn = u32();
-    const uint8_t* id = take(idn);
-    if (std::string(reinterpret_cast<const char*>(id), idn) != model_id)
-        fail(E_STATE, "state file is for a different model");
-    SavedState s;
-    const uint32_t np = u32();
-    const uint8_t* pp = take(size_t(np) * 4);
-    for (uint32_t i = 0; i < np; ++i)
-        s.prefix.push_back(uint32_t(pp[4 * i]) | uint32_t(pp[4 * i + 1]) << 8 | uint32_t(pp[4 * i + 2]) << 16 |
-                           uint32_t(pp[4 * i + 3]) << 24);
-    const uint32_t nl = u32();
-    for (uint32_t i = 0; i < nl; ++i) {
-        Layer l;
-        l.layer = u32();
-        l.row0 = u32();
-        const uint32_t len = u32();
-        const uint8_t* d = take(len);
-        l.bytes.assign(d, d + len);
-        s.layers.push_back(std::move(l));
-    }
-    return s;
-}
-
-std::optional<SavedState> StateCache::get(const std::vector<uint32_t>& prefix) {
-    for (size_t i = 0; i < entries.size(); ++i) {
-        if (entries[i].prefix == prefix) {
-            SavedState s = std::move(entries[i]);
-            entries.erase(entries.begin() + long(i));
-            entries.push_back(s);
-            return s;
-        }
-    }
-    return std::nullopt;
-}
-
-void StateCache::put(SavedState s) {
-    const size_t len = s.byte_len();
-    if (len > budget) return;
-    for (size_t i = 0; i < entries.size(); ++i)
-        if (entries[i].prefix == s.prefix) {
-            used -= entries[i].byte_len();
-            entries.erase(entries.begin() + long(i));
-            break;
-        }
-    while (used + len > budget && !entries.empty()) {
-        used -= entries.front().byte_len();
-        entries.erase(entries.begin());
-    }
-    used += len;
-    entries.push_back(std::move(s));
-}
-
-uint64_t state_key(const std::string& model_id, const uint32_t* prefix, int64_t n) {
-    uint64_t h = 0xcbf29ce484222325ull;
-    auto eat = [&](uint8_t b) {
-        h ^= b;
-        h *= 0x00000100000001b3ull;
-    };
-    for (char c : model_id) eat(uint8_t(c));
-    eat(0);
-    for (int64_t i = 0; i < n; ++i)
-        for (int s = 0; s < 4; ++s) eat(uint8_t(prefix[i] >> (8 * s)));
-    return h;
-}
-
 // ---------------------------------------------------------------- device
 
 DevBuf::DevBuf(size_t n, bool zero) : bytes(n) {
@@ -287,7 +129,10 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.cfg_ = c;
     E.capacity_ = capacity;
     E.max_rows_ = max_rows;
-    E.cap_pad_ = (capacity + 63) / 64 * 64;
+    // Groups start on a key tile and a query tile of the attention kernel.
+    E.align_ = std::max<int64_t>(attention_key_tile(), attention_rows() / (c.heads / c.kv_heads));
+    E.slots_ = capacity + (E.align_ - 1) * max_rows;
+    E.cap_pad_ = (E.slots_ + 63) / 64 * 64;
     OMG_HIP(hipStreamCreateWithFlags(&E.stream_, hipStreamNonBlocking));
     auto take_lin = [&](const std::string& n) { return std::move(linears_.at(n)); };
     auto take_norm = [&](const std::string& n) { return std::move(norms_.at(n)); };
@@ -328,8 +173,9 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     // head_dim): positions stay below the capacity (every token of a pass
     // has its own cache row).
     const int64_t hd = c.max_head_dim();
-    const int64_t cap = capacity, d = c.d;
-    E.rope_rows_ = cap;
+    const int64_t cap = E.slots_, d = c.d;
+    // positions count within a group, so they stay below the token capacity
+    E.rope_rows_ = capacity;
     {
         std::vector<std::pair<bool, int64_t>> keys;
         std::vector<DevBuf> freqs;
@@ -342,8 +188,9 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
                 std::vector<float> f(static_cast<size_t>(half));
                 for (int64_t i = 0; i < half; ++i) f[size_t(i)] = std::pow(theta, -float(i) / float(half));
                 freqs.push_back(upload_bytes(f.data(), f.size() * 4));
-                E.rope_tabs_.emplace_back(size_t(cap * half) * 8);
-                launch_rope_table(E.stream_, freqs.back().as<float>(), cap, half, E.rope_tabs_.back().as<float2>());
+                E.rope_tabs_.emplace_back(size_t(capacity * half) * 8);
+                launch_rope_table(E.stream_, freqs.back().as<float>(), capacity, half,
+                                  E.rope_tabs_.back().as<float2>());
                 keys.push_back(key);
                 it = keys.end() - 1;
             }
@@ -366,6 +213,8 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.logits_ = DevBuf(size_t(max_rows * width) * 4);
     E.wanted_ = DevBuf(size_t(max_rows) * 4);
     E.labels_ = DevBuf(size_t(c.vocab) * 4);
+    E.label_lse_ = DevBuf(size_t(max_rows * (c.vocab + 1)) * 4);
+    E.lse_part_ = DevBuf(size_t(logits_blocks(c.vocab) * max_rows) * 8);
     E.kv_stage_ = DevBuf(size_t(E.cap_pad_ * 2 * c.kv_heads * hd) * 2);
     if (c.per_layer_dim > 0) {
         const int64_t P = c.per_layer_dim;
@@ -380,9 +229,10 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     // the cache on global layers.
     {
         const int64_t kt = attention_key_tile();
-        const int64_t key_tiles = E.cap_pad_ / kt;
+        // (the global chunk follows the token capacity, not the padded rows)
+        const int64_t key_tiles = (capacity + 63) / 64 * 64 / kt;
         const int64_t tpb = attention_rows() / (c.heads / c.kv_heads);
-        const int64_t qtiles = (capacity + tpb - 1) / tpb;
+        const int64_t qtiles = (cap + tpb - 1) / tpb;
         E.attn_chunk_[0] = int(256 / kt);
         E.attn_chunk_[1] = int(std::max<int64_t>(512 / kt, (key_tiles + 7) / 8));
         // Work lists and chunk partials start sized for a few chunks per
@@ -410,7 +260,7 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     }
     E.h_in_bytes_ = size_t(cap) * 4 + size_t(cap) * 16 + size_t(max_rows) * 4 + size_t(c.vocab) * 4;
     OMG_HIP(hipHostMalloc(&E.h_in_, E.h_in_bytes_, hipHostMallocDefault));
-    E.h_out_bytes_ = size_t(max_rows * width) * 4;
+    E.h_out_bytes_ = size_t(max_rows * (width + 1)) * 4;  // + 1: the log-sum-exp after vocab labels
     OMG_HIP(hipHostMalloc(&E.h_out_, E.h_out_bytes_, hipHostMallocDefault));
     for (int64_t l = 0; l < c.layers; ++l) {
         if (!c.has_kv(l)) continue;
@@ -529,7 +379,8 @@ Packed Engine::pack_checked(const GroupIn* groups, int64_t n, int64_t first, boo
     }
     if (total > capacity_)
         fail(E_CAPACITY, std::to_string(total) + " tokens exceed the engine capacity " + std::to_string(capacity_));
-    Packed pk = pack_groups(groups, n, first, resident);
+    // the reference's layout, then groups moved onto aligned rows
+    Packed pk = align_groups(pack_groups(groups, n, first, resident), align_, slots_);
     if (int64_t(pk.wanted.size()) > max_rows_)
         fail(E_CAPACITY, std::to_string(pk.wanted.size()) + " rows requested, engine reads back at most " +
                              std::to_string(max_rows_));
@@ -541,16 +392,29 @@ Packed Engine::pack_checked(const GroupIn* groups, int64_t n, int64_t first, boo
 
 void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     const int64_t t = pk.total - pk.base, nr = int64_t(pk.wanted.size());
+    // Everything that can reject the request is checked before the first
+    // write to the device: a refused request leaves the cache and its
+    // metadata as they were.
+    if (nlabels > 0) {
+        if (!labels) fail(E_INVALID, "label readout without label ids");
+        if (nlabels > cfg_.vocab) fail(E_INVALID, "more labels than vocabulary rows");
+        for (int64_t i = 0; i < nlabels; ++i)
+            if (int64_t(labels[i]) >= cfg_.vocab) fail(E_INVALID, "label id outside the vocabulary");
+    }
+    // The pass writes cache rows and their metadata from pk.base on: a
+    // resident prefix reaching past that is gone from here on, whatever
+    // happens to the rest of the pass.
+    if (resident_ && int64_t(resident_->size()) > pk.base) resident_.reset();
     uint8_t* h = static_cast<uint8_t*>(h_in_);
     // The previous pass may still read the staging buffer.
     OMG_HIP(hipStreamSynchronize(stream_));
     size_t off = 0;
     std::memcpy(h + off, pk.ids.data(), size_t(t) * 4);
     OMG_HIP(hipMemcpyAsync(ids_.p, h + off, size_t(t) * 4, hipMemcpyHostToDevice, stream_));
-    off += size_t(capacity_) * 4;
+    off += size_t(slots_) * 4;
     std::memcpy(h + off, pk.meta.data(), size_t(t) * 16);
     OMG_HIP(hipMemcpyAsync(meta_.as<uint8_t>() + pk.base * 16, h + off, size_t(t) * 16, hipMemcpyHostToDevice, stream_));
-    off += size_t(capacity_) * 16;
+    off += size_t(slots_) * 16;
     int32_t* w = reinterpret_cast<int32_t*>(h + off);
     for (int64_t r = 0; r < nr; ++r) w[r] = int32_t(pk.wanted[size_t(r)][3]);
     if (nr) OMG_HIP(hipMemcpyAsync(wanted_.p, w, size_t(nr) * 4, hipMemcpyHostToDevice, stream_));
@@ -577,9 +441,6 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
             OMG_HIP(hipMemcpy(attn_merges_[kind].p, w.merges.data(), w.merges.size() * 16, hipMemcpyHostToDevice));
     }
     if (nlabels > 0) {
-        if (nlabels > cfg_.vocab) fail(E_INVALID, "more labels than vocabulary rows");
-        for (int64_t i = 0; i < nlabels; ++i)
-            if (int64_t(labels[i]) >= cfg_.vocab) fail(E_INVALID, "label id outside the vocabulary");
         std::memcpy(h + off, labels, size_t(nlabels) * 4);
         OMG_HIP(hipMemcpyAsync(labels_.p, h + off, size_t(nlabels) * 4, hipMemcpyHostToDevice, stream_));
     }
@@ -673,7 +534,7 @@ void Engine::forward(int64_t t, int64_t base) {
             step("attention_merge",
                  [&] { launch_attention_merge(stream_, att, attn_merges_[kind].as<int4>(), n_merges_[kind]); });
         const int so = ksplit(c.heads * hd, d), sd = ksplit(ff, d);
-        const int64_t pstride = capacity_ * d;
+        const int64_t pstride = slots_ * d;
         step("mm_o", [&] {
             launch_gemm_splitk(stream_, attn_.as<half_t>(), c.heads * hd, L.o.w, a_.as<float>(), d, t, so, pstride);
         });
@@ -732,28 +593,45 @@ void Engine::readout(const PassPlan& p) {
             launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, labels_.as<uint32_t>(), p.nlabels,
                           c.softcap, logits_.as<float>());
         });
+    } else if (p.want == WANT_LABELS_LSE) {
+        // Readout::distribution (readout.rs:124-146) needs the label logits
+        // and the log-sum-exp of the whole row: every logit is computed,
+        // only k + 1 floats per row leave the device.
+        step("logits", [&] {
+            launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, nullptr, c.vocab, c.softcap,
+                          logits_.as<float>(), lse_part_.as<float2>());
+        });
+        step("label_lse", [&] {
+            launch_label_lse(stream_, logits_.as<float>(), p.nrows, c.vocab, lse_part_.as<float2>(),
+                             logits_blocks(c.vocab), labels_.as<uint32_t>(), p.nlabels, label_lse_.as<float>());
+        });
     }
 }
 
 void Engine::evaluate_groups(const GroupIn* groups, int64_t n, int want, const uint32_t* labels,
                              int64_t nlabels, float* out, int64_t out_floats, int* sources) {
     if (n <= 0) fail(E_INVALID, "empty request");
-    if (want != WANT_LOGITS && want != WANT_HIDDEN && want != WANT_LABELS) fail(E_INVALID, "unknown want");
-    if (want == WANT_LABELS && (nlabels <= 0 || !labels)) fail(E_INVALID, "label readout without label ids");
+    if (want != WANT_LOGITS && want != WANT_HIDDEN && want != WANT_LABELS && want != WANT_LABELS_LSE)
+        fail(E_INVALID, "unknown want");
+    const bool by_label = want == WANT_LABELS || want == WANT_LABELS_LSE;
+    if (by_label && (nlabels <= 0 || !labels)) fail(E_INVALID, "label readout without label ids");
     auto [first, source] = admit(groups, n);
     Packed pk = pack_checked(groups, n, first, source != SRC_NONE);
-    const int64_t width = want == WANT_HIDDEN ? cfg_.d : (want == WANT_LOGITS ? cfg_.vocab : nlabels);
+    const int64_t width = want == WANT_HIDDEN   ? cfg_.d
+                          : want == WANT_LOGITS ? cfg_.vocab
+                          : want == WANT_LABELS ? nlabels
+                                                : nlabels + 1;
     const int64_t nrows = int64_t(pk.wanted.size());
     if (nrows * width > out_floats)
         fail(E_INVALID, "output buffer holds " + std::to_string(out_floats) + " floats, " +
                             std::to_string(nrows * width) + " needed");
-    upload(pk, labels, want == WANT_LABELS ? nlabels : 0);
+    upload(pk, labels, by_label ? nlabels : 0);
     const int64_t t = pk.total - pk.base;
     forward(t, pk.base);
     PassPlan plan{t, pk.base, nrows, nlabels, want};
     readout(plan);
     if (nrows) {
-        const DevBuf& src = want == WANT_HIDDEN ? rows_ : logits_;
+        const DevBuf& src = want == WANT_HIDDEN ? rows_ : want == WANT_LABELS_LSE ? label_lse_ : logits_;
         OMG_HIP(hipMemcpyAsync(h_out_, src.p, size_t(nrows * width) * 4, hipMemcpyDeviceToHost, stream_));
     }
     sync();
@@ -797,10 +675,14 @@ void Engine::warmup() {
 void Engine::prepare(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
                      bool resident_first) {
     if (n <= 0) fail(E_INVALID, "empty request");
+    if (want != WANT_LOGITS && want != WANT_HIDDEN && want != WANT_LABELS && want != WANT_LABELS_LSE)
+        fail(E_INVALID, "unknown want");
+    const bool by_label = want == WANT_LABELS || want == WANT_LABELS_LSE;
+    if (by_label && (nlabels <= 0 || !labels)) fail(E_INVALID, "label readout without label ids");
     if (resident_first && !is_resident(groups[0].prefix, groups[0].prefix_len))
         fail(E_INVALID, "prepare: group 0's prefix is not resident");
     Packed pk = pack_checked(groups, n, 0, resident_first);
-    upload(pk, labels, want == WANT_LABELS ? nlabels : 0);
+    upload(pk, labels, by_label ? nlabels : 0);
     prepared_ = PassPlan{pk.total - pk.base, pk.base, int64_t(pk.wanted.size()), nlabels, want};
     sync();
 }
@@ -822,7 +704,7 @@ void Engine::set_state_cache(size_t bytes, const std::string& dir, const std::st
 
 SavedState Engine::save_state_at(const uint32_t* prefix, int64_t p, int64_t row0) {
     const Config& c = cfg_;
-    if (row0 + p > capacity_) fail(E_INVALID, "state rows outside the cache");
+    if (row0 + p > slots_) fail(E_INVALID, "state rows outside the cache");
     SavedState s;
     s.prefix.assign(prefix, prefix + p);
     stage_state(p, row0);
@@ -926,6 +808,9 @@ void Engine::restore_state(const SavedState& s) {
     size_t total = 0;
     for (const SavedState::Layer& L : s.layers) total += L.bytes.size();
     if (total > h_state_bytes_) fail(E_STATE, "state larger than the staging buffer");
+    // The cache rows change from here on: no prefix is resident until the
+    // restore completes.
+    resident_.reset();
     size_t off = 0;
     for (const SavedState::Layer& L : s.layers) {
         std::memcpy(static_cast<uint8_t*>(h_state_) + off, L.bytes.data(), L.bytes.size());

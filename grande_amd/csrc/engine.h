@@ -18,62 +18,12 @@
 #include "common.h"
 #include "kernels.h"
 #include "model.h"
+#include "state.h"
 
 namespace omg {
 
-// engine.rs:21-24: bits of a sequence id that number the branch; the bits
-// above number the group within the pass.
-constexpr int SEQ_GROUP_SHIFT = 12;
-
-enum WantKind { WANT_LOGITS = 0, WANT_HIDDEN = 1, WANT_LABELS = 2 };
+enum WantKind { WANT_LOGITS = 0, WANT_HIDDEN = 1, WANT_LABELS = 2, WANT_LABELS_LSE = 3 };
 enum Source { SRC_NONE = 0, SRC_RESIDENT = 1, SRC_RAM = 2, SRC_DISK = 3, SRC_DECODED = 4 };
-
-struct BranchIn {
-    const uint32_t* tokens;
-    int64_t ntokens;
-    const uint32_t* want;
-    int64_t nwant;
-};
-struct GroupIn {
-    const uint32_t* prefix;
-    int64_t prefix_len;
-    const BranchIn* branches;
-    int64_t nbranches;
-};
-
-// One pass's packed layout (engine.rs:1512-1571).
-struct Packed {
-    int64_t base = 0, total = 0;
-    std::vector<uint32_t> ids;
-    std::vector<int32_t> meta;                        // 4 per token: pos, seq, first key row, row + 1
-    std::vector<std::array<int64_t, 4>> wanted;       // group, branch, slot, workspace row
-    std::vector<std::pair<int64_t, int64_t>> decoded; // group, cache row of its prefix
-};
-// Order: `first`, then the other groups in order (engine.rs:1479-1482).
-Packed pack_groups(const GroupIn* groups, int64_t n, int64_t first, bool resident);
-
-// engine.rs:503-580: a prefix's K/V rows as f16 per layer that owns K/V.
-struct SavedState {
-    std::vector<uint32_t> prefix;
-    struct Layer {
-        uint32_t layer, row0;
-        std::vector<uint8_t> bytes;
-    };
-    std::vector<Layer> layers;
-    size_t byte_len() const;
-    std::vector<uint8_t> to_bytes(const std::string& model_id) const;
-    static SavedState from_bytes(const uint8_t* b, size_t n, const std::string& model_id);
-};
-
-// engine.rs:582-620: LRU keyed by the exact prefix, most recent last.
-struct StateCache {
-    size_t budget = 0, used = 0;
-    std::vector<SavedState> entries;
-    std::optional<SavedState> get(const std::vector<uint32_t>& prefix);
-    void put(SavedState s);
-};
-
-uint64_t state_key(const std::string& model_id, const uint32_t* prefix, int64_t n);  // engine.rs:625-641
 
 // Owned device allocation.
 struct DevBuf {
@@ -184,6 +134,10 @@ class Engine {
 
     Config cfg_;
     int64_t capacity_ = 0, max_rows_ = 0, cap_pad_ = 0;
+    // Cache rows the workspace holds: the token capacity plus room to start
+    // every layout group after the first on a multiple of align_ rows
+    // (align_groups), for up to max_rows groups.
+    int64_t slots_ = 0, align_ = 1;
     hipStream_t stream_ = nullptr;
     DevTensor embed_;
     DevBuf final_norm_;
@@ -207,6 +161,9 @@ class Engine {
     int64_t rope_rows_ = 0;
     // workspace
     DevBuf ids_, meta_, x_, hn_, qkv_, q16_, attn_, a_, act_, rows_, logits_, wanted_, labels_, kv_stage_;
+    // Label logits + full-row log-sum-exp per wanted row (WANT_LABELS_LSE),
+    // and the logits kernel's per-workgroup (max, sum of exp) pairs.
+    DevBuf label_lse_, lse_part_;
     DevBuf x16_, pli_, plg_, pl16_;  // per-layer inputs: f16(x), [t][layers x P] f32, gate f32, gated f16
     // attention work lists of the current pass: [0] sliding layers, [1] global
     int attn_chunk_[2] = {0, 0};

@@ -101,12 +101,7 @@ struct TensorInfo {
     }
 };
 
-uint16_t f32_to_f16_bits(float x) {
-    const _Float16 h = static_cast<_Float16>(x);
-    uint16_t b;
-    std::memcpy(&b, &h, 2);
-    return b;
-}
+uint16_t f32_to_f16_bits(float x) { return f32_to_f16(x); }  // round to nearest even
 
 }  // namespace
 
@@ -129,13 +124,25 @@ Weights load_gguf(const std::string& path) {
         const uint32_t nd = r.get<uint32_t>();
         if (nd == 0 || nd > 4) fail(E_INVALID, "gguf: " + name + " has " + std::to_string(nd) + " dims");
         std::vector<int64_t> ne(nd);
-        for (uint32_t k = 0; k < nd; ++k) ne[k] = int64_t(r.get<uint64_t>());
+        // Every dimension positive and the element count below 2^40 (the
+        // byte counts below then cannot overflow); the file size bounds it
+        // further once the tensor's bytes are located.
+        uint64_t count = 1;
+        for (uint32_t k = 0; k < nd; ++k) {
+            const uint64_t x = r.get<uint64_t>();
+            if (x == 0 || x > (uint64_t(1) << 40) || count > (uint64_t(1) << 40) / x)
+                fail(E_INVALID, "gguf: " + name + " has an invalid shape");
+            count *= x;
+            ne[k] = int64_t(x);
+        }
         t.shape.assign(ne.rbegin(), ne.rend());
         t.type = r.get<uint32_t>();
         t.offset = r.get<uint64_t>();
         infos[name] = t;
     }
     const uint64_t align = kv.count("general.alignment") ? kv["general.alignment"].u64(32) : 32;
+    if (align == 0 || align > (1u << 20) || (align & (align - 1)) != 0)
+        fail(E_INVALID, "gguf: general.alignment must be a power of two up to 2^20");
     const size_t data0 = (r.at + align - 1) / align * align;
 
     const std::string arch = kv["general.architecture"].s("");
@@ -149,14 +156,22 @@ Weights load_gguf(const std::string& path) {
     };
     auto need = [&](const std::string& k) {
         const Json& v = g(k);
-        if (v.kind != Json::Number) fail(E_INVALID, "gguf: missing " + arch + "." + k);
+        if (v.kind != Json::Number || !std::isfinite(v.num)) fail(E_INVALID, "gguf: missing " + arch + "." + k);
         return v.num;
     };
+    // A count from the metadata: a whole number in [0, 2^31).
+    auto count = [&](double x, const std::string& k) {
+        if (!(x >= 0.0 && x < 2147483648.0) || x != std::floor(x)) fail(E_INVALID, "gguf: bad " + arch + "." + k);
+        return int64_t(x);
+    };
     if (!infos.count("token_embd.weight")) fail(E_INVALID, "gguf: missing token_embd.weight");
-    const int64_t layers = int64_t(need("block_count")), d = int64_t(need("embedding_length"));
-    const int64_t heads = int64_t(need("attention.head_count"));
+    const int64_t layers = count(need("block_count"), "block_count");
+    const int64_t d = count(need("embedding_length"), "embedding_length");
+    const int64_t heads = count(need("attention.head_count"), "attention.head_count");
     const Json& kvh = g("attention.head_count_kv");
-    const int64_t kv_heads = int64_t(kvh.kind == Json::Array ? kvh.arr.at(0).num : kvh.num);
+    const Json& kvh0 = kvh.kind == Json::Array ? kvh[size_t(0)] : kvh;
+    if (kvh0.kind != Json::Number) fail(E_INVALID, "gguf: missing " + arch + ".attention.head_count_kv");
+    const int64_t kv_heads = count(kvh0.num, "attention.head_count_kv");
     const int64_t vocab = infos["token_embd.weight"].shape[0];
 
     // export_wgpu_gguf.py:130-171: the text config the exported directory
@@ -196,10 +211,12 @@ Weights load_gguf(const std::string& path) {
     for (int64_t i = 0; i < layers; ++i) {
         bool swa;
         if (pat.kind == Json::Array) {
-            const Json& e = pat.arr.at(size_t(i));
+            if (int64_t(pat.arr.size()) != layers)
+                fail(E_INVALID, "gguf: attention.sliding_window_pattern has the wrong length");
+            const Json& e = pat.arr[size_t(i)];
             swa = e.kind == Json::Bool ? e.b : e.num != 0.0;
         } else {
-            const int64_t k = int64_t(pat.f64(6.0));
+            const int64_t k = count(pat.f64(6.0), "attention.sliding_window_pattern");
             swa = k == 0 ? true : (i + 1) % k != 0;
         }
         Json t;
@@ -222,7 +239,8 @@ Weights load_gguf(const std::string& path) {
         if (rf != infos.end()) {
             if (rf->second.type != G_F32) fail(E_INVALID, "gguf: rope_freqs.weight must be f32");
             const int64_t n = rf->second.numel();
-            if (data0 + rf->second.offset + uint64_t(n) * 4 > file.size())
+            if (data0 > file.size() || rf->second.offset > file.size() - data0 ||
+                uint64_t(n) * 4 > file.size() - data0 - rf->second.offset)
                 fail(E_INVALID, "gguf: rope_freqs.weight past the end of the file");
             int64_t rotated = 0;
             for (int64_t i = 0; i < n; ++i) {
@@ -273,7 +291,8 @@ Weights load_gguf(const std::string& path) {
             default: fail(E_INVALID, "gguf: " + name + " has unsupported type " + std::to_string(t.type));
         }
         if ((t.type == G_Q8_0 || t.type == G_Q4_0) && n % 32 != 0) fail(E_INVALID, "gguf: " + name + " not in whole blocks");
-        if (data0 + t.offset + uint64_t(nb) > file.size()) fail(E_INVALID, "gguf: " + name + " past the end of the file");
+        if (data0 > file.size() || t.offset > file.size() - data0 || uint64_t(nb) > file.size() - data0 - t.offset)
+            fail(E_INVALID, "gguf: " + name + " past the end of the file");
         return {reinterpret_cast<const uint8_t*>(file.data()) + data0 + t.offset, t};
     };
     // One or more GGUF tensors (rows concatenated) as one QTensor of `shape`.

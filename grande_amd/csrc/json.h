@@ -10,7 +10,7 @@
 #include <string>
 #include <vector>
 
-#include "common.h"
+#include "host_common.h"
 
 namespace omg {
 
@@ -35,7 +35,9 @@ struct Json {
         return (kind == Array && i < arr.size()) ? arr[i] : none;
     }
     // serde_json's as_u64 / as_f64 / as_str / as_bool: absent or wrong kind -> fallback.
-    bool is_uint() const { return kind == Number && num >= 0 && double(uint64_t(num)) == num; }
+    // Whole numbers up to 2^53 (every one exact in a double); anything
+    // larger, fractional or non-finite is not an unsigned integer here.
+    bool is_uint() const { return kind == Number && num >= 0 && num <= 9007199254740992.0 && double(uint64_t(num)) == num; }
     uint64_t u64(uint64_t fallback) const { return is_uint() ? uint64_t(num) : fallback; }
     double f64(double fallback) const { return kind == Number ? num : fallback; }
     std::string s(const std::string& fallback) const { return kind == String ? str : fallback; }

@@ -80,8 +80,17 @@ void launch_rope_table(hipStream_t s, const float* inv_freq, int64_t rows, int64
 void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int64_t n, int64_t d,
                        const float* w, float eps, float* rows);
 // out[r][j] = rows[r] . deq(E[col(j)]) in f32 (+ softcap), col(j) = cols ? cols[j] : j.
-void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows,
-                   const uint32_t* cols, int64_t ncols, float softcap, float* out);
+// logits[r][j] = rows[r] . deq(E[cols ? cols[j] : j]) (softcap applied),
+// f32 [nrows][ncols]; with `part` (logits_blocks(ncols) x nrows pairs) each
+// workgroup's (max, sum of exp) per row for the log-sum-exp.
+void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows, const uint32_t* cols,
+                   int64_t ncols, float softcap, float* out, float2* part = nullptr);
+int64_t logits_blocks(int64_t ncols);
+// Per row of full-vocabulary logits [nrows][vocab] and the logits kernel's
+// partials: the columns `labels`, then log-sum-exp over the whole row, into
+// out [nrows][nlabels + 1].
+void launch_label_lse(hipStream_t s, const float* logits, int64_t nrows, int64_t vocab, const float2* part,
+                      int64_t nblocks, const uint32_t* labels, int64_t nlabels, float* out);
 // K/V cache rows <-> the reference's state row format [K heads | V heads] f16.
 void launch_kv_gather(hipStream_t s, const half_t* kc, const half_t* vt, int64_t cap_pad, int kv_heads,
                       int hd, int64_t row0, int64_t rows, half_t* out);

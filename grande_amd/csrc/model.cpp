@@ -17,9 +17,30 @@ Dtype parse_dtype(const std::string& s) {
 
 int64_t payload_bytes(Dtype t, int64_t n) { return t == F16 ? n * 2 : (t == Q8 ? n : n / 2); }
 
-static int64_t need_u64(const Json& v, const char* k) {
+// Structural sizes are bounded before anything is sized by them, so a
+// hostile config.json is refused instead of exhausting memory.
+constexpr int64_t MAX_COUNT = int64_t(1) << 31;
+
+static int64_t need_u64(const Json& v, const char* k, int64_t max = MAX_COUNT) {
     if (!v[k].is_uint()) fail(E_INVALID, std::string("config.json: missing ") + k);
+    if (v[k].num > double(max)) fail(E_INVALID, std::string("config.json: ") + k + " too large");
     return int64_t(v[k].num);
+}
+
+// An optional unsigned size: absent or not an unsigned integer gives the
+// fallback (serde_json's as_u64().unwrap_or, model.rs:66-210); one above
+// `max` is refused.
+static int64_t opt_u64(const Json& x, int64_t fallback, const char* k, int64_t max = MAX_COUNT) {
+    if (!x.is_uint()) return fallback;
+    if (x.num > double(max)) fail(E_INVALID, std::string("config.json: ") + k + " too large");
+    return int64_t(x.num);
+}
+
+// An optional float parameter: finite and within float range.
+static double opt_f64(const Json& x, double fallback, const char* k) {
+    if (x.kind != Json::Number) return fallback;
+    if (!std::isfinite(x.num) || std::fabs(x.num) > 3.0e38) fail(E_INVALID, std::string("config.json: bad ") + k);
+    return x.num;
 }
 
 Config Config::from_json(const Json& root) {
@@ -27,32 +48,35 @@ Config Config::from_json(const Json& root) {
     Config c;
     const std::string mt = v["model_type"].s("gemma3_text");
     c.arch = (mt == "gemma4_text" || mt == "gemma4") ? GEMMA4 : GEMMA3;
-    c.layers = need_u64(v, "num_hidden_layers");
+    c.layers = need_u64(v, "num_hidden_layers", 4096);
     const int64_t L = c.layers;
     if (v["layer_types"].kind == Json::Array) {
         for (const Json& t : v["layer_types"].arr) c.sliding.push_back(t.s("") == "sliding_attention");
     } else {
-        const int64_t k = int64_t(v["_sliding_window_pattern"].u64(6));
+        const int64_t k = opt_u64(v["_sliding_window_pattern"], 6, "_sliding_window_pattern");
         for (int64_t i = 0; i < L; ++i) c.sliding.push_back(k == 0 ? true : (i + 1) % k != 0);
     }
     if (int64_t(c.sliding.size()) != L)
         fail(E_INVALID, "config.json: layer_types has " + std::to_string(c.sliding.size()) +
                             " entries for " + std::to_string(L) + " layers");
     const Json& rope = v["rope_parameters"];
-    c.theta_global = float(rope["full_attention"]["rope_theta"].f64(v["rope_theta"].f64(1e6)));
-    c.theta_local =
-        float(rope["sliding_attention"]["rope_theta"].f64(v["rope_local_base_freq"].f64(1e4)));
-    const int64_t hd_local = need_u64(v, "head_dim");
-    const int64_t hd_global = int64_t(v["global_head_dim"].u64(uint64_t(hd_local)));
-    const double rot_local = rope["sliding_attention"]["partial_rotary_factor"].f64(1.0);
-    const double rot_global = rope["full_attention"]["partial_rotary_factor"].f64(1.0);
+    c.theta_global = float(opt_f64(rope["full_attention"]["rope_theta"],
+                                   opt_f64(v["rope_theta"], 1e6, "rope_theta"), "rope_theta"));
+    c.theta_local = float(opt_f64(rope["sliding_attention"]["rope_theta"],
+                                  opt_f64(v["rope_local_base_freq"], 1e4, "rope_local_base_freq"), "rope_theta"));
+    const int64_t hd_local = need_u64(v, "head_dim", 65536);
+    const int64_t hd_global = opt_u64(v["global_head_dim"], hd_local, "global_head_dim", 65536);
+    const double rot_local = opt_f64(rope["sliding_attention"]["partial_rotary_factor"], 1.0, "partial_rotary_factor");
+    const double rot_global = opt_f64(rope["full_attention"]["partial_rotary_factor"], 1.0, "partial_rotary_factor");
+    if (rot_local < 0.0 || rot_local > 1.0 || rot_global < 0.0 || rot_global > 1.0)
+        fail(E_INVALID, "config.json: partial_rotary_factor outside [0, 1]");
     for (int64_t i = 0; i < L; ++i) {
         const bool s = c.sliding[size_t(i)];
         const int64_t hd = s ? hd_local : hd_global;
         c.head_dim.push_back(hd);
         c.rope_dims.push_back(int64_t(double(hd) * (s ? rot_local : rot_global)));
     }
-    const int64_t shared = int64_t(v["num_kv_shared_layers"].u64(0));
+    const int64_t shared = opt_u64(v["num_kv_shared_layers"], 0, "num_kv_shared_layers");
     if (shared >= L)
         fail(E_INVALID, "num_kv_shared_layers " + std::to_string(shared) + " >= " +
                             std::to_string(L) + " layers");
@@ -72,9 +96,10 @@ Config Config::from_json(const Json& root) {
     }
     const Json& ffj = v["intermediate_size"];
     if (ffj.kind == Json::Array) {
-        for (const Json& x : ffj.arr) c.ff.push_back(int64_t(x.u64(0)));
+        if (int64_t(ffj.arr.size()) != L) fail(E_INVALID, "config.json: intermediate_size length mismatch");
+        for (const Json& x : ffj.arr) c.ff.push_back(opt_u64(x, 0, "intermediate_size", int64_t(1) << 24));
     } else if (ffj.kind == Json::Number) {
-        const int64_t base = int64_t(ffj.u64(0));
+        const int64_t base = opt_u64(ffj, 0, "intermediate_size", int64_t(1) << 24);
         const bool dbl = v["use_double_wide_mlp"].boolean(false);
         for (int64_t i = 0; i < L; ++i) c.ff.push_back(dbl && i >= first_shared ? 2 * base : base);
     } else {
@@ -82,7 +107,8 @@ Config Config::from_json(const Json& root) {
     }
     if (int64_t(c.ff.size()) != L) fail(E_INVALID, "config.json: intermediate_size length mismatch");
     if (c.arch == GEMMA3) {
-        const double qps = v["query_pre_attn_scalar"].f64(double(hd_local));
+        const double qps = opt_f64(v["query_pre_attn_scalar"], double(hd_local), "query_pre_attn_scalar");
+        if (!(qps > 0.0)) fail(E_INVALID, "config.json: query_pre_attn_scalar must be positive");
         c.query_scale = std::pow(float(qps), -0.5f);
         c.norm_offset = 1.0f;
         c.v_norm = false;
@@ -91,16 +117,16 @@ Config Config::from_json(const Json& root) {
         c.norm_offset = 0.0f;
         c.v_norm = true;
     }
-    c.norm_offset = float(v["omg_norm_offset"].f64(double(c.norm_offset)));
+    c.norm_offset = float(opt_f64(v["omg_norm_offset"], double(c.norm_offset), "omg_norm_offset"));
     c.vocab = need_u64(v, "vocab_size");
-    c.d = need_u64(v, "hidden_size");
-    c.heads = need_u64(v, "num_attention_heads");
-    c.kv_heads = need_u64(v, "num_key_value_heads");
-    c.eps = float(v["rms_norm_eps"].f64(1e-6));
-    c.window = int64_t(v["sliding_window"].u64(512));
-    c.per_layer_dim = int64_t(v["hidden_size_per_layer_input"].u64(0));
-    c.softcap = float(v["final_logit_softcapping"].f64(0.0));
-    c.bos = uint32_t(v["bos_token_id"].u64(2));
+    c.d = need_u64(v, "hidden_size", 65536);
+    c.heads = need_u64(v, "num_attention_heads", 1024);
+    c.kv_heads = need_u64(v, "num_key_value_heads", 1024);
+    c.eps = float(opt_f64(v["rms_norm_eps"], 1e-6, "rms_norm_eps"));
+    c.window = opt_u64(v["sliding_window"], 512, "sliding_window");
+    c.per_layer_dim = opt_u64(v["hidden_size_per_layer_input"], 0, "hidden_size_per_layer_input", 65536);
+    c.softcap = float(opt_f64(v["final_logit_softcapping"], 0.0, "final_logit_softcapping"));
+    c.bos = uint32_t(opt_u64(v["bos_token_id"], 2, "bos_token_id", int64_t(0xffffffff)));
     return c;
 }
 
@@ -126,6 +152,9 @@ void Config::validate() const {
             fail(E_INVALID, "layer " + std::to_string(i) + ": shares K/V across head_dims");
     }
     if (d % 32 != 0) fail(E_INVALID, "hidden_size must be a multiple of 32");
+    // The residual / final norms hold one row per wavefront in registers.
+    if (d > 4096) fail(E_INVALID, "hidden_size " + std::to_string(d) + " above 4096 (the row norms' register rows)");
+    if (vocab <= 0) fail(E_INVALID, "vocab_size must be positive");
     for (int64_t f : ff)
         if (f % 32 != 0 || f <= 0) fail(E_INVALID, "intermediate_size must be a positive multiple of 32");
     if (per_layer_dim < 0 || per_layer_dim % 32 != 0 || per_layer_dim > 1024)

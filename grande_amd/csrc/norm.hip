@@ -535,21 +535,158 @@ __global__ __launch_bounds__(256) void logits_kernel(DevWeight E, const float* _
     }
 }
 
-void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows,
-                   const uint32_t* cols, int64_t ncols, float softcap, float* out) {
+// logits.wgsl:38-79's product, rows . deq(E[col])^T in f32 (no f16
+// rounding on this path, as in the reference).  A workgroup owns 64 output
+// columns (vocabulary rows of E, or the label ids in `cols`), one per lane;
+// its four waves split K by 32-element blocks (wave w takes blocks w, w + 4,
+// ...), each lane decoding its column's block once into registers and
+// multiplying it into up to LG_R readout rows, whose values are the same
+// for every lane (uniform loads, no LDS).  The four partial sums meet in
+// LDS and are added in wave order, so a column's value does not depend on
+// which columns share its workgroup: full rows, label columns and the
+// log-sum-exp path give bit-equal logits.  With `part`, every workgroup
+// also writes each row's (max, sum of exp(z - max)) over its columns.
+constexpr int LG_R = 16;  // readout rows per pass over K
+
+// Block b of column `col` as 32 f32 weights, (q - 8) d / q d / f16 as f32.
+template <int DT>
+__device__ inline void logit_block(const DevWeight& E, int64_t col, int64_t b, float w[32]) {
+    const int64_t K = E.cols;
+    if constexpr (DT == Q4_DT) {
+        const float d = half_bits_to_f32(E.scales[col * E.sld + b]);
+        const uint4 q = reinterpret_cast<const uint4*>(E.data)[col * (K / 32) + b];
+        const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int p = 0; p < 8; ++p) w[8 * i + p] = q4_elem_f32(words[i], p, d);
+    } else if constexpr (DT == Q8_DT) {
+        const float d = half_bits_to_f32(E.scales[col * E.sld + b]);
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(E.data) + col * K + b * 32);
+        const uint4 u0 = src[0], u1 = src[1];
+        const uint32_t words[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[4 * i + k] = float(int8_t(words[i] >> (8 * k))) * d;
+    } else {
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const half_t*>(E.data) + col * K + b * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 u = src[i];
+            const uint32_t words[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const half2v h = as_half2(words[k]);
+                w[8 * i + 2 * k] = float(h.x);
+                w[8 * i + 2 * k + 1] = float(h.y);
+            }
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void logits_kernel(DevWeight E, const float* __restrict__ rows, int64_t nrows,
+                                                     const uint32_t* __restrict__ cols, int64_t ncols, float softcap,
+                                                     float* __restrict__ out, float2* __restrict__ part) {
+    __shared__ float red[4][LG_R][WAVE];
+    const int tid = int(threadIdx.x), lane = tid % WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int64_t j = int64_t(blockIdx.x) * WAVE + lane;
+    const bool live = j < ncols;
+    const int64_t col = live ? (cols ? int64_t(cols[j]) : j) : 0;  // idle lanes read row 0 and drop it
+    const int64_t K = E.cols, nb = K / 32;
+    for (int64_t r0 = 0; r0 < nrows; r0 += LG_R) {
+        const int nr = int(nrows - r0 < LG_R ? nrows - r0 : LG_R);
+        float acc[LG_R];
+#pragma unroll
+        for (int r = 0; r < LG_R; ++r) acc[r] = 0.0f;
+        for (int64_t b = wave; b < nb; b += 4) {
+            float w[32];
+            logit_block<DT>(E, col, b, w);
+#pragma unroll
+            for (int r = 0; r < LG_R; ++r) {
+                if (r < nr) {  // uniform: the row group's tail skips its loads
+                    const float* x = rows + (r0 + r) * K + b * 32;
+#pragma unroll
+                    for (int k = 0; k < 32; ++k) acc[r] = __builtin_fmaf(w[k], x[k], acc[r]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < LG_R; ++r) red[wave][r][lane] = acc[r];
+        __syncthreads();
+        if (wave == 0) {
+            for (int r = 0; r < nr; ++r) {
+                float z = ((red[0][r][lane] + red[1][r][lane]) + red[2][r][lane]) + red[3][r][lane];
+                if (softcap > 0.0f) z = softcap * tanhf(z / softcap);
+                if (live) out[(r0 + r) * ncols + j] = z;
+                if (part) {
+                    const float m = wave_max(live ? z : -INFINITY);
+                    const float e = wave_sum(live ? expf(z - m) : 0.0f);
+                    if (lane == 0) part[int64_t(blockIdx.x) * nrows + r0 + r] = make_float2(m, e);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows, const uint32_t* cols,
+                   int64_t ncols, float softcap, float* out, float2* part) {
     if (nrows <= 0 || ncols <= 0) return;
     if (E.cols % 32 != 0) fail(E_INVALID, "logits: width must be a multiple of 32");
-    const int rb = ncols <= 1024 ? 4 : 16;
-    const dim3 grid(unsigned((ncols + 3) / 4), unsigned((nrows + rb - 1) / rb)), block(256);
-#define OMG_LG(D)                                                                                 \
-    (rb == 4 ? logits_kernel<D, 4><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out) \
-             : logits_kernel<D, 16><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out))
+    const dim3 grid(unsigned((ncols + WAVE - 1) / WAVE)), block(256);
     switch (E.dtype) {
-        case F16_DT: OMG_LG(F16_DT); break;
-        case Q8_DT: OMG_LG(Q8_DT); break;
-        default: OMG_LG(Q4_DT); break;
+        case F16_DT: logits_kernel<F16_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out, part); break;
+        case Q8_DT: logits_kernel<Q8_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out, part); break;
+        default: logits_kernel<Q4_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out, part); break;
     }
-#undef OMG_LG
+    OMG_HIP(hipGetLastError());
+}
+
+int64_t logits_blocks(int64_t ncols) { return (ncols + WAVE - 1) / WAVE; }
+
+// Readout::distribution's inputs per row (readout.rs:124-146): the label
+// columns of a full logits row and the row's log-sum-exp, from the logits
+// kernel's per-workgroup (max, sum of exp) pairs: M = max of the maxima,
+// lse = M + log(sum_b s_b exp(m_b - M)), in f32 (the reference sums the
+// row in f64 on the host; over 25,000 terms the two agree to a few 1e-7
+// relative).  One workgroup per row, the pairs summed in a fixed order.
+__global__ __launch_bounds__(256) void label_lse_kernel(const float* __restrict__ logits, int64_t vocab,
+                                                        const float2* __restrict__ part, int64_t nblocks,
+                                                        int64_t nrows, const uint32_t* __restrict__ labels,
+                                                        int64_t nlabels, float* __restrict__ out) {
+    __shared__ float red[256 / WAVE];
+    const int64_t r = blockIdx.x;
+    const int tid = int(threadIdx.x), wave = tid / WAVE, lane = tid % WAVE;
+    float m = -INFINITY;
+    for (int64_t b = tid; b < nblocks; b += 256) m = fmaxf(m, part[b * nrows + r].x);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.0f;
+    for (int64_t b = tid; b < nblocks; b += 256) {
+        const float2 p = part[b * nrows + r];
+        sum += p.y * expf(p.x - m);
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    const float* row = logits + r * vocab;
+    float* o = out + r * (nlabels + 1);
+    for (int64_t i = tid; i < nlabels; i += 256) o[i] = row[labels[i]];
+    if (tid == 0) o[nlabels] = m + logf((red[0] + red[1]) + (red[2] + red[3]));
+}
+
+void launch_label_lse(hipStream_t s, const float* logits, int64_t nrows, int64_t vocab, const float2* part,
+                      int64_t nblocks, const uint32_t* labels, int64_t nlabels, float* out) {
+    if (nrows <= 0) return;
+    if (vocab <= 0 || nlabels <= 0 || nblocks <= 0) fail(E_INVALID, "label_lse: empty row or no labels");
+    label_lse_kernel<<<dim3(unsigned(nrows)), dim3(256), 0, s>>>(logits, vocab, part, nblocks, nrows, labels,
+                                                                 nlabels, out);
     OMG_HIP(hipGetLastError());
 }
 

@@ -24,11 +24,14 @@ from .model import QTensor, Weights
 
 
 class Want(enum.IntEnum):
-    """backend.rs:14-20, plus LABELS: logits of given label ids only."""
+    """backend.rs:14-20, plus LABELS: logits of given label ids only, and
+    LABELS_LSE: those logits then the log-sum-exp of the full row (the
+    inputs of readout.rs:124-146's Readout::distribution)."""
 
     LOGITS = L.WANT_LOGITS
     HIDDEN = L.WANT_HIDDEN
     LABELS = L.WANT_LABELS
+    LABELS_LSE = L.WANT_LABELS_LSE
 
 
 class PrefixSource(enum.IntEnum):
@@ -174,7 +177,8 @@ class Engine:
                         ) -> list[GroupOutput]:
         cg = _CGroups(groups)
         lab = _u32(labels if labels is not None else [])
-        width = {Want.HIDDEN: self.d, Want.LOGITS: self.vocab, Want.LABELS: lab.size}[Want(want)]
+        width = {Want.HIDDEN: self.d, Want.LOGITS: self.vocab, Want.LABELS: lab.size,
+                 Want.LABELS_LSE: lab.size + 1}[Want(want)]
         rows = sum(len(b.want) for g in groups for b in g.branches)
         out = np.zeros((max(rows, 1), max(width, 1)), np.float32)
         src = (C.c_int * max(1, len(groups)))()
@@ -252,16 +256,19 @@ class Engine:
         return out
 
 
-def pack(groups: Sequence[Group], first: int = 0, resident: bool = False):
-    """engine.rs:1512-1571 through omg_pack: (ids, meta[n,4], wanted[r,4])."""
+def pack(groups: Sequence[Group], first: int = 0, resident: bool = False, align: int = 1, rows: int = 0):
+    """engine.rs:1512-1571 through omg_pack: (ids, meta[n,4], wanted[r,4]);
+    align > 1: the engine's layout with later groups on multiples of
+    `align` cache rows (when that fits in `rows`)."""
     cg = _CGroups(groups)
     total = sum(len(g.prefix) + sum(len(b.tokens) for b in g.branches) for g in groups)
-    rows = sum(len(b.want) for g in groups for b in g.branches)
+    total += max(0, align - 1) * len(groups)
+    nwant = sum(len(b.want) for g in groups for b in g.branches)
     ids = np.zeros(max(total, 1), np.uint32)
     meta = np.zeros((max(total, 1), 4), np.int32)
-    wanted = np.zeros((max(rows, 1), 4), np.int64)
+    wanted = np.zeros((max(nwant, 1), 4), np.int64)
     n_ids, n_w = C.c_size_t(ids.size), C.c_size_t(wanted.shape[0])
-    L.check(L.lib().omg_pack(cg.arr, cg.n, first, int(resident), ids.ctypes.data_as(C.POINTER(C.c_uint32)),
+    L.check(L.lib().omg_pack(cg.arr, cg.n, first, int(resident), align, rows, ids.ctypes.data_as(C.POINTER(C.c_uint32)),
                              meta.ctypes.data_as(C.POINTER(C.c_int32)), wanted.ctypes.data_as(C.POINTER(C.c_int64)),
                              C.byref(n_ids), C.byref(n_w)))
     return ids[:n_ids.value], meta[:n_ids.value], wanted[:n_w.value]
@@ -301,6 +308,10 @@ class DeviceWeight:
     def gemm_geglu(self, up: "DeviceWeight", x_ptr: int, ldx: int, m: int, act_ptr: int, ldact: int,
                    stream: int | None = None) -> None:
         L.check(L.lib().omg_dev_gemm_geglu(self._h, up._h, x_ptr, ldx, m, act_ptr, ldact, stream))
+
+    def label_readout(self, rows_ptr: int, nrows: int, labels_ptr: int, nlabels: int, softcap: float, out_ptr: int,
+                      stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_label_readout(self._h, rows_ptr, nrows, labels_ptr, nlabels, softcap, out_ptr, stream))
 
     def embed_norm(self, ids_ptr: int, t: int, scale: float, w_ptr: int, eps: float, x_ptr: int, hn_ptr: int,
                    stream: int | None = None) -> None:

@@ -41,12 +41,19 @@ extern "C" {
 #define OMG_DTYPE_Q8 1
 #define OMG_DTYPE_Q4 2
 
-/* omg-core backend.rs:14-20 Want; OMG_WANT_LABELS has no counterpart in the
- * reference: logits of the given label ids only (readout.rs:130-133 picks
- * them out of the full row on the host). */
+/* omg-core backend.rs:14-20 Want.  OMG_WANT_LABELS and OMG_WANT_LABELS_LSE
+ * have no counterpart in the reference, whose Readout::distribution
+ * (readout.rs:124-146) reads the full logits row on the host to pick the
+ * label columns and take log_sum_exp (math.rs:13-17) for candidate_mass:
+ *   LABELS      k floats per row: the logits of the given label ids;
+ *   LABELS_LSE  k + 1 floats per row: the same k logits, then the
+ *               log-sum-exp of the row over the whole vocabulary (f32), so
+ *               candidate_mass = exp(lse(labels) - row[k]) needs no
+ *               vocabulary-wide readback. */
 #define OMG_WANT_LOGITS 0
 #define OMG_WANT_HIDDEN 1
 #define OMG_WANT_LABELS 2
+#define OMG_WANT_LABELS_LSE 3
 
 /* omg-core backend.rs:92-104 PrefixSource (0 = none yet) */
 #define OMG_SRC_NONE 0
@@ -134,8 +141,8 @@ int omg_warmup(omg_engine *e);
 
 /* Engine::evaluate_groups / Backend::evaluate_many (engine.rs:1404-1444,
  * backend.rs:142-152).  Rows are written densely into `out` in (group,
- * branch, want) order; width n_embd (HIDDEN), n_vocab (LOGITS) or nlabels
- * (LABELS, with label_ids).  prefix_sources (may be NULL) gets one
+ * branch, want) order; width n_embd (HIDDEN), n_vocab (LOGITS), nlabels
+ * (LABELS, with label_ids) or nlabels + 1 (LABELS_LSE).  prefix_sources (may be NULL) gets one
  * OMG_SRC_* per group. */
 int omg_evaluate_groups(omg_engine *e, const omg_group *groups, size_t ngroups, int want,
                         const uint32_t *label_ids, size_t nlabels, float *out, size_t out_floats,
@@ -173,9 +180,13 @@ int omg_quantize(int dtype, const float *values, size_t n, uint8_t *data, uint8_
 /* The packing of Engine::run (engine.rs:1512-1571) with `first` laid out
  * first and its prefix resident when `resident`: ids, meta (4 int32 per
  * token: position, sequence id, first key row, own row + 1) and wanted
- * (4 int64 per row: group, branch, slot, workspace row).  Sizes in/out. */
-int omg_pack(const omg_group *groups, size_t ngroups, size_t first, int resident, uint32_t *ids,
-             int32_t *meta, int64_t *wanted, size_t *n_ids, size_t *n_wanted);
+ * (4 int64 per row: group, branch, slot, workspace row).  Sizes in/out.
+ * align <= 1 gives the reference's layout; align > 1 the engine's own,
+ * where every group after the first starts on a multiple of `align` cache
+ * rows (padding rows: token 0, sequence id -1), unless that needs more
+ * than `rows` rows. */
+int omg_pack(const omg_group *groups, size_t ngroups, size_t first, int resident, size_t align, size_t rows,
+             uint32_t *ids, int32_t *meta, int64_t *wanted, size_t *n_ids, size_t *n_wanted);
 /* state_key (engine.rs:625-641): FNV-1a 64 of model id, 0, prefix. */
 uint64_t omg_state_key(const char *model_id, const uint32_t *prefix, size_t n);
 /* SavedState::from_bytes (engine.rs:536-579) without an engine: 0 and the
@@ -210,6 +221,15 @@ int omg_dev_gemm(const omg_weight *w, const void *x_f16, int64_t ldx, int64_t m,
                  void *stream);
 int omg_dev_gemm_geglu(const omg_weight *wg, const omg_weight *wu, const void *x_f16, int64_t ldx, int64_t m,
                        void *act_f16, int64_t ldact, void *stream);
+/* The label readout on device pointers (logits.wgsl's product, then what
+ * readout.rs:124-146 takes from the row): rows f32 [nrows][d] times the
+ * embedding `embed` [vocab][d] in f32, softcap applied when > 0, then per
+ * row the logits of the device-resident label ids and the log-sum-exp of
+ * the full vocabulary row: out f32 [nrows][nlabels + 1].  The full logits
+ * and per-workgroup partials live in scratch device memory the call
+ * allocates and frees in stream order. */
+int omg_dev_label_readout(const omg_weight *embed, const float *rows, int64_t nrows, const uint32_t *labels,
+                          int64_t nlabels, float softcap, float *out, void *stream);
 /* The embedding gather + first norm kernel (embed.wgsl + rmsnorm.wgsl):
  * x[t][d] = deq(E[ids[t]]) * scale (f32), hn[t][d] = f16(rmsnorm(x) * w)
  * with w (f32, d entries) already offset.  Device pointers. */

@@ -82,6 +82,7 @@ def lib() -> C.CDLL:
             "orc_get": (C.c_float, [C.c_int, P, P, C.c_size_t]),
             "orc_model_new": (P, [C.POINTER(orc_config), C.c_int]),
             "orc_model_free": (None, [P]),
+            "orc_model_set_attention_tiles": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float]),
             "orc_model_set": (C.c_int, [P, C.c_char_p, C.c_int, C.c_int64, C.c_int64, P, P]),
             "orc_model_missing": (C.c_int, [P, C.c_char_p, C.c_size_t]),
             "orc_forward": (C.c_int, [P, P, P, P, C.c_int64, P]),
@@ -227,6 +228,14 @@ class Model:
         buf = C.create_string_buffer(1 << 16)
         if lib().orc_model_missing(self._h, buf, len(buf)):
             raise ValueError("oracle: missing " + buf.value.decode())
+
+    def set_attention_tiles(self, key_tile: int, chunk_sliding: int, chunk_global: int, tau: float = 8.0) -> "Model":
+        """Model the f16 flash kernel's attention rounding (P to f16 against a
+        lazily moved max, f16 chunk partials merged by weight) instead of
+        the reference's f32 softmax; key_tile 0 switches it off."""
+        if lib().orc_model_set_attention_tiles(self._h, key_tile, chunk_sliding, chunk_global, tau) != 0:
+            raise ValueError("oracle: bad attention tiling")
+        return self
 
     def __del__(self):
         if getattr(self, "_h", None):

@@ -186,6 +186,11 @@ static const char *LAYER_NAMES[T_COUNT] = {"attn_norm", "qkv", "q_norm", "k_norm
 struct orc_model {
     orc_config cfg;
     int gpu;
+    /* Kernel-faithful attention (orc_model_set_attention_tiles): key tile,
+     * chunk lengths in tiles for sliding / global layers, lazy-rescale
+     * threshold in log2 units; key_tile = 0 is the plain softmax. */
+    int key_tile, chunk_sliding, chunk_global;
+    float tau;
     orc_tensor embed, final_norm, pl_model_proj, pl_proj_norm, per_layer_table;
     orc_tensor layer[ORC_MAX_LAYERS][T_COUNT];
 };
@@ -203,6 +208,15 @@ orc_model *orc_model_new(const orc_config *cfg, int gpu_rounding) {
     m->cfg = *cfg;
     m->gpu = gpu_rounding;
     return m;
+}
+
+int orc_model_set_attention_tiles(orc_model *m, int key_tile, int chunk_sliding, int chunk_global, float tau) {
+    if (key_tile < 0 || (key_tile > 0 && (chunk_sliding <= 0 || chunk_global <= 0 || tau < 0.0f))) return -1;
+    m->key_tile = key_tile;
+    m->chunk_sliding = chunk_sliding;
+    m->chunk_global = chunk_global;
+    m->tau = tau;
+    return 0;
 }
 
 static void tensor_free(orc_tensor *t) {
@@ -375,6 +389,85 @@ static void norm_rows(const float *x, int64_t t, int64_t d, const orc_tensor *w,
     for (int64_t i = 0; i < t; i++) rmsnorm(x + i * d, d, w->w, eps, offset, y + i * d);
 }
 
+/* One query row of one head, with the rounding points of an f16 flash
+ * kernel instead of the reference's f32 softmax (reference.rs:284-300,
+ * shaders/attention.wgsl:55,240-252 keep P in f32): keys are taken in
+ * cache-row order in tiles of `kt`; the running max (log2 units, rounded up
+ * to a whole number) moves only when a tile's max exceeds it by more than
+ * `tau`; a probability is 2^frac(x) 2^(floor(x) - m) for x = s log2(e); each is
+ * rounded to f16 before both the sum and the P.V product, whose f32 sum is
+ * taken per tile and then added to O (one MFMA per tile); the key range is
+ * cut at absolute multiples of `chunk` tiles, each chunk's O / l is rounded
+ * to f16, and chunks are merged with weights l_c 2^(m_c - M) (one chunk:
+ * its f16 row unchanged).  `s` holds the visible keys' scores, `idx` their
+ * rows (ascending). */
+static void attend_tiled(const float *s, const int64_t *idx, int64_t n, const float *V, int64_t vstride,
+                         int64_t hd, int kt, int chunk, float tau, float *out, float *acc, float *part) {
+    const float LOG2E = 1.4426950408889634f;
+    int64_t r = 0;
+    int nchunks = 0;
+    float cm[64], cl[64];
+    while (r < n) {
+        const int64_t c = idx[r] / kt / chunk;
+        float m = -INFINITY, l = 0.0f;
+        for (int64_t e = 0; e < hd; e++) acc[e] = 0.0f;
+        while (r < n && idx[r] / kt / chunk == c) {
+            const int64_t tile = idx[r] / kt;
+            int64_t r1 = r;
+            float mt = -INFINITY;
+            while (r1 < n && idx[r1] / kt == tile) mt = fmaxf(mt, s[r1++]);
+            mt *= LOG2E;
+            const int grow = mt > m + tau;
+            const float m_new = grow ? ceilf(mt) : m; /* whole powers of two */
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            if (grow && m != -INFINITY) {
+                const float alpha = exp2f(m - m_use);
+                l *= alpha;
+                for (int64_t e = 0; e < hd; e++) acc[e] *= alpha;
+            }
+            /* the tile's P.V in its own f32 sum, then added to O, as one
+             * MFMA over the tile's keys adds to the accumulator */
+            float psum = 0.0f, *tacc = acc + hd;
+            for (int64_t e = 0; e < hd; e++) tacc[e] = 0.0f;
+            for (; r < r1; r++) {
+                /* 2^frac(x) * 2^(floor(x) - m): exact power-of-two scaling under another max */
+                const float x = fmaxf(s[r] * LOG2E, -16384.0f), xi = floorf(x);
+                const float p = r16(ldexpf(exp2f(x - xi), (int)(xi - m_use)));
+                psum += p;
+                const float *vj = V + idx[r] * vstride;
+                for (int64_t e = 0; e < hd; e++) tacc[e] += p * vj[e];
+            }
+            for (int64_t e = 0; e < hd; e++) acc[e] += tacc[e];
+            l += psum;
+            m = m_new;
+        }
+        if (nchunks >= 64) break; /* more chunks than the kernel's work lists make */
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        for (int64_t e = 0; e < hd; e++) part[nchunks * hd + e] = r16(acc[e] * inv);
+        cm[nchunks] = m;
+        cl[nchunks] = l;
+        nchunks++;
+    }
+    if (nchunks == 0) {
+        for (int64_t e = 0; e < hd; e++) out[e] = 0.0f;
+        return;
+    }
+    if (nchunks == 1) {
+        for (int64_t e = 0; e < hd; e++) out[e] = part[e];
+        return;
+    }
+    float M = -INFINITY, L = 0.0f;
+    for (int k = 0; k < nchunks; k++) M = fmaxf(M, cm[k]);
+    for (int64_t e = 0; e < hd; e++) acc[e] = 0.0f;
+    for (int k = 0; k < nchunks; k++) {
+        const float w = cl[k] * exp2f(cm[k] - M);
+        L += w;
+        for (int64_t e = 0; e < hd; e++) acc[e] += part[k * hd + e] * w;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int64_t e = 0; e < hd; e++) out[e] = r16(acc[e] * inv);
+}
+
 /* reference.rs:175-349, without Gemma 4's per-layer inputs. */
 int orc_forward(const orc_model *m, const uint32_t *ids, const int32_t *pos, const int32_t *seq,
                 int64_t t, float *hidden) {
@@ -485,6 +578,8 @@ int orc_forward(const orc_model *m, const uint32_t *ids, const int32_t *pos, con
         {
             float *sc_ = (float *)malloc((size_t)t * 4);
             int64_t *idx = (int64_t *)malloc((size_t)t * 8);
+            float *acc_ = (float *)malloc((size_t)(2 * hd) * 4);
+            float *part_ = (float *)malloc((size_t)(64 * hd) * 4);
 #pragma omp for schedule(dynamic, 8)
             for (int64_t i = 0; i < t; i++) {
                 for (int64_t hh = 0; hh < H; hh++) {
@@ -498,6 +593,12 @@ int orc_forward(const orc_model *m, const uint32_t *ids, const int32_t *pos, con
                         for (int64_t e = 0; e < hd; e++) s += qh[e] * kj[e];
                         idx[n] = j;
                         sc_[n++] = s;
+                    }
+                    if (m->key_tile > 0) {
+                        attend_tiled(sc_, idx, n, V + gh * hd, KV * hd, hd, m->key_tile,
+                                     sl ? m->chunk_sliding : m->chunk_global, m->tau, att + (i * H + hh) * hd,
+                                     acc_, part_);
+                        continue;
                     }
                     float mx = -3.402823466e38f;
                     for (int64_t r = 0; r < n; r++) mx = fmaxf(mx, sc_[r]);
@@ -514,6 +615,8 @@ int orc_forward(const orc_model *m, const uint32_t *ids, const int32_t *pos, con
             }
             free(sc_);
             free(idx);
+            free(acc_);
+            free(part_);
         }
         if (m->gpu) round_rows(att, t * H * hd);
         linear(att, t, H * hd, L[T_O].w, d, a);

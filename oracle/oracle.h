@@ -75,6 +75,14 @@ typedef struct orc_model orc_model;
  * to f16); 0 is the plain f32 forward of tests/reference.rs. */
 orc_model *orc_model_new(const orc_config *cfg, int gpu_rounding);
 void orc_model_free(orc_model *m);
+/* Replace the reference's f32 softmax with the rounding points of an f16
+ * flash-attention kernel (keys in tiles of key_tile cache rows; running max
+ * moved lazily by more than tau log2 units; P rounded to f16; key ranges
+ * cut at absolute multiples of chunk_sliding / chunk_global tiles with
+ * f16 O / l partials merged by weight).  key_tile = 0 restores the plain
+ * softmax.  Models what the HIP attention kernel computes, so tests can
+ * bound its difference from the reference with the same rounding. */
+int orc_model_set_attention_tiles(orc_model *m, int key_tile, int chunk_sliding, int chunk_global, float tau);
 int orc_model_set(orc_model *m, const char *name, int dtype, int64_t rows, int64_t cols,
                   const uint8_t *data, const uint8_t *scales);
 /* Missing tensor names, newline separated, into buf; returns their count. */

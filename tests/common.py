@@ -90,3 +90,33 @@ def random_request(rng: np.random.Generator, vocab: int, state: int, nbranches: 
                                [branch_tokens - 1] if want_last else list(range(branch_tokens)))
                 for _ in range(nbranches)]
     return prefix, branches
+
+
+def tiled_oracle(cfg: str, tensors, capacity: int) -> oracle.Model:
+    """The f16-rounding oracle with the HIP attention kernel's own rounding
+    points too (32-key tiles, lazily moved whole-power-of-two max, P in f16,
+    f16 chunk partials at the engine's chunk lengths for this capacity:
+    256 keys on sliding layers, max(512 keys, an eighth of the cache) on
+    global ones)."""
+    kt = 32
+    cap_pad = (capacity + 63) // 64 * 64
+    return oracle.Model(cfg, tensors, gpu_rounding=True).set_attention_tiles(
+        kt, 256 // kt, max(512 // kt, (cap_pad // kt + 7) // 8))
+
+
+def worst_rel(a, b) -> float:
+    """Largest rel_diff over matching rows of two [branch][row] lists."""
+    return max(rel_diff(x, y) for oa, ob in zip(a, b) for x, y in zip(oa, ob))
+
+
+def rounding_spread(cfg: str, tensors, prefix, branches, capacity: int):
+    """Rows of the three CPU forwards that differ only in where they round
+    (plain f32; f16 operands as the reference GPU path; f16 operands plus
+    the flash kernel's attention rounding) and the largest distance between
+    any two of them: how far legitimate f16 implementations of this
+    configuration can sit apart."""
+    f32 = oracle_rows(oracle.Model(cfg, tensors), prefix, branches)
+    f16 = oracle_rows(oracle.Model(cfg, tensors, gpu_rounding=True), prefix, branches)
+    tiled = oracle_rows(tiled_oracle(cfg, tensors, capacity), prefix, branches)
+    spread = max(worst_rel(f32, f16), worst_rel(f32, tiled), worst_rel(f16, tiled))
+    return f32, f16, tiled, spread

@@ -11,7 +11,8 @@ import pytest
 import grande_amd as g
 import oracle
 from grande_amd import BranchTokens, PrefixSource, Want
-from tests.common import assert_close, build, gemma4_tiny, oracle_rows, rel_diff
+from tests.common import (assert_close, build, gemma4_tiny, oracle_rows, rel_diff, rounding_spread, tiled_oracle,
+                          worst_rel)
 
 pytestmark = pytest.mark.gpu
 
@@ -59,19 +60,6 @@ def test_gemma4_gqa_q4_matches_cpu_reference():
     check_hidden(gemma4_tiny(8, 2), 11, g.Q4, g.Q8)
 
 
-def soften(ts, f: float = 0.3):
-    """The tensors with q_norm / k_norm weights scaled by f: smaller scores,
-    a smooth softmax, so that rounding differences are not amplified over a
-    long prefix (the two CPU forwards then differ by 1.3e-3, not 1.4e-2)."""
-    out = []
-    for t in ts:
-        if t.name.endswith(".q_norm") or t.name.endswith(".k_norm"):
-            v = (t.data.view(np.float16).astype(np.float32) * f).astype(np.float16)
-            t = g.QTensor(t.name, t.dtype, t.shape, v.view(np.uint8).copy(), t.scales)
-        out.append(t)
-    return out
-
-
 def engine_of(cfg: str, ts, capacity: int, max_rows: int = 16) -> g.Engine:
     b = g.EngineBuilder(cfg)
     for t in ts:
@@ -79,25 +67,65 @@ def engine_of(cfg: str, ts, capacity: int, max_rows: int = 16) -> g.Engine:
     return b.finish(capacity, max_rows)
 
 
+def check_chaotic(out, cfg: str, ts, prefix, branches, capacity: int, what: str):
+    """Rows of a long-prefix Gemma 4 pass on the reference's own weight
+    distribution.  With query scale 1 and normed q / k over 256 / 512 dims
+    the scores reach several tens and near-ties between keys are common
+    over hundreds of keys, so any rounding difference is amplified layer by
+    layer: the three CPU forwards that differ only in where they round
+    (f32, f16 operands, f16 operands + the flash kernel's rounding) sit up
+    to 4e-2 apart here (`rounding_spread`), beyond the reference's 2e-2 bar
+    that holds on its short-prefix tests.  The GPU rows must stay within
+    twice that spread of every one of them, so a real defect (O(1) errors,
+    a lost mask or window) still fails; the depth-limited cases in
+    test_gemma4_long_prefix_by_depth hold the reference's 2e-2 bar."""
+    f32, f16, tiled, spread = rounding_spread(cfg, ts, prefix, branches, capacity)
+    hip = [o.rows for o in out]
+    d = {k: worst_rel(hip, v) for k, v in (("f32", f32), ("f16", f16), ("tiled", tiled))}
+    print(f"{what}: CPU rounding spread {spread:.2e}; GPU vs f32 {d['f32']:.2e}, "
+          f"vs f16 operands {d['f16']:.2e}, vs kernel rounding {d['tiled']:.2e}")
+    bound = max(2e-2, 2.0 * spread)
+    for k, v in d.items():
+        assert v < bound, f"{what}: {v} from the {k} forward (bound {bound})"
+
+
 @pytest.mark.parametrize("capacity", [1024, 8192])
-def test_gemma4_long_prefix_global_key_ranges(capacity):
-    """A 700-token prefix: at capacity 1024 the head_dim-512 global layers'
-    key ranges are cut into 512-key chunks and merged, at 8192 they are not
-    (1024-key chunks); both within the bounds of the f32 and f16-rounding
-    forwards."""
+@pytest.mark.parametrize("heads,kv", [(8, 2), (4, 1)])
+def test_gemma4_long_prefix_global_key_ranges(capacity, heads, kv):
+    """A 700-token prefix on the reference's gemma4 configs and weights
+    (reference.rs:66-104, 108-139): at capacity 1024 the head_dim-512 global
+    layers' key ranges are cut into 512-key chunks and merged, at 8192 they
+    are not (1024-key chunks)."""
     rng = np.random.default_rng(4)
     prefix = rng.integers(0, 64, 700).tolist()
     branches = [BranchTokens(rng.integers(0, 64, 37).tolist(), [0, 20, 36]) for _ in range(3)]
-    cfg = gemma4_tiny(8, 2)
-    ts = soften(list(g.Weights.synth(cfg, 13, g.Q4, g.Q8).tensors()))
+    cfg = gemma4_tiny(heads, kv)
+    ts = list(g.Weights.synth(cfg, 13, g.Q4, g.Q8).tensors())
     out = engine_of(cfg, ts, capacity).evaluate(prefix, branches, Want.HIDDEN)
-    worst_p = worst_g = 0.0
-    for gpu_rounding in (False, True):
-        exp = oracle_rows(oracle.Model(cfg, ts, gpu_rounding=gpu_rounding), prefix, branches)
-        w = max(rel_diff(r, e) for o, ex in zip(out, exp) for r, e in zip(o.rows, ex))
-        worst_g, worst_p = (w, worst_p) if gpu_rounding else (worst_g, w)
-    print(f"rel diff vs f32 oracle {worst_p:.2e}, vs f16-rounding oracle {worst_g:.2e}")
-    assert worst_p < 2e-2 and worst_g < 4e-3
+    check_chaotic(out, cfg, ts, prefix, branches, capacity, f"{heads}/{kv} heads, capacity {capacity}")
+
+
+@pytest.mark.parametrize("layers", [1, 2])
+@pytest.mark.parametrize("heads,kv", [(8, 2), (4, 1)])
+def test_gemma4_long_prefix_by_depth(layers, heads, kv):
+    """The same 700-token request and weight distribution through one global
+    layer, or a sliding then a global layer (no K/V sharing): before the
+    amplification compounds, the GPU rows hold the reference's 2e-2 bar
+    against the f32 forward and sit within 3e-3 of the forward with the
+    kernel's own rounding points (measured 2e-4 .. 1.2e-3)."""
+    rng = np.random.default_rng(4)
+    prefix = rng.integers(0, 64, 700).tolist()
+    branches = [BranchTokens(rng.integers(0, 64, 37).tolist(), [0, 20, 36]) for _ in range(3)]
+    sliding = [False] if layers == 1 else [True, False]
+    cfg = gemma4_tiny(heads, kv, layers=layers, sliding=sliding, shared_kv_layers=0, ff=96, double_wide_mlp=False)
+    ts = list(g.Weights.synth(cfg, 13, g.Q4, g.Q8).tensors())
+    out = engine_of(cfg, ts, 1024).evaluate(prefix, branches, Want.HIDDEN)
+    hip = [o.rows for o in out]
+    f32 = oracle_rows(oracle.Model(cfg, ts), prefix, branches)
+    tiled = oracle_rows(tiled_oracle(cfg, ts, 1024), prefix, branches)
+    dp, dt = worst_rel(hip, f32), worst_rel(hip, tiled)
+    print(f"{layers} layer(s), {heads}/{kv} heads: GPU vs f32 {dp:.2e}, vs kernel rounding {dt:.2e}")
+    assert dp < 2e-2 and dt < 3e-3
 
 
 def test_gemma4_logits_apply_softcap():
@@ -167,15 +195,11 @@ def test_gemma4_open_dir_loads_the_per_layer_table(tmp_path):
 def test_gemma4_every_head_grouping(heads, kv):
     """Every query-heads-per-K/V-head grouping of the head_dim 256 and 512
     kernels (1, 2, 8, 16 per group; 4 is covered above), on a prefix long
-    enough for split key ranges, with q / k norms scaled down (see soften)."""
+    enough for split key ranges, on the reference's weight distribution."""
     rng = np.random.default_rng(6)
     prefix = rng.integers(0, 64, 300).tolist()
     branches = [BranchTokens(rng.integers(0, 64, 21).tolist(), [0, 20]) for _ in range(2)]
     cfg = gemma4_tiny(heads, kv)
-    ts = soften(list(g.Weights.synth(cfg, 29, g.Q4, g.Q8).tensors()))
+    ts = list(g.Weights.synth(cfg, 29, g.Q4, g.Q8).tensors())
     out = engine_of(cfg, ts, 512).evaluate(prefix, branches, Want.HIDDEN)
-    for gpu_rounding, tol in ((False, 2e-2), (True, 6e-3)):
-        exp = oracle_rows(oracle.Model(cfg, ts, gpu_rounding=gpu_rounding), prefix, branches)
-        worst = max(rel_diff(r, e) for o, ex in zip(out, exp) for r, e in zip(o.rows, ex))
-        print(f"gpu_rounding={gpu_rounding}: rel diff {worst:.2e}")
-        assert worst < tol
+    check_chaotic(out, cfg, ts, prefix, branches, 512, f"{heads}/{kv} heads")

@@ -85,6 +85,44 @@ def test_pack_matches_oracle():
         assert np.array_equal(wanted, owanted)
 
 
+def test_aligned_pack_is_the_reference_layout_with_groups_moved():
+    """The engine's layout (align_groups): the reference's packing with every
+    group after the first moved up to a multiple of `align` cache rows.
+    Real tokens keep their ids, positions and sequence ids in order; a
+    group's first key row is its new first row; padding rows between
+    groups carry token 0 and sequence id -1 and see only themselves;
+    wanted rows still point at the same tokens; a layout that would need
+    more rows than available stays the reference's."""
+    rng = np.random.default_rng(12)
+    for trial in range(60):
+        groups = random_groups(rng, int(rng.integers(1, 6)))
+        first = int(rng.integers(0, len(groups)))
+        resident = bool(trial % 2)
+        align = [32, 64][trial % 2]
+        ids, meta, wanted = g.pack(groups, first, resident)
+        aids, ameta, awanted = g.pack(groups, first, resident, align=align, rows=1 << 20)
+        base = len(groups[first].prefix) if resident else 0
+        real = ameta[:, 1] >= 0
+        assert np.array_equal(aids[real], ids) and np.array_equal(ameta[real][:, :2], meta[:, :2])
+        assert (aids[~real] == 0).all() and (ameta[~real][:, 0] == 0).all()
+        rows = base + np.arange(len(aids))
+        assert np.array_equal(ameta[:, 3], rows + 1)
+        assert np.array_equal(ameta[~real][:, 2], rows[~real])
+        groups_seen = ameta[real][:, 1] >> 12
+        starts = [int(rows[real][np.argmax(groups_seen == k)]) for k in np.unique(groups_seen) if k > 0]
+        assert all(r % align == 0 for r in starts)
+        for k in np.unique(groups_seen):
+            sel = real & ((ameta[:, 1] >> 12) == k)
+            lo = ameta[sel][:, 2]
+            assert (lo == lo[0]).all()
+            assert lo[0] == (0 if k == 0 else rows[sel][0])
+        assert np.array_equal(wanted[:, :3], awanted[:, :3])
+        assert np.array_equal(aids[awanted[:, 3]], ids[wanted[:, 3]])
+        # no room: the reference's layout
+        tight = g.pack(groups, first, resident, align=align, rows=base + len(ids))
+        assert np.array_equal(tight[1], meta)
+
+
 def test_pack_errors():
     # engine.rs:1537-1562: too many branches, wanted past the branch
     with pytest.raises(L.OmgError, match="past"):

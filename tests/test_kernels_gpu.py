@@ -118,3 +118,32 @@ def test_embed_gather_bit_exact(dtype):
     ms = (exp.astype(np.float64) ** 2).mean(axis=1, keepdims=True)
     exp_h = exp / np.sqrt(ms + 1e-6) * norm_w
     assert np.max(np.abs(hn.cpu().numpy().astype(np.float32) - exp_h)) < 1e-2 * np.max(np.abs(exp_h))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("vocab,d,nrows,softcap", [(25000, 640, 12, 0.0), (1000, 64, 1, 30.0), (4097, 1152, 37, 0.0)])
+def test_label_readout_matches_cpu(vocab, d, nrows, softcap, dtype):
+    """logits = rows . deq(E)^T in f32 (softcap applied), then the label
+    columns and log_sum_exp of the whole row (readout.rs:124-146,
+    math.rs:13-17), against float64 on the dequantized weights: label
+    logits within 1e-4 of the row scale, log-sum-exp within 1e-5."""
+    rng = np.random.default_rng(vocab + d + nrows + dtype)
+    t, _ = weight(rng, vocab, d, dtype, "embed")
+    e = t.to_f32().astype(np.float64)
+    rows = rng.uniform(-1, 1, (nrows, d)).astype(np.float32)
+    labels = rng.choice(vocab, 26, replace=False).astype(np.uint32)
+    w = g.DeviceWeight(t)
+    out = torch.zeros((nrows, 27), dtype=torch.float32, device="cuda")
+    lab = dev(labels.view(np.int32))
+    rd = dev(rows)
+    w.label_readout(rd.data_ptr(), nrows, lab.data_ptr(), 26, softcap, out.data_ptr())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    z = rows.astype(np.float64) @ e.T
+    if softcap > 0:
+        z = softcap * np.tanh(z / softcap)
+    m = z.max(1, keepdims=True)
+    lse = (m + np.log(np.exp(z - m).sum(1, keepdims=True)))[:, 0]
+    scale = np.maximum(np.abs(z).max(1), 1.0)
+    assert np.max(np.abs(got[:, :26] - z[:, labels]) / scale[:, None]) < 1e-4
+    assert np.max(np.abs(got[:, 26] - lse) / np.maximum(np.abs(lse), 1.0)) < 1e-5

@@ -409,3 +409,56 @@ def test_fold_averages_orders():
     # label A three logits ahead in both orders -> each option gets 1.5
     out = oracle.fold_mean([[0, 1], [1, 0]], [[3.0, 0.0], [3.0, 0.0]])
     assert out.tolist() == [1.5, 1.5]
+
+
+# ------------------------------------------- kernel-rounding attention
+
+def test_tiled_attention_is_the_softmax_up_to_f16_probabilities():
+    """set_attention_tiles models the flash kernel's rounding: with every
+    key in one chunk it differs from the f16-operand forward only by P's
+    f16 rounding (relative 2^-11 per probability), on the transformers
+    fixtures; with one-tile chunks (every tile a partial, merged by
+    weight) it stays within the f16 rounding of the partials of that."""
+    for n, cfg, seed, lin, emb, request, hidden in golden_cases():
+        ts = list(g.Weights.synth(cfg, seed, lin, emb).tensors())
+        ids, pos, seq = flat_request(request)
+        f16 = oracle.Model(cfg, ts, gpu_rounding=True).forward(ids, pos, seq)
+        whole = oracle.Model(cfg, ts, gpu_rounding=True).set_attention_tiles(32, 1000, 1000).forward(ids, pos, seq)
+        split = oracle.Model(cfg, ts, gpu_rounding=True).set_attention_tiles(4, 1, 1).forward(ids, pos, seq)
+        assert 0 < rel_diff(whole, f16) < 2e-3, (n, rel_diff(whole, f16))
+        assert rel_diff(split, whole) < 2e-3, (n, rel_diff(split, whole))
+        assert rel_diff(whole, hidden) < 4e-3
+
+
+def test_tiled_attention_does_not_depend_on_an_aligned_cache_offset():
+    """The property the engine's group alignment relies on: with the
+    kernel's whole-power-of-two max, every probability and rescale differs
+    by an exact power of two under another running max, so a group's rows
+    are bit-equal whether it starts the cache or starts on a key tile after
+    another group.  At an offset that is not a multiple of the key tile the
+    group's keys share MFMA tiles differently: f32 summation order changes,
+    and the f16 rounding of the attention output turns that into
+    ~1e-4 changes (why the engine starts every group on a key tile)."""
+    cfg = g.config_json(vocab=64, d=64, layers=3, heads=4, kv_heads=1, head_dim=256, ff=96, window=7,
+                        sliding=[True, False, True], norm_offset=0.0)
+    ts = list(g.Weights.synth(cfg, 5, g.Q4, g.Q8).tensors())
+    rng = np.random.default_rng(2)
+    prefix, toks = rng.integers(0, 64, 45).tolist(), rng.integers(0, 64, 13).tolist()
+    m = oracle.Model(cfg, ts, gpu_rounding=True).set_attention_tiles(32, 1000, 1000)
+    alone_ids = np.array(prefix + toks, np.uint32)
+    alone_pos = np.arange(len(prefix) + len(toks), dtype=np.int32)
+    alone_seq = np.array([0] * len(prefix) + [1] * len(toks), np.int32)
+    alone = m.forward(alone_ids, alone_pos, alone_seq)
+
+    def after(lead_len: int) -> np.ndarray:
+        # the same group (group bits 1 << 12) after a lead_len-token group 0
+        lead = rng.integers(0, 64, lead_len).tolist()
+        ids = np.array(lead + prefix + toks, np.uint32)
+        pos = np.array(list(range(lead_len)) + list(range(len(prefix) + len(toks))), np.int32)
+        seq = np.array([0] * lead_len + [1 << 12] * len(prefix) + [(1 << 12) | 1] * len(toks), np.int32)
+        return m.forward(ids, pos, seq)[lead_len:]
+
+    assert np.array_equal(after(32), alone)
+    assert np.array_equal(after(64), alone)
+    d = rel_diff(after(19), alone)
+    assert 0 < d < 5e-4, d
