@@ -108,6 +108,7 @@ _SIGS = {
     "omg_dev_gemm_geglu": (C.c_int, [_P, _P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
     "omg_dev_embed_norm": (C.c_int, [_P, _P, C.c_int64, C.c_float, _P, C.c_float, _P, _P, _P]),
     "omg_dev_label_readout": (C.c_int, [_P, _P, C.c_int64, _P, C.c_int64, C.c_float, _P, _P]),
+    "omg_dev_label_readout_noalloc": (C.c_int, [_P, _P, C.c_int64, _P, C.c_int64, C.c_float, _P, _P]),
     "omg_dev_gemm_geglu_erf": (C.c_int, [_P, _P, _P, C.c_int64, C.c_int64, _P, C.c_int64, _P]),
     "omg_dev_gemm_bias_relu": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, _P, C.c_int64, _P]),
     "omg_dev_qkv_heads": (C.c_int, [_P, _P, C.c_int64, C.c_int64, _P, _P, _P, C.c_float, C.c_int64, _P, _P, _P,

@@ -462,6 +462,15 @@ int omg_dev_label_readout(const omg_weight* embed, const float* rows, int64_t nr
     });
 }
 
+int omg_dev_label_readout_noalloc(const omg_weight* embed, const float* rows, int64_t nrows, const uint32_t* labels,
+                                  int64_t nlabels, float softcap, float* out, void* stream) {
+    return guard([&] {
+        if (!embed || !rows || !labels || !out) omg::fail(omg::E_INVALID, "null argument");
+        omg::launch_label_readout_noalloc(static_cast<hipStream_t>(stream), embed->t.w, rows, nrows, labels, nlabels,
+                                          softcap, out);
+    });
+}
+
 int omg_dev_embed_norm(const omg_weight* embed, const uint32_t* ids, int64_t t, float scale, const float* w,
                        float eps, float* x, void* hn_f16, void* stream) {
     return guard([&] {

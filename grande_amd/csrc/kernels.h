@@ -86,6 +86,13 @@ void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int
 void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows, const uint32_t* cols,
                    int64_t ncols, float softcap, float* out, float2* part = nullptr);
 int64_t logits_blocks(int64_t ncols);
+// The label readout (logits, then launch_label_lse) with its scratch in a
+// fixed device array instead of allocated memory: nothing is allocated;
+// nrows x vocab + 2 x nrows x logits_blocks(vocab) floats must fit
+// label_readout_scratch_floats().
+void launch_label_readout_noalloc(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows,
+                                  const uint32_t* labels, int64_t nlabels, float softcap, float* out);
+int64_t label_readout_scratch_floats();
 // Per row of full-vocabulary logits [nrows][vocab] and the logits kernel's
 // partials: the columns `labels`, then log-sum-exp over the whole row, into
 // out [nrows][nlabels + 1].

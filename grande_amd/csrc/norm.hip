@@ -4,6 +4,7 @@
 // the K/V <-> state-row conversions.  One wave64 per row; reductions are
 // wave-level shuffles, no LDS round trips.
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -688,6 +689,52 @@ void launch_label_lse(hipStream_t s, const float* logits, int64_t nrows, int64_t
     label_lse_kernel<<<dim3(unsigned(nrows)), dim3(256), 0, s>>>(logits, vocab, part, nblocks, nrows, labels,
                                                                  nlabels, out);
     OMG_HIP(hipGetLastError());
+}
+
+// ------------------------------------------- readout without allocation
+
+// Scratch of launch_label_readout_noalloc: the full logits rows, then the
+// logits kernel's (max, sum of exp) pairs.  A file-scope device array, so
+// every GPU the library runs on holds its own copy (16 MiB) until the
+// process ends; calls that overlap on one GPU share it and race.  Nothing
+// in it needs to start at zero: both parts are written whole before they
+// are read.
+constexpr int64_t READOUT_SCRATCH_FLOATS = int64_t(4) << 20;
+static __device__ __align__(256) float scratch[READOUT_SCRATCH_FLOATS];
+
+// The array's device address on the current GPU, looked up once per device
+// (in host code `scratch` names a host-side stand-in, not device memory).
+static float* readout_scratch() {
+    int dev = 0;
+    OMG_HIP(hipGetDevice(&dev));
+    constexpr int MAX_DEV = 64;
+    if (dev < 0 || dev >= MAX_DEV) fail(E_DEVICE, "label_readout_noalloc: device index out of range");
+    static std::mutex mu;
+    static float* ptr[MAX_DEV] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        OMG_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) fail(E_DEVICE, "label_readout_noalloc: no device address for the scratch array");
+        ptr[dev] = static_cast<float*>(p);
+    }
+    return ptr[dev];
+}
+
+int64_t label_readout_scratch_floats() { return READOUT_SCRATCH_FLOATS; }
+
+void launch_label_readout_noalloc(hipStream_t s, const DevWeight& E, const float* rows, int64_t nrows,
+                                  const uint32_t* labels, int64_t nlabels, float softcap, float* out) {
+    if (nrows <= 0 || nlabels <= 0) fail(E_INVALID, "label readout: no rows or no labels");
+    const int64_t vocab = E.rows, nb = logits_blocks(vocab);
+    const int64_t nlog = (nrows * vocab + 1) / 2 * 2;  // float2 partials on an 8-byte boundary
+    if (nlog + 2 * nb * nrows > READOUT_SCRATCH_FLOATS)
+        fail(E_CAPACITY, "label_readout_noalloc: " + std::to_string(nrows) + " rows x " + std::to_string(vocab) +
+                             " logits exceed the " + std::to_string(READOUT_SCRATCH_FLOATS) + "-float scratch");
+    float* base = readout_scratch();
+    float2* part = reinterpret_cast<float2*>(base + nlog);
+    launch_logits(s, E, rows, nrows, nullptr, vocab, softcap, base, part);
+    launch_label_lse(s, base, nrows, vocab, part, nb, labels, nlabels, out);
 }
 
 // ---------------------------------------------------------- state rows

@@ -313,6 +313,11 @@ class DeviceWeight:
                       stream: int | None = None) -> None:
         L.check(L.lib().omg_dev_label_readout(self._h, rows_ptr, nrows, labels_ptr, nlabels, softcap, out_ptr, stream))
 
+    def label_readout_noalloc(self, rows_ptr: int, nrows: int, labels_ptr: int, nlabels: int, softcap: float,
+                              out_ptr: int, stream: int | None = None) -> None:
+        L.check(L.lib().omg_dev_label_readout_noalloc(self._h, rows_ptr, nrows, labels_ptr, nlabels, softcap, out_ptr,
+                                                      stream))
+
     def embed_norm(self, ids_ptr: int, t: int, scale: float, w_ptr: int, eps: float, x_ptr: int, hn_ptr: int,
                    stream: int | None = None) -> None:
         L.check(L.lib().omg_dev_embed_norm(self._h, ids_ptr, t, scale, w_ptr, eps, x_ptr, hn_ptr, stream))

@@ -230,6 +230,14 @@ int omg_dev_gemm_geglu(const omg_weight *wg, const omg_weight *wu, const void *x
  * allocates and frees in stream order. */
 int omg_dev_label_readout(const omg_weight *embed, const float *rows, int64_t nrows, const uint32_t *labels,
                           int64_t nlabels, float softcap, float *out, void *stream);
+/* No counterpart in the reference.  omg_dev_label_readout for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops):
+ * same arguments and results, nothing allocated; its scratch is a fixed
+ * 16 MiB device array per GPU (4,194,304 floats), which must hold
+ * nrows * vocab + 2 * nrows * ceil(vocab / 64) floats, else OMG_E_CAPACITY.
+ * Calls that overlap on one GPU share that array and race. */
+int omg_dev_label_readout_noalloc(const omg_weight *embed, const float *rows, int64_t nrows, const uint32_t *labels,
+                                  int64_t nlabels, float softcap, float *out, void *stream);
 /* The embedding gather + first norm kernel (embed.wgsl + rmsnorm.wgsl):
  * x[t][d] = deq(E[ids[t]]) * scale (f32), hn[t][d] = f16(rmsnorm(x) * w)
  * with w (f32, d entries) already offset.  Device pointers. */
