@@ -6,7 +6,10 @@ vocabulary, one 2,000-token state plus 12 question branches of 32 tokens
 in one block-causal pass, label readout at each branch's last position:
 the 26 label logits and the log-sum-exp of the full 25,000-wide row, what
 the reference's Readout::distribution takes from the row
-(crates/omg-core/src/readout.rs:124-146).  A step is one cold pass (state + branches, T = 2,384) with
+(crates/omg-core/src/readout.rs:124-146).  Each timed step launches the
+whole pass: eagerly (one launch per kernel) and as a replay of the pass
+captured once into a HIP graph; `value` takes the faster, both are
+reported under `launch`.  A step is one cold pass (state + branches, T = 2,384) with
 the token ids and metadata already in HBM; the warm pass (branches only on
 the resident state, T = 384) and the API wall times (host upload and
 readback included) are reported beside it.
@@ -154,9 +157,12 @@ def main() -> int:
     restored_equal = all(np.array_equal(a.rows[0], b.rows[0]) for a, b in zip(warm_rows, restored_rows))
     warm_equal_cold = max(float(np.max(np.abs(a.rows[0] - b.rows[0]))) for a, b in zip(cold_rows, warm_rows))
 
-    def timed(first_resident: bool, steps: int, warmup: int) -> float:
+    def timed(first_resident: bool, steps: int, warmup: int, graph: bool = False) -> float:
         eng.prepare([Group(prefix, branches)], Want.LABELS_LSE, labels, first_resident=first_resident)
         for _ in range(warmup):
+            eng.launch()
+        if graph:
+            eng.graph(True)  # the pass's launches captured once, replayed per step
             eng.launch()
         eng.sync()
         t = time.perf_counter()
@@ -166,9 +172,12 @@ def main() -> int:
         return (time.perf_counter() - t) / steps
 
     eng.evict_resident()
-    cold_s = timed(False, args.steps, args.warmup)
+    cold_eager_s = timed(False, args.steps, args.warmup)
+    cold_graph_s = timed(False, args.steps, args.warmup, graph=True)
     eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)  # leaves the state resident
-    warm_s = timed(True, args.steps, args.warmup)
+    warm_eager_s = timed(True, args.steps, args.warmup)
+    warm_graph_s = timed(True, args.steps, args.warmup, graph=True)
+    cold_s, warm_s = min(cold_eager_s, cold_graph_s), min(warm_eager_s, warm_graph_s)
 
     # Per-kernel HIP-event times over a second timed region of cold steps.
     eng.profile(True)
@@ -209,6 +218,8 @@ def main() -> int:
         "config": {"workload": f"{args.config}: {shape}, vocab 25k, state {P} + {NB}x{BT} branches, "
                                "26 label logits + full-row log-sum-exp readout", "tokens": T, "state_tokens": P, "branches": NB,
                    "branch_tokens": BT},
+        "launch": {"cold_eager_ms": round(cold_eager_s * 1e3, 4), "cold_graph_ms": round(cold_graph_s * 1e3, 4),
+                   "warm_eager_ms": round(warm_eager_s * 1e3, 4), "warm_graph_ms": round(warm_graph_s * 1e3, 4)},
         "cold_tok_per_s": round(T / cold_s, 1),
         "warm_ms": round(warm_s * 1e3, 4),
         "warm_questions_per_s": round(NB / warm_s, 2),

@@ -99,6 +99,8 @@ _SIGS = {
     "omg_pass_prepare": (C.c_int, [_P, C.POINTER(omg_group), C.c_size_t, C.c_int, C.POINTER(C.c_uint32),
                                    C.c_size_t, C.c_int]),
     "omg_pass_launch": (C.c_int, [_P]),
+    "omg_pass_graph": (C.c_int, [_P, C.c_int]),
+    "omg_pass_read": (C.c_int, [_P, _P, C.c_size_t, C.POINTER(C.c_size_t)]),
     "omg_sync": (C.c_int, [_P]),
     "omg_profile": (C.c_int, [_P, C.c_int]),
     "omg_profile_report": (C.c_size_t, [_P, C.c_char_p, C.c_size_t]),

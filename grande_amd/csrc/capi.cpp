@@ -384,6 +384,18 @@ int omg_pass_launch(omg_engine* e) {
     return guard([&] { eng(e).launch_prepared(); });
 }
 
+int omg_pass_read(omg_engine* e, float* out, size_t out_floats, size_t* written) {
+    return guard([&] {
+        if (!out) omg::fail(omg::E_INVALID, "null output");
+        const int64_t n = eng(e).read_prepared(out, int64_t(out_floats));
+        if (written) *written = size_t(n);
+    });
+}
+
+int omg_pass_graph(omg_engine* e, int on) {
+    return guard([&] { eng(e).set_graph(on != 0); });
+}
+
 int omg_sync(omg_engine* e) {
     return guard([&] { eng(e).sync(); });
 }

@@ -276,6 +276,7 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
 
 Engine::~Engine() {
     if (stream_) (void)hipStreamSynchronize(stream_);
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
     for (Timed& t : pending_) (void)hipEventDestroy(t.e);
     for (hipEvent_t ev : event_pool_) (void)hipEventDestroy(ev);
     if (stream_) (void)hipStreamSynchronize(stream_);
@@ -405,6 +406,8 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     // resident prefix reaching past that is gone from here on, whatever
     // happens to the rest of the pass.
     if (resident_ && int64_t(resident_->size()) > pk.base) resident_.reset();
+    // A captured pass reads the work lists and buffers this upload may move.
+    drop_graph();
     uint8_t* h = static_cast<uint8_t*>(h_in_);
     // The previous pass may still read the staging buffer.
     OMG_HIP(hipStreamSynchronize(stream_));
@@ -689,8 +692,63 @@ void Engine::prepare(const GroupIn* groups, int64_t n, int want, const uint32_t*
 
 void Engine::launch_prepared() {
     if (prepared_.t <= 0) fail(E_INVALID, "no prepared pass");
+    if (graph_exec_ && !profile_) {
+        OMG_HIP(hipGraphLaunch(graph_exec_, stream_));
+        return;
+    }
     forward(prepared_.t, prepared_.base);
     readout(prepared_);
+}
+
+// The pass is kernels only (no copies or memsets between prepare and the
+// readout), so its captured graph replays exactly the launches above; the
+// work lists and buffers it reads stay where prepare put them until the
+// next prepare or evaluate, which drops the graph.
+void Engine::set_graph(bool on) {
+    drop_graph();
+    if (!on) return;
+    if (prepared_.t <= 0) fail(E_INVALID, "no prepared pass");
+    if (profile_) fail(E_INVALID, "graph capture while profiling");
+    sync();
+    hipGraph_t g = nullptr;
+    OMG_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    try {
+        forward(prepared_.t, prepared_.base);
+        readout(prepared_);
+    } catch (...) {
+        (void)hipStreamEndCapture(stream_, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    OMG_HIP(hipStreamEndCapture(stream_, &g));
+    const hipError_t err = hipGraphInstantiate(&graph_exec_, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (err != hipSuccess) {
+        graph_exec_ = nullptr;
+        fail(E_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(err));
+    }
+}
+
+int64_t Engine::read_prepared(float* out, int64_t out_floats) {
+    const PassPlan& p = prepared_;
+    if (p.t <= 0) fail(E_INVALID, "no prepared pass");
+    const int64_t width = p.want == WANT_HIDDEN   ? cfg_.d
+                          : p.want == WANT_LOGITS ? cfg_.vocab
+                          : p.want == WANT_LABELS ? p.nlabels
+                                                  : p.nlabels + 1;
+    if (p.nrows * width > out_floats) fail(E_INVALID, "output buffer too small for the prepared pass's rows");
+    const DevBuf& src = p.want == WANT_HIDDEN ? rows_ : p.want == WANT_LABELS_LSE ? label_lse_ : logits_;
+    sync();
+    if (p.nrows) OMG_HIP(hipMemcpy(out, src.p, size_t(p.nrows * width) * 4, hipMemcpyDeviceToHost));
+    return p.nrows * width;
+}
+
+void Engine::drop_graph() {
+    if (graph_exec_) {
+        (void)hipStreamSynchronize(stream_);
+        (void)hipGraphExecDestroy(graph_exec_);
+        graph_exec_ = nullptr;
+    }
 }
 
 // ----------------------------------------------------------- state cache

@@ -109,6 +109,13 @@ class Engine {
     void prepare(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
                  bool resident_first);
     void launch_prepared();
+    // Capture the prepared pass's launches into a HIP graph (on = true) that
+    // launch_prepared then replays as one submission; dropped by the next
+    // prepare, by any pass through evaluate, and by on = false.
+    void set_graph(bool on);
+    // The prepared pass's output rows after its launches (wanted order:
+    // group, branch, slot), width as evaluate_groups gives them.
+    int64_t read_prepared(float* out, int64_t out_floats);
     void sync();
     void set_profile(bool on);
     std::string profile_report() const;
@@ -188,6 +195,8 @@ class Engine {
     std::string model_id_ = "hip";
     // measurement
     PassPlan prepared_;
+    hipGraphExec_t graph_exec_ = nullptr;
+    void drop_graph();
     bool profile_ = false;
     struct Timed {
         const char* name;  // null for the sequence's start event

@@ -239,6 +239,17 @@ class Engine:
     def launch(self) -> None:
         L.check(L.lib().omg_pass_launch(self._h))
 
+    def graph(self, on: bool) -> None:
+        """Replay the prepared pass as one captured HIP graph."""
+        L.check(L.lib().omg_pass_graph(self._h, int(on)))
+
+    def read_prepared(self, max_floats: int) -> np.ndarray:
+        """The prepared pass's rows (wanted order) after its launches."""
+        out = np.zeros(max(max_floats, 1), np.float32)
+        n = C.c_size_t()
+        L.check(L.lib().omg_pass_read(self._h, out.ctypes.data_as(C.POINTER(C.c_float)), out.size, C.byref(n)))
+        return out[:n.value]
+
     def sync(self) -> None:
         L.check(L.lib().omg_sync(self._h))
 

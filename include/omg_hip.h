@@ -204,6 +204,15 @@ int omg_state_check(const uint8_t *bytes, size_t len, const char *model_id, size
 int omg_pass_prepare(omg_engine *e, const omg_group *groups, size_t ngroups, int want,
                      const uint32_t *label_ids, size_t nlabels, int first_resident);
 int omg_pass_launch(omg_engine *e);
+/* No counterpart in the reference (it records one command buffer per
+ * request, engine.rs:1761-1861): capture the prepared pass's kernel
+ * launches into a HIP graph (on != 0), which omg_pass_launch then replays
+ * as one submission; on = 0, the next omg_pass_prepare or any evaluate
+ * drops it. */
+int omg_pass_graph(omg_engine *e, int on);
+/* The prepared pass's rows after its launches (waits for them), in wanted
+ * order (group, branch, slot), width as omg_evaluate_groups gives them. */
+int omg_pass_read(omg_engine *e, float *out, size_t out_floats, size_t *written);
 int omg_sync(omg_engine *e);
 /* HIP-event time per kernel of every launch while on; the report is lines
  * "name launches total_ms". */

@@ -450,3 +450,33 @@ def test_long_groups_bit_equal_to_separate_passes(heads, kv):
         for x, y in zip(a, t.branches):
             for r, s in zip(x.rows, y.rows):
                 assert np.array_equal(r, s), f"group {i}"
+
+
+def test_graph_replay_matches_eager_pass():
+    """omg_pass_graph: the prepared pass captured once and replayed gives
+    the eager launch's rows bit for bit on every replay, with other eager
+    work (another engine's passes) and synchronisations between replays;
+    the same rows as evaluate; a new prepare drops the graph."""
+    eng, _, _, _ = build(gguf_tiny(8, 2, window=9), 41, g.Q4, g.Q8, capacity=512, oracle_models=False)
+    other, _, _, _ = build(gemma3_tiny(), 3, g.F16, g.F16, oracle_models=False)
+    rng = np.random.default_rng(5)
+    prefix = rng.integers(0, 64, 300).tolist()
+    branches = [BranchTokens(rng.integers(0, 64, n).tolist(), [n - 1]) for n in (9, 17, 4)]
+    labels = [3, 9, 27, 40]
+    ref = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
+    eng.evict_resident()
+    eng.prepare([Group(prefix, branches)], Want.LABELS_LSE, labels)
+    eng.launch()
+    eager = eng.read_prepared(1 << 12)
+    assert np.array_equal(eager.reshape(3, 5), np.stack([b.rows[0] for b in ref]))
+    eng.graph(True)
+    for rep in range(4):
+        eng.launch()
+        got = eng.read_prepared(1 << 12)
+        assert np.array_equal(got, eager), f"replay {rep}"
+        other.evaluate([2, 3, 4], [BranchTokens([5, 6], [1])], Want.HIDDEN)
+        other.sync()
+    eng.prepare([Group(prefix[:100], branches)], Want.LABELS_LSE, labels)  # drops the graph
+    eng.launch()
+    short = eng.read_prepared(1 << 12)
+    assert not np.array_equal(short, eager)
