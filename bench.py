@@ -179,10 +179,16 @@ def main() -> int:
     warm_graph_s = timed(True, args.steps, args.warmup, graph=True)
     cold_s, warm_s = min(cold_eager_s, cold_graph_s), min(warm_eager_s, warm_graph_s)
 
-    # Per-kernel HIP-event times over a second timed region of cold steps.
+    # Per-kernel HIP-event times over a second timed region of cold steps,
+    # then of warm steps (the branches on the resident state).
     eng.profile(True)
     timed(False, args.steps, 0)
     prof = eng.profile_report()
+    eng.profile(False)
+    eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
+    eng.profile(True)
+    timed(True, args.steps, 0)
+    wprof = eng.profile_report()
     eng.profile(False)
 
     macs = linear_macs_per_token(mc)
@@ -201,6 +207,15 @@ def main() -> int:
     dom = max((k for k in kernels if k in flops), key=lambda k: prof[k][1])
     dom_tf = kernels[dom]["tflops"]
     total_flop = sum(flops.values()) * mc["layers"]
+    warm_flops = {k: 2.0 * NB * BT * v for k, v in macs.items()}
+    warm_kernels = {}
+    for name, (n, ms) in wprof.items():
+        avg_us = ms / n * 1e3
+        entry = {"launches_per_step": n // args.steps, "avg_us": round(avg_us, 2),
+                 "share": round(ms / sum(v[1] for v in wprof.values()), 4)}
+        if name in warm_flops:
+            entry["tflops"] = round(warm_flops[name] / (avg_us * 1e-6) / 1e12, 1)
+        warm_kernels[name] = entry
 
     out = {
         "metric": METRIC if args.config == "c2" else f"questions/sec ({args.config}: {shape}), 1 GPU",
@@ -233,6 +248,7 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_F16_TFLOPS, 4),
                      "traffic": profiled_traffic(args.config, dom)},
         "kernels": kernels,
+        "warm_kernels": warm_kernels,
         "load_s": round(load_s, 2),
     }
 
@@ -420,6 +436,7 @@ def bench_gemma4(args) -> int:
         "warm_vs_cold_max_abs_logit": warm_equal_cold,
         "pass_tflops": round(sum(flop.values()) / cold_s / 1e12, 2),
         "kernels": kernels,
+        "warm_kernels": warm_kernels,
         "load_s": round(load_s, 2),
     }
     print(json.dumps(out))
@@ -511,6 +528,7 @@ def bench_encoder(args) -> int:
                      "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_F16_TFLOPS, 4),
                      "traffic": profiled_traffic("c4", dom)},
         "kernels": kernels,
+        "warm_kernels": warm_kernels,
         "load_s": round(load_s, 2),
     }
     if not args.no_cpu:

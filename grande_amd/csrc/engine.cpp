@@ -45,20 +45,20 @@ static DevBuf upload_bytes(const void* src, size_t n) {
     return b;
 }
 
-DevTensor upload_weight(const QTensor& t) {
+DevTensor upload_weight(const QTensor& t, bool tiled) {
     if (t.shape.size() != 2 || t.shape[1] % 32 != 0) fail(E_INVALID, "weight: expected [rows, cols % 32 == 0]");
     DevTensor d;
     d.w.dtype = int(t.dtype);
     d.w.rows = t.shape[0];
     d.w.cols = t.shape[1];
     const int64_t n = d.w.rows * d.w.cols, kb = d.w.cols / BLOCK;
+    std::vector<uint8_t> rep;
     if (t.dtype == Q4) {
-        std::vector<uint8_t> rep(t.data.size());
+        rep.resize(t.data.size());
         repack_q4(t.data.data(), rep.data(), n);
-        d.data = upload_bytes(rep.data(), rep.size());
-    } else {
-        d.data = upload_bytes(t.data.data(), t.data.size());
     }
+    const uint8_t* src = t.dtype == Q4 ? rep.data() : t.data.data();  // row-major device bytes
+    d.data = upload_bytes(src, t.data.size());
     if (t.dtype != F16) {
         // Scale rows padded to an even count of blocks (zeros in the pad).
         d.w.sld = (kb + 1) / 2 * 2;
@@ -69,6 +69,37 @@ DevTensor upload_weight(const QTensor& t) {
     }
     d.w.data = d.data.p;
     d.w.scales = d.scales.as<uint16_t>();
+    if (!tiled) return d;
+
+    // Stage tiles (kernels.h): from the row-major device bytes above.
+    const int64_t rb = (d.w.rows + 31) / 32, st = (d.w.cols + 63) / 64;
+    const int PK = tile_packet_bytes(d.w.dtype);
+    const int64_t row_bytes = t.dtype == Q4 ? d.w.cols / 2 : (t.dtype == Q8 ? d.w.cols : 2 * d.w.cols);
+    const int CB = PK / 32, piece = CB / 8;  // bytes of one row per stage, per (k-step, half)
+    std::vector<uint8_t> tiles(size_t(rb * st * PK), 0);
+    std::vector<uint8_t> tsc(t.dtype == F16 ? 0 : size_t(rb * st * TILE_SCALE_BYTES), 0);
+    for (int64_t r = 0; r < d.w.rows; ++r) {
+        const int64_t b = r / 32, rr = r % 32;
+        for (int64_t s = 0; s < st; ++s) {
+            uint8_t* pk = tiles.data() + (b * st + s) * PK;
+            for (int ks = 0; ks < 4; ++ks)
+                for (int h = 0; h < 2; ++h) {
+                    const int64_t at = s * CB + ks * (CB / 4) + h * piece;
+                    if (at + piece <= row_bytes)
+                        std::memcpy(pk + (32 * h + rr) * (PK / 64) + ks * (PK / 256), src + r * row_bytes + at,
+                                    size_t(piece));
+                }
+            if (t.dtype != F16)
+                for (int64_t blk = 2 * s; blk < 2 * s + 2 && blk < kb; ++blk)
+                    std::memcpy(tsc.data() + (b * st + s) * TILE_SCALE_BYTES + rr * 4 + (blk - 2 * s) * 2,
+                                t.scales.data() + (r * kb + blk) * 2, 2);
+        }
+    }
+    d.tiles = upload_bytes(tiles.data(), tiles.size());
+    if (!tsc.empty()) d.tscales = upload_bytes(tsc.data(), tsc.size());
+    d.w.tiles = d.tiles.as<uint8_t>();
+    d.w.tscales = d.tscales.as<uint8_t>();
+    d.w.stages = st;
     return d;
 }
 
@@ -104,7 +135,9 @@ void Builder::push(const std::string& name, const QTensor& t) {
         return;
     }
     if (t.shape[1] % 32 != 0) fail(E_INVALID, name + ": inner dimension is not a multiple of 32");
-    linears_[name] = upload_weight(t);
+    // The embedding tables are only gathered by rows (and the token table
+    // read by the readout's own kernel), never fed to a GEMM.
+    linears_[name] = upload_weight(t, name != "embed" && name != "per_layer_table");
     norms_.erase(name);
 }
 
@@ -449,19 +482,23 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     }
 }
 
-// K splits of the deep o / down products (output width n <= 2048): one
-// per 2048 of K, at most OMG_KSPLIT, whole 64-wide stages per split.
-// Their tiles are few and each runs K / 64 stages in series; the splits
-// run side by side and the residual norm adds them.  Widths up to 1280 get
-// 64-column tiles (twice the workgroups of the 128-column tiles above), so
-// they split from K 8192, wider ones from K 4096 (measured: Gemma 4 E2B's
-// K 4096 / 6144 / 12288 at n 1536 gain on cold and warm passes, the 1B's
-// K 6912 at n 1152 loses 3% cold).  A function of the shape only, so a
-// row's sums do not depend on the pass (rows over a resident prefix stay
-// bit-equal to a full pass).
+// K splits of the o / down products (output width n <= 2048): their tiles
+// are few (128 output columns each) and each runs K / 64 stages in series;
+// the splits run side by side and the residual norm adds them.  Widths up
+// to 1280 split in two from K 1024 (measured on the 270M model's o and
+// down, K 1024 / 2048 at n 640: both the 2,384-token cold pass and the
+// 384-token warm pass gain, the warm one most), and every width splits
+// one per 2048 of K from K 8192 (4096 above n 1280), at most OMG_KSPLIT
+// (Gemma 4 E2B's K 4096 / 6144 / 12288 at n 1536).  Whole 64-wide stages
+// per split.  A function of the shape only, so a row's sums do not depend
+// on the pass (rows over a resident prefix stay bit-equal to a full pass).
 static int ksplit(int64_t k, int64_t n) {
-    if (n > 2048 || k < (n > 1280 ? 4096 : 8192)) return 1;
-    int s = int(std::min<int64_t>(OMG_KSPLIT, k / 2048));
+    if (n > 2048 || k < 1024) return 1;
+    int s = 1;
+    if (k >= (n > 1280 ? 4096 : 8192))
+        s = int(std::min<int64_t>(OMG_KSPLIT, k / 2048));
+    else if (n <= 1280)
+        s = 2;
     while (s > 1 && k % (64 * s) != 0) --s;
     return s;
 }

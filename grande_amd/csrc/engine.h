@@ -47,11 +47,12 @@ struct DevBuf {
 
 struct DevTensor {
     DevWeight w;
-    DevBuf data, scales;
+    DevBuf data, scales, tiles, tscales;
 };
 // Upload a linear weight in the device layout (Q4 repacked, scale rows
-// padded to an even block count).
-DevTensor upload_weight(const QTensor& t);
+// padded to an even block count) and, when `tiled` (every weight a GEMM
+// reads; not the gather-only embedding tables), as stage tiles.
+DevTensor upload_weight(const QTensor& t, bool tiled = true);
 
 class Engine;
 

@@ -39,6 +39,7 @@
 // lanes and weight lanes past K are sent out of range by their lane offset
 // (a zero activation times a zero weight).
 #include <string>
+#include <utility>
 
 #include "common.h"
 #include "kern_common.h"
@@ -91,8 +92,16 @@ __device__ inline void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// LDS writes done, then the workgroup barrier; a compiler fence for memory.
-__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// LDS operations done (s_waitcnt lgkmcnt(0), other counters left alone),
+// then the workgroup barrier, between compiler fences for memory.  Written
+// with builtins rather than inline assembly so that the compiler's own
+// wait-count tracking knows the LDS counter is clear afterwards.
+__device__ inline void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 // matmul_gated.wgsl:117-129: exact GELU, 0.5 x (1 + erf(x / sqrt 2)), with
 // erf from Abramowitz & Stegun 7.1.26 (|error| < 1.5e-7), the form the
@@ -459,6 +468,297 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
     }
 }
 
+// ------------------------------------------------------ 32x32x16 tiles
+
+// The decoder's products (f32 out and the gated GeGLU) on
+// v_mfma_f32_32x32x16_f16, which issues at full rate on gfx950 with one or
+// two accumulation chains per wave (16x16x32 needs about sixteen).  Row-
+// owner scheme: each wave owns 32 * NJ weight rows across all BM = 32 * MI
+// activation rows, so its weights are private to it and go straight from
+// their stage tiles (kernels.h) into registers: per stage and row block
+// one coalesced 16-byte-per-lane load of the packet (lane 32 h + r gets
+// row r's four k-steps of half h) and one 4-byte load of the row's block
+// scales.  Only the activation tile, which every wave reads, goes through
+// LDS.  Per 64-wide K stage, four 16-wide steps: lane l supplies A = the
+// decoded weight word of row l % 32 at k 16 s + 8 (l / 32) (one Q4 word,
+// two Q8 words or 16 bytes of f16), B = X row l % 32 of each activation
+// block at the same k (one 16-byte LDS read), and holds D for activation
+// row l % 32 at weight rows 8 j + 4 (l / 32) + i: four consecutive output
+// columns per j, stored as one vector.  The K order (stage, step) does not
+// depend on the tile shape, so every dispatch gives every output element
+// the same sums: rows of a pass are the same whatever else it holds.
+//
+// Pipeline, iteration kt (stage kt):
+//   wait for stage kt + 1's X DMA (this wave's), barrier (everyone's; and
+//       everyone has finished reading the ring slot of stage kt - 1);
+//   DMA stage kt + NS - 1's X tile into that slot;
+//   read stage kt + 1's X fragments from LDS into registers;
+//   decode + MFMA stage kt (X fragments read one iteration earlier,
+//       weights loaded NS - 1 iterations earlier);
+//   load stage kt + NS - 1's weights into the register slot just used.
+// Every wave issues the same memory instructions in every iteration (past
+// the end they read empty resources), so the wait counts are constants.
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_ = 4>
+struct Cfg32 {
+    static constexpr bool GATED = EPI == EPI_GELU_TANH || EPI == EPI_GELU_ERF;
+    static constexpr int NW = NW_, T = NW * WAVE;
+    static constexpr int BM = 32 * MI;
+    static constexpr int WR = 32 * NJ;                 // weight rows per wave
+    static constexpr int BNW = NW * WR;                // weight rows per tile
+    static constexpr int BN = GATED ? BNW / 2 : BNW;   // output columns per tile
+    static constexpr int PM = BN / 32;                 // row blocks per matrix
+    static constexpr int PK = tile_packet_bytes(QUANT);
+    static constexpr int CL = PK / 1024;               // 16-byte code loads per row block and stage
+    static constexpr int X_CH = BM * 8, X_I = (X_CH + T - 1) / T;
+    static constexpr int WL = NJ * (CL + (QUANT == F16_DT ? 0 : 1));  // weight loads per wave and stage
+    static constexpr int C = X_I + WL;                 // memory instructions per wave and stage
+    static constexpr int R = NS - 1;                   // weight register slots
+    static constexpr int U = R % 2 == 0 ? R : 2 * R;   // loop unroll: X fragments alternate two sets
+    static constexpr int X_BYTES = X_I * T * 16;
+    static constexpr int LDS = NS * X_BYTES;
+    static_assert(LDS <= 160 * 1024, "ring larger than the LDS");
+    static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
+    static_assert(NS >= 3, "ring needs >= 3 slots: one read into registers, one landing, one in flight");
+    static_assert(WL + (NS - 2) * C <= 63, "vmcnt range");
+};
+
+template <class F, size_t... I>
+__device__ inline bool run_phases(F& f, std::index_sequence<I...>) {
+    return (f(std::integral_constant<int, int(I)>{}) && ...);
+}
+
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_>
+__global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
+    using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW_>;
+    constexpr bool GATED = P::GATED;
+    constexpr int NW = P::NW, BM = P::BM, BN = P::BN, WR = P::WR, PK = P::PK, PM = P::PM, R = P::R;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = int(threadIdx.x), lane = tid % WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+
+    // XCD-aware tile order (see gemm_kernel).
+    const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
+    const int ntn = int((N + BN - 1) / BN);
+    const int ntiles = ntn * int((M + BM - 1) / BM);
+    const int per_xcd = int(gridDim.x) / 8;
+    const int tile = (int(blockIdx.x) % 8) * per_xcd + int(blockIdx.x) / 8;
+    if (tile >= ntiles) return;
+    const int64_t n0 = int64_t(tile % ntn) * BN, m0 = int64_t(tile / ntn) * BM;
+    const int kbeg = int(blockIdx.y) * int(K / g.ksplit);
+    const int nk = int((K / g.ksplit + G_BK - 1) / G_BK);
+    const int K32 = int(K);
+    const int64_t rows_m = M - m0 < BM ? M - m0 : BM;
+
+    uint32_t xoff[P::X_I];
+    int xcol[P::X_I];
+#pragma unroll
+    for (int i = 0; i < P::X_I; ++i) {
+        const int slot = (i * NW + wave) * WAVE + lane;
+        const int r = slot / 8, lc = (slot % 8) ^ swz(r);
+        xcol[i] = lc * 8;
+        xoff[i] = slot < P::X_CH ? uint32_t((r * g.ldx + lc * 8) * 2) : OOB;
+    }
+
+    // This wave's row blocks: j < NJ / 2 of the gate matrix and the rest of
+    // the up matrix when gated.  Block j's packet of stage st sits at
+    // st * PK + bj * stages * PK from the matrix's first block of the tile.
+    const int64_t stages = g.w0.stages, rblocks = (N + 31) / 32, rb0 = n0 / 32;
+    const int64_t live_blocks = rblocks - rb0;  // > 0: the tile starts inside N
+    auto mat_of = [&](int j) { return GATED && j >= NJ / 2 ? 1 : 0; };
+    auto blk_of = [&](int j) { return GATED ? wave * (NJ / 2) + (j % (NJ / 2)) : wave * NJ + j; };
+    uint32_t coff[NJ], scoff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        coff[j] = blk_of(j) < live_blocks ? uint32_t(blk_of(j) * stages * PK + lane * (PK / 64)) : OOB;
+        scoff[j] = blk_of(j) < live_blocks ? uint32_t(blk_of(j) * stages * TILE_SCALE_BYTES + (lane % 32) * 4) : OOB;
+    }
+
+    auto slot_base = [&](int s) { return smem + (s % NS) * P::X_BYTES; };
+    // X tile of stage s into its ring slot (only the K-tail stage, K % 64 ==
+    // 32, masks lanes; past the end the resource is empty).
+    auto issue_x = [&](int s) {
+        uint8_t* base = slot_base(s);
+        const bool live = s < nk;
+        const int k0 = __builtin_amdgcn_readfirstlane(kbeg + s * G_BK);  // uniform: a scalar offset
+        const int64_t xbytes = live ? rows_m * g.ldx * 2 : 0;
+        const bool tail = k0 + G_BK > K32;
+#pragma unroll
+        for (int i = 0; i < P::X_I; ++i) {
+            const uint32_t o = tail && xcol[i] >= K32 - k0 ? OOB : xoff[i];
+            const __amdgpu_buffer_rsrc_t r = rsrc(g.x + m0 * g.ldx, xbytes);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(base + (i * NW + wave) * WAVE * 16), 16, o,
+                                                     k0 * 2, 0, 0);
+        }
+    };
+
+    // A stage's weights in registers.
+    struct WRegs {
+        uint4 code[NJ][P::CL];
+        uint32_t sc[NJ];
+    };
+    auto issue_w = [&](int s, WRegs& w) {
+        const bool live = s < nk;
+        const int st = __builtin_amdgcn_readfirstlane((kbeg + s * G_BK) / G_BK);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const DevWeight& wt = mat_of(j) ? g.w1 : g.w0;
+            const __amdgpu_buffer_rsrc_t r = rsrc(wt.tiles + rb0 * stages * PK, live ? live_blocks * stages * PK : 0);
+#pragma unroll
+            for (int c = 0; c < P::CL; ++c)
+                w.code[j][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             r, coff[j] + 16 * c, st * PK, 0));
+            if constexpr (QUANT != F16_DT) {
+                const __amdgpu_buffer_rsrc_t rs = rsrc(wt.tscales + rb0 * stages * TILE_SCALE_BYTES,
+                                                       live ? live_blocks * stages * TILE_SCALE_BYTES : 0);
+                w.sc[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, scoff[j], st * TILE_SCALE_BYTES, 0);
+            }
+        }
+    };
+
+    floatx16 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[i][j] = floatx16{};
+
+    const int lr = lane % 32, lh = lane / 32;
+    int foff[4];  // the lane's X fragment offset within a 32-row block, per k-step
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) foff[ks] = lr * G_ROW + (((2 * ks + lh) ^ swz(lr)) * 16);
+
+    struct XRegs {
+        half8 x[4][MI];
+    };
+    auto read_x = [&](int s, XRegs& f) {
+        const uint8_t* X = slot_base(s);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int i = 0; i < MI; ++i) f.x[ks][i] = *reinterpret_cast<const half8*>(X + i * 32 * G_ROW + foff[ks]);
+    };
+    auto compute = [&](const XRegs& f, const WRegs& w) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            half8 wf[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                if constexpr (QUANT == F16_DT) {
+                    wf[j] = __builtin_bit_cast(half8, w.code[j][ks]);
+                } else {
+                    // k-steps 0, 1 are the stage's first block, 2, 3 its second
+                    const half_t d = __builtin_bit_cast(half_t, uint16_t(w.sc[j] >> (16 * (ks / 2))));
+                    if constexpr (QUANT == Q4_DT) {
+                        const uint4 u = w.code[j][0];
+                        const uint32_t word = ks == 0 ? u.x : ks == 1 ? u.y : ks == 2 ? u.z : u.w;
+                        wf[j] = dq4_word(word, half2v{d, d});
+                    } else {
+                        const uint4 u = w.code[j][ks / 2];
+                        wf[j] = ks % 2 == 0 ? dq8_words(u.x, u.y, half2v{d, d}) : dq8_words(u.z, u.w, half2v{d, d});
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], f.x[ks][i], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Prologue: stages 0 .. NS - 2 in the same order as the loop issues
+    // them (X, then weights), then stage 0's X fragments.
+    WRegs wr[R];
+    XRegs xa, xb;
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+        issue_x(s);
+        issue_w(s, wr[s]);
+    }
+    wait_vm<P::WL + (NS - 2) * P::C>();
+    lds_barrier();
+    read_x(0, xa);
+    int kt = 0;
+    auto step = [&](auto phase) {
+        constexpr int PH = decltype(phase)::value;
+        XRegs& cur = PH % 2 == 0 ? xa : xb;
+        XRegs& nxt = PH % 2 == 0 ? xb : xa;
+        // Stage kt + 1's X landed: after it this wave issued its weights
+        // and NS - 3 whole stages.
+        wait_vm<P::WL + (NS - 3) * P::C>();
+        lds_barrier();
+        issue_x(kt + NS - 1);
+        if (kt + 1 < nk) read_x(kt + 1, nxt);
+        compute(cur, wr[PH % R]);
+        issue_w(kt + NS - 1, wr[PH % R]);
+        return ++kt < nk;
+    };
+    while (run_phases(step, std::make_index_sequence<P::U>{})) {
+    }
+    wait_vm<0>();
+
+    // Epilogue: lane (lr, lh) holds, for activation row lr of block i,
+    // output columns 8 q + 4 lh + 0..3 of weight block j (q = 0..3).
+    constexpr int NO = GATED ? NJ / 2 : NJ;
+    const int64_t nw0 = n0 + (GATED ? wave * (WR / 2) : wave * WR);
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+        const int64_t m = m0 + i * 32 + lr;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < NO; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t n = nw0 + j * 32 + 8 * q + 4 * lh;
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (EPI == EPI_GELU_TANH)
+                        v[r] = gelu_tanh(acc[i][j][4 * q + r]) * acc[i][j + NJ / 2][4 * q + r];
+                    else if constexpr (EPI == EPI_GELU_ERF)
+                        v[r] = gelu_erf(acc[i][j][4 * q + r]) * acc[i][j + NJ / 2][4 * q + r];
+                    else
+                        v[r] = acc[i][j][4 * q + r];
+                }
+                if (n + 3 < N) {
+                    if constexpr (GATED)
+                        *reinterpret_cast<half4*>(static_cast<half_t*>(g.y) + m * g.ldy + n) =
+                            half4{half_t(v[0]), half_t(v[1]), half_t(v[2]), half_t(v[3])};
+                    else
+                        *reinterpret_cast<float4*>(static_cast<float*>(g.y) + int64_t(blockIdx.y) * g.part_stride +
+                                                   m * g.ldy + n) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (n + r >= N) break;
+                        if constexpr (GATED)
+                            static_cast<half_t*>(g.y)[m * g.ldy + n + r] = half_t(v[r]);
+                        else
+                            static_cast<float*>(g.y)[int64_t(blockIdx.y) * g.part_stride + m * g.ldy + n + r] = v[r];
+                    }
+                }
+            }
+    }
+}
+
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4>
+static void run32(hipStream_t s, const GemmArgs& g) {
+    using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW>;
+    for (const DevWeight* w : {&g.w0, &g.w1})
+        if (!w->tiles || w->stages != (w->cols + G_BK - 1) / G_BK || (QUANT != F16_DT && !w->tscales))
+            fail(E_INVALID, "gemm: weight without stage tiles");
+    static bool lds_set = false;
+    if (!lds_set) {
+        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
+        lds_set = true;
+    }
+    const int64_t N = g.w0.rows;
+    const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + P::BM - 1) / P::BM);
+    const dim3 grid(unsigned((tiles + 7) / 8 * 8), unsigned(g.ksplit));
+    gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW><<<grid, dim3(P::T), P::LDS, s>>>(g);
+    OMG_HIP(hipGetLastError());
+}
+
 template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4, int WM = 1>
 static void run(hipStream_t s, const GemmArgs& g) {
     using P = Cfg<QUANT, MI, NJ, EPI, NS, NW, WM>;
@@ -475,35 +775,28 @@ static void run(hipStream_t s, const GemmArgs& g) {
     OMG_HIP(hipGetLastError());
 }
 
-// Tile choice, measured on MI355X over the 270M / 1B / 4B decoder shapes
-// (cold passes of 2,384 tokens, warm passes of 384); tiles below are
-// activation rows x weight rows.  A two-slot ring (one stage of DMA in
-// flight, its latency covered by the other workgroups on the CU) fits more
-// workgroups per CU, which wins for the gated and wide launches that would
-// otherwise spill into a second round; the narrow o / down launches keep
-// four slots (between the pass's other kernels their loads wait longer).
-//   short passes (M <= 512): 32 x 64, two waves, four slots;
-//   narrow outputs (N <= 1280, the o and down projections): 64 x 64,
-//   96 x 64 from N = 768, four slots;
-//   wide outputs (the qkv projection): 128 x 64, 96 x 128 for K >= 4096.
-//   Tiles whose waves also split the activation rows (WM > 1: each wave
-//   reads fewer X fragments per MFMA) measured no faster at any of these
-//   shapes, so every dispatch keeps WM = 1.
-//   Long passes (M >= 8192, the encoder's 49,152-token batches; tile
-//   count is no constraint): 192 x 128, the best of the measured shapes
-//   for every linear of the mmBERT-base encoder; the q/k/v head scatter
-//   needs 64 weight rows per wave: 96 x 256.
+// Tile choice, measured on MI355X (tiles are activation rows x weight rows).
+// f32 products (gemm32_kernel, 32x32x16, four waves; whole-pass A/B on the
+// 270M model and an isolated sweep with rotating weight sets): 32 x 128
+// for short passes (M <= 512), 64 x 128, 96 x 128 when K is split (twice
+// the tiles), 128 x 128 for long passes (M >= 8192, the encoder's
+// 49,152-token batches).  The other epilogues (gemm_kernel, 16x16x32):
+//   bias+ReLU: short passes 32 x 32 on two waves; 64 x 64 (96 x 64 from
+//   N = 768) for N <= 1280; 128 x 64, 96 x 128 for K >= 4096; 192 x 128
+//   for long passes.  Q/K/V head scatter (64 weight rows per wave): 32 x
+//   256 short, 96 x 256 otherwise.
 //   Gated: 160 x 128 weight rows (64 output columns; a 2,384-token pass
 //   of the 270M model is 480 tiles, at most two per CU, where 128-row
 //   tiles made 608 and left 96 CUs a third), 128 x 256 with three slots
-//   for very wide layers, 64 x 128 for short passes.
+//   for very wide layers, 192 x 128 for long passes, 64 x 128 for short.
+// One template per product type for every M: rows do not depend on M.
 template <int QUANT, int EPI>
 static void dispatch(hipStream_t s, const GemmArgs& g) {
     const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
     if constexpr (EPI == EPI_QKV) {
         if (M <= 512) return run<QUANT, 2, 4, EPI, 4, 4>(s, g);
         return run<QUANT, 6, 4, EPI, 2, 4>(s, g);
-    } else if constexpr (EPI == EPI_F32 || EPI == EPI_RELU_F16) {
+    } else if constexpr (EPI == EPI_RELU_F16) {
         if (M <= 512) return run<QUANT, 2, 1, EPI, 4, 2>(s, g);
         if (M >= 8192) return run<QUANT, 12, 2, EPI, 2, 4>(s, g);
         if (N <= 1280) {
@@ -512,6 +805,12 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         }
         if (K >= 4096) return run<QUANT, 6, 2, EPI, 2, 4>(s, g);
         return run<QUANT, 8, 1, EPI, 2, 4>(s, g);
+    } else if constexpr (EPI == EPI_F32) {
+        // 32x32x16 tiles (gemm32_kernel) for every M: the same sums per element
+        if (M <= 512) return run32<QUANT, 1, 1, EPI, 4, 4>(s, g);
+        if (M >= 8192) return run32<QUANT, 4, 1, EPI, 3, 4>(s, g);
+        if (g.ksplit > 1) return run32<QUANT, 3, 1, EPI, 4, 4>(s, g);  // split K: twice the tiles
+        return run32<QUANT, 2, 1, EPI, 4, 4>(s, g);
     } else {
         if (M <= 512) return run<QUANT, 4, 2, EPI, 2, 4>(s, g);
         if (N >= 8192) return run<QUANT, 8, 4, EPI, 3, 4>(s, g);

@@ -22,13 +22,34 @@ constexpr int F16_DT = 0, Q8_DT = 1, Q4_DT = 2;
 //        block, 32-bit word w holds elements 8w..8w+7 with element 8w+p at
 //        bit 4*(p/2) (p even) or 16+4*(p/2) (p odd), so two shifts and a
 //        mask yield them as f16 pairs in order.  scales as Q8.
+//
+// Stage tiles: the same weight again for the decoder GEMMs, cut into
+// packets of 32 rows x 64 columns (one K stage of one MFMA row block) so
+// that a workgroup's DMA of a stage reads whole contiguous packets instead
+// of 32-byte pieces of many rows.  Packet (rb, st) of row block rb and
+// stage st sits at (rb * stages + st) * tile_packet_bytes(dtype) in
+// `tiles`; inside it, the 8-column group of row r at k-step ks (columns
+// 16 ks .. 16 ks + 15 of the stage) and half h (columns 16 ks + 8 h ..
+// + 7) sits at (32 h + r) * PK / 64 + ks * PK / 256, so one lane of a
+// 32x32x16 MFMA operand (row r, half h) reads all four k-steps of the
+// stage as one contiguous 16 / 32 / 64-byte run.  `tscales` holds a
+// 128-byte packet per (rb, st): row r's two block scales at 4 r (f16,
+// block 2 st in the low half).  Rows past `rows` and columns past `cols`
+// are zeros (codes and scales), so they contribute nothing.
 struct DevWeight {
     int dtype = 0;
     int64_t rows = 0, cols = 0;
     const void* data = nullptr;
     const uint16_t* scales = nullptr;  // [rows][sld] f16, block b of row r at r * sld + b
     int64_t sld = 0;                   // cols / 32 rounded up to even (the pad holds zeros)
+    const uint8_t* tiles = nullptr;    // stage tiles (see above)
+    const uint8_t* tscales = nullptr;  // their scale packets (Q8, Q4)
+    int64_t stages = 0;                // cols / 64 rounded up
 };
+
+// Bytes per stage-tile packet: 32 rows x 64 columns of codes.
+constexpr int tile_packet_bytes(int dtype) { return dtype == Q4_DT ? 1024 : (dtype == Q8_DT ? 2048 : 4096); }
+constexpr int TILE_SCALE_BYTES = 128;
 
 // Repack one Q4_0 tensor (model.rs layout: byte j = element j | element
 // j+16 << 4) into the device layout above.  n = element count.

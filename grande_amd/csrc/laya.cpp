@@ -308,7 +308,7 @@ void LayaBuilder::push(const std::string& name, const QTensor& t) {
         return;
     }
     if (t.shape[1] % 32 != 0) fail(E_INVALID, name + ": inner dimension " + std::to_string(t.shape[1]) + " is not a multiple of 32");
-    linears_[name] = upload_weight(t);
+    linears_[name] = upload_weight(t, name != "embed");
 }
 
 std::vector<std::string> LayaBuilder::missing() const {
