@@ -527,32 +527,35 @@ void Engine::forward(int64_t t, int64_t base) {
         Layer& L = layers_[size_t(l)];
         const int64_t hd = c.head_dim[size_t(l)], qw = c.qkv_width(l), ff = c.ff[size_t(l)];
         const int64_t src = c.kv_source[size_t(l)];
-        step("mm_qkv", [&] { launch_gemm(stream_, hn_.as<half_t>(), d, L.qkv.w, qkv_.as<float>(), qw, t); });
-        step("qk_prep", [&] {
-            QkArgs q{};
-            q.qkv = qkv_.as<float>();
-            q.qkv_stride = qw;
-            q.meta = meta_.as<int32_t>();
-            q.q_norm = L.q_norm.as<float>();
-            q.k_norm = c.has_kv(l) ? L.k_norm.as<float>() : nullptr;
-            q.rope = rope_tabs_[size_t(rope_of_[size_t(l)])].as<float2>();
-            q.rope_rows = rope_rows_;
-            q.rope_dims = c.rope_dims[size_t(l)];
-            q.eps = c.eps;
-            q.q_scale = c.query_scale;
-            q.heads = int(c.heads);
-            q.kv_heads = int(c.kv_heads);
-            q.hd = int(hd);
-            q.has_kv = c.has_kv(l);
-            q.v_norm = c.v_norm;
-            q.t = t;
-            q.base = base;
-            q.cap_pad = cap_pad_;
-            q.q16 = q16_.as<half_t>();
-            q.kc = kc_[size_t(src)].as<half_t>();
-            q.vt = vt_[size_t(src)].as<half_t>();
-            launch_qk_prep(stream_, q);
-        });
+        QkArgs q{};
+        q.qkv = qkv_.as<float>();
+        q.qkv_stride = qw;
+        q.meta = meta_.as<int32_t>();
+        q.q_norm = L.q_norm.as<float>();
+        q.k_norm = c.has_kv(l) ? L.k_norm.as<float>() : nullptr;
+        q.rope = rope_tabs_[size_t(rope_of_[size_t(l)])].as<float2>();
+        q.rope_rows = rope_rows_;
+        q.rope_dims = c.rope_dims[size_t(l)];
+        q.eps = c.eps;
+        q.q_scale = c.query_scale;
+        q.heads = int(c.heads);
+        q.kv_heads = int(c.kv_heads);
+        q.hd = int(hd);
+        q.has_kv = c.has_kv(l);
+        q.v_norm = c.v_norm;
+        q.t = t;
+        q.base = base;
+        q.cap_pad = cap_pad_;
+        q.q16 = q16_.as<half_t>();
+        q.kc = kc_[size_t(src)].as<half_t>();
+        q.vt = vt_[size_t(src)].as<half_t>();
+        if (hd == 256) {
+            // qk_prep's norms, RoPE and cache writes in the product's epilogue
+            step("mm_qkv", [&] { launch_gemm_qkprep(stream_, hn_.as<half_t>(), d, L.qkv.w, q, t); });
+        } else {
+            step("mm_qkv", [&] { launch_gemm(stream_, hn_.as<half_t>(), d, L.qkv.w, qkv_.as<float>(), qw, t); });
+            step("qk_prep", [&] { launch_qk_prep(stream_, q); });
+        }
         AttnArgs att{};
         att.q16 = q16_.as<half_t>();
         att.kc = kc_[size_t(src)].as<half_t>();

@@ -59,7 +59,10 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 //   EPI_RELU_F16   y[m][n] = f16(max(acc + bias[n], 0))
 //   EPI_QKV        the fused [q | k | v] projection of a bidirectional
 //                  encoder, scattered per head as f16 (see QkvHeads)
-constexpr int EPI_F32 = 0, EPI_GELU_TANH = 1, EPI_GELU_ERF = 2, EPI_RELU_F16 = 3, EPI_QKV = 4;
+//   EPI_QKPREP     the decoder's [q | k | v] projection with qk_prep's
+//                  work (per-head RMS norm, RoPE, query scale; q as f16
+//                  rows, k and V^T into the f16 cache), head_dim 256
+constexpr int EPI_F32 = 0, EPI_GELU_TANH = 1, EPI_GELU_ERF = 2, EPI_RELU_F16 = 3, EPI_QKV = 4, EPI_QKPREP = 5;
 
 struct GemmArgs {
     const half_t* x;
@@ -69,10 +72,13 @@ struct GemmArgs {
     int64_t ldy;
     const uint16_t* bias;  // f16 per output column (EPI_RELU_F16; EPI_QKV, may be null)
     QkvHeads qkv;          // EPI_QKV
+    QkArgs qk;             // EPI_QKPREP (its qkv / qkv_stride unused)
     // Split K (EPI_F32): blockIdx.y = split z sums K range
     // [z K / ksplit, (z + 1) K / ksplit) into y + z * part_stride.
     int ksplit = 1;
     int64_t part_stride = 0;
+    // gemm32_kernel: row tiles start at BM * i - mshift (0 <= mshift < BM)
+    int64_t mshift = 0;
 };
 
 constexpr int RSRC_FLAGS = 0x00020000;  // raw (untyped) 32-bit buffer
@@ -515,7 +521,13 @@ struct Cfg32 {
     static constexpr int R = NS - 1;                   // weight register slots
     static constexpr int U = R % 2 == 0 ? R : 2 * R;   // loop unroll: X fragments alternate two sets
     static constexpr int X_BYTES = X_I * T * 16;
-    static constexpr int LDS = NS * X_BYTES;
+    // EPI_QKPREP stages the f32 tile [BM][256] (rows padded to 260
+    // floats), eight partial sums of squares and a scale per row in LDS
+    // after the K loop.
+    static constexpr int QK_TS = 260;
+    static constexpr int QK_LDS = EPI == EPI_QKPREP ? BM * (QK_TS + 9) * 4 : 0;  // + [BM][8] sums, [BM] scales
+    static constexpr int LDS = NS * X_BYTES > QK_LDS ? NS * X_BYTES : QK_LDS;
+    static_assert(EPI != EPI_QKPREP || (BN == 256 && NW == 4), "the q/k/v epilogue: one 256-wide head, a thread per dimension");
     static_assert(LDS <= 160 * 1024, "ring larger than the LDS");
     static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
     static_assert(NS >= 3, "ring needs >= 3 slots: one read into registers, one landing, one in flight");
@@ -536,19 +548,23 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     const int tid = int(threadIdx.x), lane = tid % WAVE;
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
 
-    // XCD-aware tile order (see gemm_kernel).
+    // XCD-aware tile order (see gemm_kernel).  Row tiles start at
+    // BM * i - mshift (mshift < BM: the first tile is short), so a caller
+    // can align the tiles to its own row grid.
     const int64_t N = g.w0.rows, K = g.w0.cols, M = g.m;
     const int ntn = int((N + BN - 1) / BN);
-    const int ntiles = ntn * int((M + BM - 1) / BM);
+    const int ntiles = ntn * int((M + g.mshift + BM - 1) / BM);
     const int per_xcd = int(gridDim.x) / 8;
     const int tile = (int(blockIdx.x) % 8) * per_xcd + int(blockIdx.x) / 8;
     if (tile >= ntiles) return;
-    const int64_t n0 = int64_t(tile % ntn) * BN, m0 = int64_t(tile / ntn) * BM;
+    const int64_t n0 = int64_t(tile % ntn) * BN, m0 = int64_t(tile / ntn) * BM - g.mshift;
     const int kbeg = int(blockIdx.y) * int(K / g.ksplit);
     const int nk = int((K / g.ksplit + G_BK - 1) / G_BK);
     const int K32 = int(K);
-    const int64_t rows_m = M - m0 < BM ? M - m0 : BM;
+    auto row_ok = [&](int64_t r) { return m0 + r >= 0 && m0 + r < M; };  // tile row r is a row of the pass
 
+    // X lanes: row m0 + r of the whole matrix (rows before 0 or from M on
+    // are out of range, so they read as zeros).
     uint32_t xoff[P::X_I];
     int xcol[P::X_I];
 #pragma unroll
@@ -556,7 +572,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         const int slot = (i * NW + wave) * WAVE + lane;
         const int r = slot / 8, lc = (slot % 8) ^ swz(r);
         xcol[i] = lc * 8;
-        xoff[i] = slot < P::X_CH ? uint32_t((r * g.ldx + lc * 8) * 2) : OOB;
+        xoff[i] = slot < P::X_CH && row_ok(r) ? uint32_t(((m0 + r) * g.ldx + lc * 8) * 2) : OOB;
     }
 
     // This wave's row blocks: j < NJ / 2 of the gate matrix and the rest of
@@ -580,12 +596,12 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         uint8_t* base = slot_base(s);
         const bool live = s < nk;
         const int k0 = __builtin_amdgcn_readfirstlane(kbeg + s * G_BK);  // uniform: a scalar offset
-        const int64_t xbytes = live ? rows_m * g.ldx * 2 : 0;
+        const int64_t xbytes = live ? M * g.ldx * 2 : 0;
         const bool tail = k0 + G_BK > K32;
 #pragma unroll
         for (int i = 0; i < P::X_I; ++i) {
             const uint32_t o = tail && xcol[i] >= K32 - k0 ? OOB : xoff[i];
-            const __amdgpu_buffer_rsrc_t r = rsrc(g.x + m0 * g.ldx, xbytes);
+            const __amdgpu_buffer_rsrc_t r = rsrc(g.x, xbytes);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(base + (i * NW + wave) * WAVE * 16), 16, o,
                                                      k0 * 2, 0, 0);
         }
@@ -665,6 +681,25 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         }
     };
 
+    // EPI_QKPREP, q and k heads: the rope rows of the rows this thread
+    // finishes (8 rows per pass of the workgroup, row p * 8 + tid / 32),
+    // loaded now so their latency hides behind the K loop.
+    constexpr int QK_PASSES = EPI == EPI_QKPREP ? BM / 8 : 1;
+    int qpos[QK_PASSES];
+    if constexpr (EPI == EPI_QKPREP) {
+        const QkArgs& a = g.qk;
+#pragma unroll
+        for (int p = 0; p < QK_PASSES; ++p) {
+            const int r = p * 8 + tid / 32;
+            int pos = 0;
+            if (n0 / 256 < a.heads + a.kv_heads && row_ok(r)) {
+                pos = a.meta[4 * (a.base + m0 + r)];
+                pos = pos < 0 ? 0 : (pos >= a.rope_rows ? int(a.rope_rows - 1) : pos);
+            }
+            qpos[p] = pos;
+        }
+    }
+
     // Prologue: stages 0 .. NS - 2 in the same order as the loop issues
     // them (X, then weights), then stage 0's X fragments.
     WRegs wr[R];
@@ -696,6 +731,143 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     }
     wait_vm<0>();
 
+    if constexpr (EPI == EPI_QKPREP) {
+        // qk_prep.wgsl:66-114 on the tile's rows, without cross-lane
+        // traffic: each lane's sum of squares over its 32 accumulators of a
+        // row goes to LDS with the f32 tile (the ring is free: every DMA
+        // landed, every read done); a row's RMS is the sum of its eight
+        // partials in a fixed order.  q and k heads: 32 threads per row,
+        // thread c holding head dimensions 4c..4c+3 and their RoPE partners
+        // 128 + 4c..: RMS norm with the head's weight, RoPE, query scale,
+        // f16 q rows or k cache rows.  v head: (optional) RMS norm, then
+        // the V^T tiles of the cache in whole 16-byte chunks of 8 keys, 8
+        // lanes per 128-byte dimension row (the caller aligns the row tiles
+        // to 32 cache rows, so every chunk belongs to one tile; at the
+        // pass's edges a chunk keeps the cache's other keys).
+        constexpr int HD = 256, TS = P::QK_TS, HALF = HD / 2;
+        const QkArgs& a = g.qk;
+        float* T = reinterpret_cast<float*>(smem);
+        float* ssp = T + BM * TS;  // [BM][8] partial sums of squares
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    *reinterpret_cast<float4*>(T + (i * 32 + lr) * TS + wave * WR + j * 32 + 8 * q + 4 * lh) =
+                        make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ss += acc[i][j][4 * q + r] * acc[i][j][4 * q + r];
+                }
+            ssp[(i * 32 + lr) * 8 + 2 * wave + lh] = ss;
+        }
+        const int slot = int(n0 / HD);
+        const int H = a.heads, KV = a.kv_heads;
+        const bool is_v = slot >= H + KV;
+        const int c = tid % 32, d0 = 4 * c;
+        // The rope pairs of every pass now, while the tile is staged.
+        float4 r01[QK_PASSES], r23[QK_PASSES];
+        if (!is_v) {
+#pragma unroll
+            for (int p = 0; p < QK_PASSES; ++p) {
+                const float4* rt = reinterpret_cast<const float4*>(a.rope + int64_t(qpos[p]) * HALF + d0);
+                r01[p] = rt[0];
+                r23[p] = rt[1];
+            }
+        }
+        lds_barrier();
+        auto row_inv = [&](int r) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ss += ssp[r * 8 + k];
+            return 1.0f / sqrtf(ss / float(HD) + a.eps);
+        };
+        if (!is_v) {
+            const bool is_q = slot < H;
+            const int head = is_q ? slot : slot - H;
+            const float* wn = is_q ? a.q_norm : a.k_norm;
+            const float4 wl = *reinterpret_cast<const float4*>(wn + d0), wh = *reinterpret_cast<const float4*>(wn + HALF + d0);
+            const float w_lo[4] = {wl.x, wl.y, wl.z, wl.w}, w_hi[4] = {wh.x, wh.y, wh.z, wh.w};
+            const float sc = is_q ? a.q_scale : 1.0f;
+            const int rot = int(a.rope_dims / 2);
+#pragma unroll
+            for (int p = 0; p < QK_PASSES; ++p) {
+                const int r = p * 8 + tid / 32;
+                if (!row_ok(r)) continue;
+                const float inv = row_inv(r);
+                const float4 vl = *reinterpret_cast<const float4*>(T + r * TS + d0);
+                const float4 vh = *reinterpret_cast<const float4*>(T + r * TS + HALF + d0);
+                const float v_lo[4] = {vl.x, vl.y, vl.z, vl.w}, v_hi[4] = {vh.x, vh.y, vh.z, vh.w};
+                const float cs[4] = {r01[p].x, r01[p].z, r23[p].x, r23[p].z};
+                const float sn[4] = {r01[p].y, r01[p].w, r23[p].y, r23[p].w};
+                float o_lo[4], o_hi[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float y0 = v_lo[k] * inv * w_lo[k], y1 = v_hi[k] * inv * w_hi[k];
+                    if (d0 + k < rot) {
+                        o_lo[k] = y0 * cs[k] - y1 * sn[k];
+                        o_hi[k] = y1 * cs[k] + y0 * sn[k];
+                    } else {
+                        o_lo[k] = y0;
+                        o_hi[k] = y1;
+                    }
+                }
+                const int64_t tok = m0 + r, row = a.base + tok;
+                half_t* dst = is_q ? a.q16 + (tok * H + head) * HD : a.kc + (int64_t(head) * a.cap_pad + row) * HD;
+                *reinterpret_cast<half4*>(dst + d0) =
+                    half4{half_t(o_lo[0] * sc), half_t(o_lo[1] * sc), half_t(o_lo[2] * sc), half_t(o_lo[3] * sc)};
+                *reinterpret_cast<half4*>(dst + HALF + d0) =
+                    half4{half_t(o_hi[0] * sc), half_t(o_hi[1] * sc), half_t(o_hi[2] * sc), half_t(o_hi[3] * sc)};
+            }
+            return;
+        }
+        // V head: per 32-key half of the tile, item (dim, chunk cc) for
+        // 256 dims x 4 chunks; chunk 4 hf + cc of a 64-key cache tile holds
+        // keys 32 hf + 4 cc + {0..3, 16..19} (vt_col).
+        const int head = slot - H - KV;
+        float* rinv = ssp + BM * 8;  // [BM] row scales (v_norm)
+        if (a.v_norm) {
+            if (tid < BM) rinv[tid] = row_inv(tid);
+            lds_barrier();
+        }
+#pragma unroll
+        for (int hh = 0; hh < BM / 32; ++hh) {
+            const int64_t kh = a.base + m0 + 32 * hh;  // first cache row of this half (a multiple of 32)
+            if (m0 + 32 * hh + 32 <= 0 || m0 + 32 * hh >= M) continue;
+            const int64_t t0 = kh / 64 * 64;
+            const int hf = int((kh % 64) / 32);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int item = tid + 256 * u;
+                const int dim = item / 4, cc = item % 4;
+                half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + t0 / 64) * HD + dim) * 64 + 8 * (4 * hf + cc);
+                half_t h[8];
+                bool all = true;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int r = 32 * hh + 4 * cc + 16 * (e / 4) + e % 4;  // tile row of key e
+                    const bool in = row_ok(r);
+                    all = all && in;
+                    const float v = T[r * TS + dim];
+                    h[e] = half_t(a.v_norm ? v * rinv[r] : v);
+                }
+                if (!all) {
+                    // a pass edge: the chunk's other keys keep the cache's values
+                    const half8 old = *reinterpret_cast<const half8*>(dst);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int r = 32 * hh + 4 * cc + 16 * (e / 4) + e % 4;
+                        if (!row_ok(r)) h[e] = old[e];
+                    }
+                }
+                *reinterpret_cast<half8*>(dst) = half8{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+            }
+        }
+        return;
+    }
+
     // Epilogue: lane (lr, lh) holds, for activation row lr of block i,
     // output columns 8 q + 4 lh + 0..3 of weight block j (q = 0..3).
     constexpr int NO = GATED ? NJ / 2 : NJ;
@@ -703,7 +875,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
         const int64_t m = m0 + i * 32 + lr;
-        if (m >= M) continue;
+        if (m < 0 || m >= M) continue;
 #pragma unroll
         for (int j = 0; j < NO; ++j)
 #pragma unroll
@@ -753,7 +925,8 @@ static void run32(hipStream_t s, const GemmArgs& g) {
         lds_set = true;
     }
     const int64_t N = g.w0.rows;
-    const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + P::BM - 1) / P::BM);
+    if (g.mshift < 0 || g.mshift >= P::BM) fail(E_INVALID, "gemm: row tile shift out of range");
+    const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + g.mshift + P::BM - 1) / P::BM);
     const dim3 grid(unsigned((tiles + 7) / 8 * 8), unsigned(g.ksplit));
     gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW><<<grid, dim3(P::T), P::LDS, s>>>(g);
     OMG_HIP(hipGetLastError());
@@ -805,6 +978,9 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         }
         if (K >= 4096) return run<QUANT, 6, 2, EPI, 2, 4>(s, g);
         return run<QUANT, 8, 1, EPI, 2, 4>(s, g);
+    } else if constexpr (EPI == EPI_QKPREP) {
+        if (M <= 512) return run32<QUANT, 1, 2, EPI, 4, 4>(s, g);
+        return run32<QUANT, 2, 2, EPI, 4, 4>(s, g);
     } else if constexpr (EPI == EPI_F32) {
         // 32x32x16 tiles (gemm32_kernel) for every M: the same sums per element
         if (M <= 512) return run32<QUANT, 1, 1, EPI, 4, 4>(s, g);
@@ -880,6 +1056,22 @@ void launch_gemm_bias_relu(hipStream_t s, const half_t* x, int64_t ldx, const De
     if (!bias) fail(E_INVALID, "gemm_bias_relu: bias required");
     if (m == 0) return;
     dispatch_dtype<EPI_RELU_F16>(s, GemmArgs{x, ldx, m, w, w, y, ldy, bias, {}});
+}
+
+void launch_gemm_qkprep(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, const QkArgs& a, int64_t m) {
+    check(x, ldx, w, w.rows, m);
+    const int64_t slots = a.heads + (a.has_kv ? 2 * a.kv_heads : 0);
+    if (a.hd != 256 || a.heads <= 0 || a.kv_heads <= 0 || w.rows != slots * 256)
+        fail(E_INVALID, "gemm_qkprep: head_dim 256 and N = (heads + 2 kv_heads) x 256 (heads x 256 without K/V)");
+    if (a.base < 0 || a.base + m > a.cap_pad || a.cap_pad % 64) fail(E_INVALID, "gemm_qkprep: cache rows out of range");
+    if (a.rope_rows <= 0 || a.rope_dims > a.hd || !a.rope || !a.meta || !a.q_norm || !a.q16)
+        fail(E_INVALID, "gemm_qkprep: rope table, row meta, q norm and q output required");
+    if (a.has_kv && (!a.k_norm || !a.kc || !a.vt)) fail(E_INVALID, "gemm_qkprep: K/V layer without k norm or cache");
+    if (m == 0) return;
+    GemmArgs g{x, ldx, m, w, w, nullptr, 0, nullptr, {}};
+    g.qk = a;
+    g.mshift = a.base % 32;  // row tiles on the cache's 32-row grid: whole V^T chunks per tile
+    dispatch_dtype<EPI_QKPREP>(s, g);
 }
 
 void launch_gemm_qkv_heads(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w,

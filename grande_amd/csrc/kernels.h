@@ -95,6 +95,10 @@ struct QkArgs {
     half_t* vt;   // [kv_heads][cap_pad/64][hd][64], key columns ordered by vt_col
 };
 void launch_qk_prep(hipStream_t s, const QkArgs& a);
+// The q/k/v projection x . W^T with launch_qk_prep's work in its epilogue
+// (head_dim 256; a.qkv unused): one launch instead of the f32 product and
+// qk_prep, the same rows.
+void launch_gemm_qkprep(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, const QkArgs& a, int64_t m);
 // out[p][i] = (cos, sin)(float(p) * inv_freq[i]) for p < rows, i < half.
 void launch_rope_table(hipStream_t s, const float* inv_freq, int64_t rows, int64_t half, float2* out);
 // rows[i] = rmsnorm(x[wanted[i]]) * w, f32.
