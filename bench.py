@@ -38,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "questions/sec + state prefill tok/s (Gemma-3-270M Q4_0, 2k state, 12 Qs), 1 GPU"
 PEAK_F16_TFLOPS = 2500.0   # MI355X dense FP16/BF16 MFMA
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 SEED = 0x5EED
 
@@ -63,6 +64,62 @@ def visible_pairs(prefix: int, nb: int, bt: int, window: int, layers: int, patte
     return total
 
 
+def storage_bytes_per_elem(dtype) -> float:
+    """Q4_0 / Q8_0 / F16 bytes per weight (codes + block scales)."""
+    import grande_amd as g
+
+    return {g.Q4: 18 / 32, g.Q8: 34 / 32, g.F16: 2.0}[dtype]
+
+
+def pass_bytes(cfg, dtype, prefix: int, nb: int, bt: int, pattern: int = 6) -> dict:
+    """Algorithmic HBM bytes of one pass over a resident prefix: every
+    linear weight once, the token embedding once (the full-row log-sum-exp
+    reads every logit), and each layer's K and V rows that some query of
+    the pass can see (global layers: the whole prefix and the branches;
+    sliding layers: the last `window` prefix keys and the branches),
+    f16 K / V of kv_heads x head_dim per key."""
+    d, ff, H, KV, hd, L = cfg["d"], cfg["ff"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["layers"]
+    per_tok = sum(linear_macs_per_token(cfg).values())
+    w = per_tok * L * storage_bytes_per_elem(dtype)
+    emb = cfg["vocab"] * d * storage_bytes_per_elem(dtype)
+    kv = 0
+    for layer in range(L):
+        win = cfg["window"] if (layer + 1) % pattern != 0 else 0
+        keys = (min(prefix, win) if win else prefix) + nb * bt
+        kv += keys * KV * hd * 2 * 2
+    return {"weights": w, "embedding": emb, "kv": kv, "total": w + emb + kv}
+
+
+class MallFlush:
+    """Evicts the MALL between timed reps: one device-to-device copy of
+    `nbytes` (reads nbytes, writes nbytes), through the HIP runtime the
+    engine's library is linked against (a second runtime in the process,
+    such as torch's, would not see the GPU)."""
+
+    def __init__(self, nbytes: int):
+        import ctypes
+
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.nbytes = nbytes
+        self.src, self.dst = ctypes.c_void_p(), ctypes.c_void_p()
+        for ptr in (self.src, self.dst):
+            if self.hip.hipMalloc(ctypes.byref(ptr), ctypes.c_size_t(nbytes)) != 0:
+                raise RuntimeError("hipMalloc failed")
+        self.hip.hipMemset(self.src, 1, ctypes.c_size_t(nbytes))
+        self.hip.hipDeviceSynchronize()
+
+    def __call__(self):
+        import ctypes
+
+        if self.hip.hipMemcpy(self.dst, self.src, ctypes.c_size_t(self.nbytes), 3) != 0:  # device to device
+            raise RuntimeError("hipMemcpy failed")
+        self.hip.hipDeviceSynchronize()
+
+    def close(self):
+        self.hip.hipFree(self.src)
+        self.hip.hipFree(self.dst)
+
+
 def profiled_traffic(config: str, kernel: str):
     """HBM bytes per launch of `kernel` from the committed counter summary
     (profiles/<config>_<kernel>_traffic.md, a line "traffic_bytes_per_launch:
@@ -84,6 +141,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--small-reps", type=int, default=10,
+                    help="reps of the small-batch leg (one branch on the resident state, MALL flushed)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device to device three times (calibrates the HBM byte counters)")
     args = ap.parse_args()
@@ -195,6 +254,46 @@ def main() -> int:
     pairs = visible_pairs(P, NB, BT, mc["window"], mc["layers"])
     flops = {k: 2.0 * T * v for k, v in macs.items()}
     flops["attention"] = 4.0 * mc["heads"] * mc["head_dim"] * pairs / mc["layers"]
+    # Small-batch leg: one branch of BT tokens on the resident state, the
+    # serving loop's common case.  Before every rep 1 GiB is read and
+    # written, which evicts the 256 MB MALL, so the pass's weights, embedding
+    # and K/V come from HBM; each rep is one graph launch, timed to its end.
+    small = None
+    if args.small_reps > 0:
+        one = branches[:1]
+        eng.evaluate(prefix, one, Want.LABELS_LSE, labels)  # resident state stays
+        eng.prepare([Group(prefix, one)], Want.LABELS_LSE, labels, first_resident=True)
+        eng.graph(True)
+        eng.launch()
+        eng.sync()
+        flush = MallFlush(512 << 20)
+        times = []
+        for _ in range(args.small_reps):
+            flush()
+            t = time.perf_counter()
+            eng.launch()
+            eng.sync()
+            times.append(time.perf_counter() - t)
+        eng.graph(False)
+        # per-kernel HIP-event times of flushed reps (eager launches)
+        eng.profile(True)
+        for _ in range(3):
+            flush()
+            eng.launch()
+            eng.sync()
+        sprof = eng.profile_report()
+        eng.profile(False)
+        flush.close()
+        sb = pass_bytes(mc, spec["dtype"], P, 1, BT)
+        s_ms = float(np.median(times)) * 1e3
+        gbs = sb["total"] / (s_ms * 1e-3) / 1e9
+        small = {"branches": 1, "branch_tokens": BT, "reps": args.small_reps, "ms_median": round(s_ms, 4),
+                 "ms_min": round(min(times) * 1e3, 4), "mall_flush_bytes": 2 * flush.nbytes,
+                 "algorithmic_bytes": {k: int(v) for k, v in sb.items()}, "gb_per_s": round(gbs, 1),
+                 "hbm_peak_gb_per_s": HBM_PEAK_GBS, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                 "kernels": {name: {"launches_per_step": n // 3, "avg_us": round(ms / n * 1e3, 2)}
+                             for name, (n, ms) in sprof.items()}}
+
     kernels = {}
     for name, (n, ms) in prof.items():
         avg_us = ms / n * 1e3
@@ -208,6 +307,9 @@ def main() -> int:
     dom_tf = kernels[dom]["tflops"]
     total_flop = sum(flops.values()) * mc["layers"]
     warm_flops = {k: 2.0 * NB * BT * v for k, v in macs.items()}
+    wb = pass_bytes(mc, spec["dtype"], P, NB, BT)
+    warm_pairs = visible_pairs(P, NB, BT, mc["window"], mc["layers"]) - visible_pairs(P, 0, BT, mc["window"], mc["layers"])
+    warm_flop = sum(warm_flops.values()) * mc["layers"] + 4.0 * mc["heads"] * mc["head_dim"] * warm_pairs
     warm_kernels = {}
     for name, (n, ms) in wprof.items():
         avg_us = ms / n * 1e3
@@ -249,6 +351,11 @@ def main() -> int:
                      "traffic": profiled_traffic(args.config, dom)},
         "kernels": kernels,
         "warm_kernels": warm_kernels,
+        "warm_roofline": {"flop": warm_flop, "tflops": round(warm_flop / warm_s / 1e12, 2),
+                          "mfma_frac": round(warm_flop / warm_s / 1e12 / PEAK_F16_TFLOPS, 4),
+                          "algorithmic_bytes": int(wb["total"]), "gb_per_s": round(wb["total"] / warm_s / 1e9, 1),
+                          "hbm_frac": round(wb["total"] / warm_s / 1e9 / HBM_PEAK_GBS, 4)},
+        "small_batch": small,
         "load_s": round(load_s, 2),
     }
 
@@ -436,7 +543,6 @@ def bench_gemma4(args) -> int:
         "warm_vs_cold_max_abs_logit": warm_equal_cold,
         "pass_tflops": round(sum(flop.values()) / cold_s / 1e12, 2),
         "kernels": kernels,
-        "warm_kernels": warm_kernels,
         "load_s": round(load_s, 2),
     }
     print(json.dumps(out))
@@ -528,7 +634,6 @@ def bench_encoder(args) -> int:
                      "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_F16_TFLOPS, 4),
                      "traffic": profiled_traffic("c4", dom)},
         "kernels": kernels,
-        "warm_kernels": warm_kernels,
         "load_s": round(load_s, 2),
     }
     if not args.no_cpu:
