@@ -18,11 +18,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int WAVE = 64;
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
 
 __device__ inline float wave_max(float v) {
 #pragma unroll
@@ -50,6 +45,22 @@ __device__ inline float sum_lanes_16_32(float v) {
     const uint32_t w = __builtin_bit_cast(uint32_t, m);
     const auto q = __builtin_amdgcn_permlane32_swap(w, w, false, false);
     return __builtin_bit_cast(float, uint32_t(q[0])) + __builtin_bit_cast(float, uint32_t(q[1]));
+}
+
+// Sum over the wave, the same bits in every lane: within each row of 16
+// lanes by DPP (quad swaps, then half-row and row mirrors: each step adds
+// two equal-shaped partial sums, so lanes that pair up get the same result),
+// then across rows with the permlane swaps above.  No LDS round trips.
+template <int CTRL>
+__device__ inline float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ inline float wave_sum(float v) {
+    v += dpp_f32<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_f32<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    return sum_lanes_16_32(v);
 }
 
 __device__ inline float half_bits_to_f32(uint16_t h) {

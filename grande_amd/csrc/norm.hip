@@ -67,8 +67,11 @@ void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, i
 // post-attention / post-feedforward norm of `a` is added into the stream x,
 // then the norm that reads x next writes its f16 input hn.  One wave per
 // row holding the row in registers (NV float4 per lane, element
-// 4 * (lane + 64 j)): every load is issued before the first reduction.
-template <int NV>
+// 4 * (lane + 64 j)): every load, the PARTS split-K partials included, is
+// issued before the first reduction; the partials are then added in
+// order p = 0, 1, ...  (PARTS = 0: a runtime count, one partial at a time,
+// for the widest rows with many splits.)
+template <int NV, int PARTS>
 __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ a,
                                                             const float* __restrict__ w1,
                                                             float* __restrict__ x,
@@ -83,18 +86,39 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
     const float* ar = a + row * d;
     float* xr = x + row * d;
     float4 av[NV], xv[NV], g1[NV], g2[NV];
+    constexpr int PE = PARTS > 1 ? PARTS - 1 : 1;  // extra partials held in registers
+    float4 pv[PE][NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int64_t q = lane + j * WAVE;
         if (q < nq) {
             av[j] = *reinterpret_cast<const float4*>(ar + 4 * q);
-            for (int p = 1; p < parts; ++p) {
-                const float4 b = *reinterpret_cast<const float4*>(ar + p * part_stride + 4 * q);
-                av[j].x += b.x, av[j].y += b.y, av[j].z += b.z, av[j].w += b.w;
+            if constexpr (PARTS > 1) {
+#pragma unroll
+                for (int p = 1; p < PARTS; ++p)
+                    pv[p - 1][j] = *reinterpret_cast<const float4*>(ar + p * part_stride + 4 * q);
             }
             xv[j] = *reinterpret_cast<const float4*>(xr + 4 * q);
             g1[j] = *reinterpret_cast<const float4*>(w1 + 4 * q);
             if (w2) g2[j] = *reinterpret_cast<const float4*>(w2 + 4 * q);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t q = lane + j * WAVE;
+        if (q < nq) {
+            if constexpr (PARTS > 1) {
+#pragma unroll
+                for (int p = 0; p < PARTS - 1; ++p) {
+                    const float4 b = pv[p][j];
+                    av[j].x += b.x, av[j].y += b.y, av[j].z += b.z, av[j].w += b.w;
+                }
+            } else if constexpr (PARTS == 0) {
+                for (int p = 1; p < parts; ++p) {
+                    const float4 b = *reinterpret_cast<const float4*>(ar + p * part_stride + 4 * q);
+                    av[j].x += b.x, av[j].y += b.y, av[j].z += b.z, av[j].w += b.w;
+                }
+            }
         }
     }
     float ss = 0.0f;
@@ -155,13 +179,20 @@ void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float*
         fail(E_INVALID, "residual_norm: split-K partials");
     const int nv = int((d / 4 + WAVE - 1) / WAVE);
     const dim3 grid(unsigned((t + 3) / 4)), block(256);
-#define OMG_RN(N) \
-    case N: residual_norm_kernel<N><<<grid, block, 0, s>>>(a, w1, x, w2, hn, t, d, eps, scale, parts, part_stride); break;
-    switch (nv) {
-        OMG_RN(1) OMG_RN(2) OMG_RN(3) OMG_RN(4) OMG_RN(5) OMG_RN(6) OMG_RN(7) OMG_RN(8)
-        OMG_RN(9) OMG_RN(10) OMG_RN(11) OMG_RN(12) OMG_RN(13) OMG_RN(14) OMG_RN(15) OMG_RN(16)
-        default: fail(E_INVALID, "residual_norm: width above 4096");
+    // Partials in registers while nv * parts <= 24 float4 per lane.
+    const int pk = parts == 1 ? 1 : (nv * parts <= 24 && parts <= 4 ? parts : 0);
+#define OMG_RN(N, P)                                                                                           \
+    case N * 8 + P:                                                                                            \
+        residual_norm_kernel<N, P><<<grid, block, 0, s>>>(a, w1, x, w2, hn, t, d, eps, scale, parts, part_stride); \
+        break;
+#define OMG_RNP(N) OMG_RN(N, 0) OMG_RN(N, 1) OMG_RN(N, 2) OMG_RN(N, 3) OMG_RN(N, 4)
+    if (nv > 16) fail(E_INVALID, "residual_norm: width above 4096");
+    switch (nv * 8 + pk) {
+        OMG_RNP(1) OMG_RNP(2) OMG_RNP(3) OMG_RNP(4) OMG_RNP(5) OMG_RNP(6) OMG_RNP(7) OMG_RNP(8)
+        OMG_RNP(9) OMG_RNP(10) OMG_RNP(11) OMG_RNP(12) OMG_RNP(13) OMG_RNP(14) OMG_RNP(15) OMG_RNP(16)
+        default: fail(E_INVALID, "residual_norm: unsupported shape");
     }
+#undef OMG_RNP
 #undef OMG_RN
     OMG_HIP(hipGetLastError());
 }
