@@ -523,96 +523,45 @@ void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int
 }
 
 // logits.wgsl:38-79's product, rows . deq(E[col])^T in f32 (no f16
-// rounding on this path, as in the reference): one wave per output column
-// (a vocabulary row of E) and block of up to 16 wanted rows.  Lanes split
-// the width, so each wave streams its E row once, coalesced, and finishes
-// with one wave reduction per row.  For the label readout the columns are
-// the label ids only.
-// LG_R rows per block: 16 for full-vocabulary logits (each E row is read
-// once per 16 rows), 4 for a few label columns (measured 16.6 -> 8.6 us
-// for 26 labels x 12 rows: more waves, shorter chains).
-template <int DT, int LG_R>
-__global__ __launch_bounds__(256) void logits_kernel(DevWeight E, const float* __restrict__ rows, int64_t nrows,
-                                                     const uint32_t* __restrict__ cols, int64_t ncols,
-                                                     float softcap, float* __restrict__ out) {
-    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
-    const int64_t j = int64_t(blockIdx.x) * 4 + wave;
-    if (j >= ncols) return;
-    const int64_t col = cols ? int64_t(cols[j]) : j;
-    const int64_t r0 = int64_t(blockIdx.y) * LG_R;
-    const int nr = int(nrows - r0 < LG_R ? nrows - r0 : LG_R);
-    const int64_t K = E.cols;
-    float acc[LG_R];
-#pragma unroll
-    for (int r = 0; r < LG_R; ++r) acc[r] = 0.0f;
-    for (int64_t q = lane; q < K / 4; q += WAVE) {
-        float wv[4];
-        load4_f32<DT>(E, col, 4 * q, wv);
-#pragma unroll
-        for (int r = 0; r < LG_R; ++r) {
-            if (r < nr) {
-                const float4 x = *reinterpret_cast<const float4*>(rows + (r0 + r) * K + 4 * q);
-                acc[r] += x.x * wv[0] + x.y * wv[1] + x.z * wv[2] + x.w * wv[3];
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < LG_R; ++r) {
-        if (r >= nr) break;
-        float z = wave_sum(acc[r]);
-        if (lane == 0) {
-            if (softcap > 0.0f) z = softcap * tanhf(z / softcap);
-            out[(r0 + r) * ncols + j] = z;
-        }
-    }
-}
-
-// logits.wgsl:38-79's product, rows . deq(E[col])^T in f32 (no f16
-// rounding on this path, as in the reference).  A workgroup owns 64 output
-// columns (vocabulary rows of E, or the label ids in `cols`), one per lane;
-// its four waves split K by 32-element blocks (wave w takes blocks w, w + 4,
-// ...), each lane decoding its column's block once into registers and
-// multiplying it into up to LG_R readout rows, whose values are the same
-// for every lane (uniform loads, no LDS).  The four partial sums meet in
-// LDS and are added in wave order, so a column's value does not depend on
-// which columns share its workgroup: full rows, label columns and the
+// rounding on this path, as in the reference), on v_mfma_f32_16x16x4_f32.
+// A workgroup owns 64 output columns (vocabulary rows of E, or the label
+// ids in `cols`), 16 per wave, and up to LG_R = 16 readout rows at a time:
+// D[col][row] = sum_k E[col][k] x[row][k] with A = the decoded weights
+// (lane l: column l % 16) and B = the rows from LDS.  Inside a 32-element
+// block the K order is permuted alike in both operands: MFMA step s of
+// lane group G = l / 16 takes element 8 G + s, so a lane decodes one Q4
+// word (one Q8 pair, 16 bytes of f16) per block.  A column's sums do not
+// depend on which columns share its wave: full rows, label columns and the
 // log-sum-exp path give bit-equal logits.  With `part`, every workgroup
-// also writes each row's (max, sum of exp(z - max)) over its columns.
-constexpr int LG_R = 16;  // readout rows per pass over K
+// also writes each row's (max, sum of exp(z - max)) over its 64 columns.
+constexpr int LG_R = 16;     // readout rows per pass over K
+constexpr int LG_KC = 512;   // K elements of the rows staged in LDS at once
 
-// Block b of column `col` as 32 f32 weights, (q - 8) d / q d / f16 as f32.
+// Elements 8 g .. 8 g + 7 of block b of column `col`, f32.
 template <int DT>
-__device__ inline void logit_block(const DevWeight& E, int64_t col, int64_t b, float w[32]) {
+__device__ inline void logit_octet(const DevWeight& E, int64_t col, int64_t b, int g, float w[8]) {
     const int64_t K = E.cols;
     if constexpr (DT == Q4_DT) {
         const float d = half_bits_to_f32(E.scales[col * E.sld + b]);
-        const uint4 q = reinterpret_cast<const uint4*>(E.data)[col * (K / 32) + b];
-        const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+        const uint32_t word = static_cast<const uint32_t*>(E.data)[(col * (K / 32) + b) * 4 + g];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int p = 0; p < 8; ++p) w[8 * i + p] = q4_elem_f32(words[i], p, d);
+        for (int p = 0; p < 8; ++p) w[p] = q4_elem_f32(word, p, d);
     } else if constexpr (DT == Q8_DT) {
         const float d = half_bits_to_f32(E.scales[col * E.sld + b]);
-        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(E.data) + col * K + b * 32);
-        const uint4 u0 = src[0], u1 = src[1];
-        const uint32_t words[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(E.data) + col * K + b * 32 + 8 * g);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) w[4 * i + k] = float(int8_t(words[i] >> (8 * k))) * d;
+        for (int k = 0; k < 4; ++k) {
+            w[k] = float(int8_t(u.x >> (8 * k))) * d;
+            w[4 + k] = float(int8_t(u.y >> (8 * k))) * d;
+        }
     } else {
-        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const half_t*>(E.data) + col * K + b * 32);
+        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const half_t*>(E.data) + col * K + b * 32 + 8 * g);
+        const uint32_t words[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 u = src[i];
-            const uint32_t words[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const half2v h = as_half2(words[k]);
-                w[8 * i + 2 * k] = float(h.x);
-                w[8 * i + 2 * k + 1] = float(h.y);
-            }
+        for (int k = 0; k < 4; ++k) {
+            const half2v h = as_half2(words[k]);
+            w[2 * k] = float(h.x);
+            w[2 * k + 1] = float(h.y);
         }
     }
 }
@@ -621,46 +570,78 @@ template <int DT>
 __global__ __launch_bounds__(256) void logits_kernel(DevWeight E, const float* __restrict__ rows, int64_t nrows,
                                                      const uint32_t* __restrict__ cols, int64_t ncols, float softcap,
                                                      float* __restrict__ out, float2* __restrict__ part) {
-    __shared__ float red[4][LG_R][WAVE];
+    __shared__ __attribute__((aligned(16))) float xs[LG_R][LG_KC];
+    __shared__ float red[4][LG_R][2];
     const int tid = int(threadIdx.x), lane = tid % WAVE;
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
-    const int64_t j = int64_t(blockIdx.x) * WAVE + lane;
-    const bool live = j < ncols;
-    const int64_t col = live ? (cols ? int64_t(cols[j]) : j) : 0;  // idle lanes read row 0 and drop it
-    const int64_t K = E.cols, nb = K / 32;
+    const int lr = lane % 16, G = lane / 16;
+    // A operand: column wave * 16 + lr of the workgroup's 64
+    const int64_t ja = int64_t(blockIdx.x) * 64 + wave * 16 + lr;
+    const int64_t col = ja < ncols ? (cols ? int64_t(cols[ja]) : ja) : 0;  // idle columns read row 0, dropped
+    // D: columns wave * 16 + 4 G + r, row lr
+    const int64_t jd = int64_t(blockIdx.x) * 64 + wave * 16 + 4 * G;
+    const int64_t K = E.cols;
     for (int64_t r0 = 0; r0 < nrows; r0 += LG_R) {
         const int nr = int(nrows - r0 < LG_R ? nrows - r0 : LG_R);
-        float acc[LG_R];
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int64_t k0 = 0; k0 < K; k0 += LG_KC) {
+            const int kc = int(K - k0 < LG_KC ? K - k0 : LG_KC);
+            __syncthreads();  // the previous chunk's reads are done
+            for (int i = tid; i < LG_R * (kc / 4); i += 256) {
+                const int r = i / (kc / 4), c4 = i % (kc / 4);
+                const float4 v = r < nr ? *reinterpret_cast<const float4*>(rows + (r0 + r) * K + k0 + 4 * c4)
+                                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *reinterpret_cast<float4*>(&xs[r][4 * c4]) = v;
+            }
+            __syncthreads();
+            for (int bl = 0; bl < kc / 32; ++bl) {
+                float w[8];
+                logit_octet<DT>(E, col, k0 / 32 + bl, G, w);
+                const float4 x0 = *reinterpret_cast<const float4*>(&xs[lr][bl * 32 + 8 * G]);
+                const float4 x1 = *reinterpret_cast<const float4*>(&xs[lr][bl * 32 + 8 * G + 4]);
+                const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-        for (int r = 0; r < LG_R; ++r) acc[r] = 0.0f;
-        for (int64_t b = wave; b < nb; b += 4) {
-            float w[32];
-            logit_block<DT>(E, col, b, w);
-#pragma unroll
-            for (int r = 0; r < LG_R; ++r) {
-                if (r < nr) {  // uniform: the row group's tail skips its loads
-                    const float* x = rows + (r0 + r) * K + b * 32;
-#pragma unroll
-                    for (int k = 0; k < 32; ++k) acc[r] = __builtin_fmaf(w[k], x[k], acc[r]);
-                }
+                for (int st = 0; st < 8; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w[st], x[st], acc, 0, 0, 0);
             }
         }
+        // lane: row lr, columns jd .. jd + 3
+        const bool row_ok = lr < nr;
+        float z[4];
 #pragma unroll
-        for (int r = 0; r < LG_R; ++r) red[wave][r][lane] = acc[r];
-        __syncthreads();
-        if (wave == 0) {
-            for (int r = 0; r < nr; ++r) {
-                float z = ((red[0][r][lane] + red[1][r][lane]) + red[2][r][lane]) + red[3][r][lane];
-                if (softcap > 0.0f) z = softcap * tanhf(z / softcap);
-                if (live) out[(r0 + r) * ncols + j] = z;
-                if (part) {
-                    const float m = wave_max(live ? z : -INFINITY);
-                    const float e = wave_sum(live ? expf(z - m) : 0.0f);
-                    if (lane == 0) part[int64_t(blockIdx.x) * nrows + r0 + r] = make_float2(m, e);
-                }
+        for (int r = 0; r < 4; ++r) {
+            z[r] = acc[r];
+            if (softcap > 0.0f) z[r] = softcap * tanhf(z[r] / softcap);
+        }
+        if (row_ok) {
+            float* dst = out + (r0 + lr) * ncols + jd;
+            if (jd + 3 < ncols) {
+                *reinterpret_cast<float4*>(dst) = make_float4(z[0], z[1], z[2], z[3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (jd + r < ncols) dst[r] = z[r];
             }
         }
-        __syncthreads();
+        if (part) {
+            // per row: max and sum of exp over the workgroup's 64 columns,
+            // lanes (row, G) then waves in a fixed order
+            float m = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m = fmaxf(m, jd + r < ncols ? z[r] : -INFINITY);
+            m = max_lanes_16_32(m);
+            if (G == 0) red[wave][lr][0] = m;
+            __syncthreads();
+            m = fmaxf(fmaxf(red[0][lr][0], red[1][lr][0]), fmaxf(red[2][lr][0], red[3][lr][0]));
+            float e = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) e += jd + r < ncols ? expf(z[r] - m) : 0.0f;
+            e = sum_lanes_16_32(e);
+            if (G == 0) red[wave][lr][1] = e;
+            __syncthreads();
+            if (wave == 0 && G == 0 && row_ok)
+                part[int64_t(blockIdx.x) * nrows + r0 + lr] =
+                    make_float2(m, ((red[0][lr][1] + red[1][lr][1]) + red[2][lr][1]) + red[3][lr][1]);
+        }
     }
 }
 
