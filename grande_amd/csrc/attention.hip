@@ -35,6 +35,7 @@
 #include <algorithm>
 #include <climits>
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 #include "kern_common.h"
@@ -100,16 +101,20 @@ struct TileDma {
     static constexpr int VINS = (HD / attn_col_splits<HD>()) * A_KT / 8 / WAVE / A_NW;
 };
 
-// exp2(s log2(e) - m) for a whole-number m, as 2^frac(x) * 2^(floor(x) - m)
-// with x = s log2(e): the fraction and the exponent depend on the score
-// alone, so a probability taken against another whole-number max differs by
-// an exact power of two, and so does its f16 rounding (above f16's
-// subnormals).  Masked scores (-inf) give 0.
-__device__ inline float prob(float s, float m) {
+// exp2(s log2(e) - m) for a whole-number m (as the integer mi), as
+// 2^frac(x) * 2^(floor(x) - m) with x = s log2(e): the fraction and the
+// exponent depend on the score alone, so a probability taken against
+// another whole-number max differs by an exact power of two, and so does
+// its f16 rounding (above f16's subnormals).  With MASKED, scores may be
+// -inf (masked keys) and give 0; without, every score is finite.
+template <bool MASKED>
+__device__ inline float prob(float s, int mi) {
     constexpr float LOG2E = 1.4426950408889634f;
-    const float x = fmaxf(s * LOG2E, -16384.0f);
-    const float xi = floorf(x);
-    return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(x - xi), int(xi - m));
+    float x = s * LOG2E;
+    if constexpr (MASKED) x = fmaxf(x, -16384.0f);
+    int xi;  // floor(x) as an integer in one instruction
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(xi) : "v"(x));
+    return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(__builtin_amdgcn_fractf(x)), xi - mi);
 }
 
 // One work item per workgroup: A_ROWS query rows (TPW tokens x HPG heads
@@ -132,6 +137,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 
     const int4 item = items[blockIdx.x];
     const int qtile = item.x, tb = item.y, te = item.z, slot = item.w;
+    if (qtile < 0) return;  // padding of the launch order
     const int tid = int(threadIdx.x), lane = tid % WAVE;
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
     const int H = a.heads;
@@ -354,20 +360,28 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
             alpha[b] = grow ? __builtin_amdgcn_exp2f(m_run[b] - m_use) : 1.0f;
             // A row that had seen nothing still holds O = 0: no rescale.
             any_rescale = any_rescale || (grow && m_run[b] != -INFINITY);
+            const int mi = int(m_use);
             float psum = 0.0f;
+            auto probs = [&](auto masked) {
+                constexpr bool MK = decltype(masked)::value;
 #pragma unroll
-            for (int j = 0; j < A_KB; ++j) {
-                half2v pr[2];
+                for (int j = 0; j < A_KB; ++j) {
+                    half2v pr[2];
 #pragma unroll
-                for (int r = 0; r < 4; r += 2) {
-                    pr[r / 2] = half2v{half_t(prob(sacc[b][j][r], m_use)), half_t(prob(sacc[b][j][r + 1], m_use))};
-                    psum = __builtin_amdgcn_fdot2(pr[r / 2], half2v{half_t(1.0f), half_t(1.0f)}, psum, false);
+                    for (int r = 0; r < 4; r += 2) {
+                        pr[r / 2] = half2v{half_t(prob<MK>(sacc[b][j][r], mi)), half_t(prob<MK>(sacc[b][j][r + 1], mi))};
+                        psum = __builtin_amdgcn_fdot2(pr[r / 2], half2v{half_t(1.0f), half_t(1.0f)}, psum, false);
+                    }
+                    pb[b][j / 2][(j % 2) * 4 + 0] = pr[0].x;
+                    pb[b][j / 2][(j % 2) * 4 + 1] = pr[0].y;
+                    pb[b][j / 2][(j % 2) * 4 + 2] = pr[1].x;
+                    pb[b][j / 2][(j % 2) * 4 + 3] = pr[1].y;
                 }
-                pb[b][j / 2][(j % 2) * 4 + 0] = pr[0].x;
-                pb[b][j / 2][(j % 2) * 4 + 1] = pr[0].y;
-                pb[b][j / 2][(j % 2) * 4 + 2] = pr[1].x;
-                pb[b][j / 2][(j % 2) * 4 + 3] = pr[1].y;
-            }
+            };
+            if (full)
+                probs(std::false_type{});
+            else
+                probs(std::true_type{});
             l_run[b] = l_run[b] * alpha[b] + psum;
             m_run[b] = m_new;
         }
@@ -583,12 +597,36 @@ void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int
         w.merges.push_back({int(qt), first, slot - first, 0});
     }
     w.slots = slot;
-    // Longest items first: the workgroup dispatcher places one workgroup
-    // per CU before it doubles up, so the long items each start on a CU of
-    // their own and the short ones share.  (The result does not depend on
-    // the order.)
-    std::stable_sort(w.items.begin(), w.items.end(),
-                     [](const int4& x, const int4& y) { return x.z - x.y > y.z - y.y; });
+    // Launch order.  Workgroup b runs on XCD b % 8, and each XCD has its
+    // own L2: XCD x gets the x-th of eight contiguous runs of query tiles
+    // (cut at equal work, a tile counting one and an item's start about
+    // two and a half, its first loads' latency), so the key tiles its
+    // items read are mostly the same few and stay in its L2.  Inside a
+    // run, longest items first: the dispatcher places one workgroup per CU
+    // before it doubles up, so the long items each start on a CU of their
+    // own.  Runs are padded to one length with no-op items (query tile -1),
+    // which keeps b % 8 the XCD for every blockIdx.y too.  (The result does
+    // not depend on the order.)
+    constexpr int NXCD = 8;
+    constexpr double START = 2.5;
+    double total = 0.0;
+    for (const int4& it : w.items) total += START + (it.z - it.y);
+    std::vector<std::vector<int4>> runs(NXCD);
+    double acc = 0.0;
+    for (const int4& it : w.items) {
+        const double wgt = START + (it.z - it.y);
+        const int x = std::min(NXCD - 1, int((acc + 0.5 * wgt) * NXCD / total));
+        runs[size_t(x)].push_back(it);
+        acc += wgt;
+    }
+    size_t len = 0;
+    for (auto& r : runs) {
+        std::stable_sort(r.begin(), r.end(), [](const int4& x, const int4& y) { return x.z - x.y > y.z - y.y; });
+        len = std::max(len, r.size());
+    }
+    w.items.assign(len * NXCD, int4{-1, 0, 0, -1});
+    for (int x = 0; x < NXCD; ++x)
+        for (size_t i = 0; i < runs[size_t(x)].size(); ++i) w.items[i * NXCD + size_t(x)] = runs[size_t(x)][i];
 }
 
 template <int HD, int HPG>
