@@ -402,6 +402,38 @@ def test_label_lse_readout():
                 assert np.max(np.abs(oracle.softmax(got[:-1]) - probs)) < 2e-2
 
 
+def test_logits_many_rows_and_wide_rows():
+    """The logits kernel's edges: more readout rows than one pass of the
+    kernel takes (44 rows: three passes of 16), a model width spanning two
+    staged K chunks (d 576 = 512 + 64) and a vocabulary that ends inside a
+    workgroup's 64 columns (300).  Every row against the oracle's logits
+    of the engine's own hidden rows (reference.rs:564-598's 1e-3 of the
+    scale); label columns and LABELS_LSE's columns bit-equal to the full
+    row; the log-sum-exp within 1e-5 of the float64 one."""
+    cfg = gemma3_tiny(d=576, vocab=300)
+    eng, plain, _, w = build(cfg, 12, g.F16, g.F16, max_rows=48)
+    rng = np.random.default_rng(3)
+    prefix = rng.integers(0, 300, 9).tolist()
+    branches = [BranchTokens(rng.integers(0, 300, n).tolist(), list(range(n))) for n in (12, 15, 17)]
+    hid = eng.evaluate(prefix, branches, Want.HIDDEN)
+    full = eng.evaluate(prefix, branches, Want.LOGITS)
+    labels = [0, 299, 64, 63, 7, 128, 250]
+    lab = eng.evaluate(prefix, branches, Want.LABELS, labels)
+    lse = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
+    nrows = 0
+    for ho, fo, la, lo in zip(hid, full, lab, lse):
+        for h, row, lr, ls in zip(ho.rows, fo.rows, la.rows, lo.rows):
+            nrows += 1
+            exp = plain.logits(np.asarray(h)[None, :])[0]
+            assert np.max(np.abs(row - exp)) <= 1e-3 * max(float(np.max(np.abs(exp))), 1.0)
+            assert np.array_equal(lr, row[labels]) and np.array_equal(ls[:-1], row[labels])
+            r64 = row.astype(np.float64)
+            m = r64.max()
+            exp_lse = m + np.log(np.exp(r64 - m).sum())
+            assert abs(ls[-1] - exp_lse) <= 1e-5 * max(1.0, abs(exp_lse))
+    assert nrows == 44
+
+
 def test_refused_request_leaves_resident_prefix_intact():
     """A request refused for a bad label id changes nothing on the device: a
     later pass over the resident prefix equals a fresh pass.  A prepared
