@@ -241,21 +241,22 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
 
     // Issue stage s's DMA into its ring slot.  The stage's K offset rides in
     // the scalar offset, so the lane offsets stay fixed; only the K-tail
-    // stage (K % 64 == 32) masks X lanes per lane.  Stages past the end use
-    // empty resources (every lane out of range), so every wave always
-    // issues P::C instructions per stage.
-    auto slot_base = [&](int s) { return smem + (s % NS) * P::STAGE; };
+    // stage (K % 64 == 32) masks X lanes per lane.  Stages past the end
+    // repeat the last one (in range, never consumed), so every wave always
+    // issues P::C instructions per stage and the resources do not change.
+    auto slot_base = [&](int s) { return smem + (unsigned(s) % unsigned(NS)) * P::STAGE; };
+    const int last = nk - 1;
+    const int64_t xbytes = rows_m * g.ldx * 2;
+    const bool ktail = (K32 & (G_BK - 1)) != 0;
     auto issue = [&](int s) {
         uint8_t* base = slot_base(s);
-        const bool live = s < nk;
-        const int k0 = kbeg + s * G_BK;
-        const int64_t xbytes = live ? rows_m * g.ldx * 2 : 0;
+        const int k0 = __builtin_amdgcn_readfirstlane(kbeg + (s < last ? s : last) * G_BK);
         // (Range checks cover the lane offset only: a row's offset plus the
         // stage offset stays inside the row, and rows past M are out of
         // range by their lane offset.  Each resource is a named value built
         // at its use: passed inline, or held across branches, it is not
         // accepted by the host-side compile of this kernel.)
-        const bool tail = k0 + G_BK > K32;
+        const bool tail = ktail && k0 + G_BK > K32;
 #pragma unroll
         for (int i = 0; i < P::X_I; ++i) {
             const uint32_t o = tail && xcol[i] >= K32 - k0 ? OOB : xoff[i];
@@ -269,13 +270,13 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < P::W_I; ++i) {
             const uint32_t o = tail ? wtail[i] : woff[i];
-            const __amdgpu_buffer_rsrc_t r = rsrc(wup[i] ? wbase1 : wbase0, live ? rows_n * wrow : 0);
+            const __amdgpu_buffer_rsrc_t r = rsrc(wup[i] ? wbase1 : wbase0, rows_n * wrow);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(base + P::X_BYTES + (i * NW + wave) * WAVE * 16),
                                                      16, o, wstep, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < P::S_I; ++i) {
-            const __amdgpu_buffer_rsrc_t r = rsrc(sup[i] ? sbase1 : sbase0, live ? sbytes : 0);
+            const __amdgpu_buffer_rsrc_t r = rsrc(sup[i] ? sbase1 : sbase0, sbytes);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 r, (lds_ptr_t)(base + P::X_BYTES + P::W_BYTES + (i * NW + wave) * WAVE * 4), 4, soff[i], k0 / 16, 0, 0);
         }
@@ -589,15 +590,18 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         scoff[j] = blk_of(j) < live_blocks ? uint32_t(blk_of(j) * stages * TILE_SCALE_BYTES + (lane % 32) * 4) : OOB;
     }
 
-    auto slot_base = [&](int s) { return smem + (s % NS) * P::X_BYTES; };
-    // X tile of stage s into its ring slot (only the K-tail stage, K % 64 ==
-    // 32, masks lanes; past the end the resource is empty).
+    // Stages past the end repeat the last one (in range, never consumed),
+    // so the resources and lane offsets stay the same for every stage and
+    // only the scalar stage offset moves.
+    auto slot_base = [&](int s) { return smem + (unsigned(s) % unsigned(NS)) * P::X_BYTES; };
+    const int last = nk - 1;
+    const int64_t xbytes = M * g.ldx * 2;
+    const bool ktail = (K32 & (G_BK - 1)) != 0;  // K % 64 == 32: the last stage masks lanes
+    // X tile of stage s into its ring slot.
     auto issue_x = [&](int s) {
         uint8_t* base = slot_base(s);
-        const bool live = s < nk;
-        const int k0 = __builtin_amdgcn_readfirstlane(kbeg + s * G_BK);  // uniform: a scalar offset
-        const int64_t xbytes = live ? M * g.ldx * 2 : 0;
-        const bool tail = k0 + G_BK > K32;
+        const int k0 = __builtin_amdgcn_readfirstlane(kbeg + (s < last ? s : last) * G_BK);  // a scalar offset
+        const bool tail = ktail && k0 + G_BK > K32;
 #pragma unroll
         for (int i = 0; i < P::X_I; ++i) {
             const uint32_t o = tail && xcol[i] >= K32 - k0 ? OOB : xoff[i];
@@ -612,20 +616,20 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         uint4 code[NJ][P::CL];
         uint32_t sc[NJ];
     };
+    const int st0 = kbeg / G_BK;  // this split's first stage
     auto issue_w = [&](int s, WRegs& w) {
-        const bool live = s < nk;
-        const int st = __builtin_amdgcn_readfirstlane((kbeg + s * G_BK) / G_BK);
+        const int st = __builtin_amdgcn_readfirstlane(st0 + (s < last ? s : last));
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const DevWeight& wt = mat_of(j) ? g.w1 : g.w0;
-            const __amdgpu_buffer_rsrc_t r = rsrc(wt.tiles + rb0 * stages * PK, live ? live_blocks * stages * PK : 0);
+            const __amdgpu_buffer_rsrc_t r = rsrc(wt.tiles + rb0 * stages * PK, live_blocks * stages * PK);
 #pragma unroll
             for (int c = 0; c < P::CL; ++c)
                 w.code[j][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                              r, coff[j] + 16 * c, st * PK, 0));
             if constexpr (QUANT != F16_DT) {
                 const __amdgpu_buffer_rsrc_t rs = rsrc(wt.tscales + rb0 * stages * TILE_SCALE_BYTES,
-                                                       live ? live_blocks * stages * TILE_SCALE_BYTES : 0);
+                                                       live_blocks * stages * TILE_SCALE_BYTES);
                 w.sc[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, scoff[j], st * TILE_SCALE_BYTES, 0);
             }
         }
