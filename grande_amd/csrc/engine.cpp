@@ -231,7 +231,6 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
         }
         OMG_HIP(hipStreamSynchronize(E.stream_));
     }
-    E.ids_ = DevBuf(size_t(cap) * 4);
     E.meta_ = DevBuf(size_t(E.cap_pad_) * 16, true);
     E.x_ = DevBuf(size_t(cap * d) * 4);
     E.hn_ = DevBuf(size_t(cap * d) * 2);
@@ -244,8 +243,6 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.rows_ = DevBuf(size_t(max_rows * d) * 4);
     const int64_t width = std::max(c.vocab, d);
     E.logits_ = DevBuf(size_t(max_rows * width) * 4);
-    E.wanted_ = DevBuf(size_t(max_rows) * 4);
-    E.labels_ = DevBuf(size_t(c.vocab) * 4);
     E.label_lse_ = DevBuf(size_t(max_rows * (c.vocab + 1)) * 4);
     E.lse_part_ = DevBuf(size_t(logits_blocks(c.vocab) * max_rows) * 8);
     E.kv_stage_ = DevBuf(size_t(E.cap_pad_ * 2 * c.kv_heads * hd) * 2);
@@ -268,12 +265,11 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
         const int64_t qtiles = (cap + tpb - 1) / tpb;
         E.attn_chunk_[0] = int(256 / kt);
         E.attn_chunk_[1] = int(std::max<int64_t>(512 / kt, (key_tiles + 7) / 8));
-        // Work lists and chunk partials start sized for a few chunks per
-        // query tile and grow with the passes that need more (upload).
-        for (int k = 0; k < 2; ++k) {
-            E.attn_items_[k] = DevBuf(size_t(qtiles * 4) * 16);
-            E.attn_merges_[k] = DevBuf(size_t(qtiles) * 16);
-        }
+        // The pass inputs (ids, wanted rows, labels, both layer types'
+        // work lists) and the chunk partials start sized for a few chunks
+        // per query tile and grow with the passes that need more (upload).
+        E.in_bytes_ = size_t(cap) * 4 + size_t(max_rows) * 4 + size_t(c.vocab) * 4 + size_t(qtiles * 5) * 16 * 2 + 64;
+        E.in_ = DevBuf(E.in_bytes_);
         E.part_slots_ = qtiles * 4;
         E.part_o_ = DevBuf(size_t(E.part_slots_ * c.kv_heads * attention_rows()) * size_t(hd) * 2);
         E.part_ml_ = DevBuf(size_t(E.part_slots_ * c.kv_heads * attention_rows()) * 2 * 4);
@@ -291,7 +287,7 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
             E.vt_.emplace_back();
         }
     }
-    E.h_in_bytes_ = size_t(cap) * 4 + size_t(cap) * 16 + size_t(max_rows) * 4 + size_t(c.vocab) * 4;
+    E.h_in_bytes_ = size_t(cap) * 16 + E.in_bytes_;
     OMG_HIP(hipHostMalloc(&E.h_in_, E.h_in_bytes_, hipHostMallocDefault));
     E.h_out_bytes_ = size_t(max_rows * (width + 1)) * 4;  // + 1: the log-sum-exp after vocab labels
     OMG_HIP(hipHostMalloc(&E.h_out_, E.h_out_bytes_, hipHostMallocDefault));
@@ -441,28 +437,43 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     if (resident_ && int64_t(resident_->size()) > pk.base) resident_.reset();
     // A captured pass reads the work lists and buffers this upload may move.
     drop_graph();
-    uint8_t* h = static_cast<uint8_t*>(h_in_);
-    // The previous pass may still read the staging buffer.
-    OMG_HIP(hipStreamSynchronize(stream_));
-    size_t off = 0;
-    std::memcpy(h + off, pk.ids.data(), size_t(t) * 4);
-    OMG_HIP(hipMemcpyAsync(ids_.p, h + off, size_t(t) * 4, hipMemcpyHostToDevice, stream_));
-    off += size_t(slots_) * 4;
-    std::memcpy(h + off, pk.meta.data(), size_t(t) * 16);
-    OMG_HIP(hipMemcpyAsync(meta_.as<uint8_t>() + pk.base * 16, h + off, size_t(t) * 16, hipMemcpyHostToDevice, stream_));
-    off += size_t(slots_) * 16;
-    int32_t* w = reinterpret_cast<int32_t*>(h + off);
-    for (int64_t r = 0; r < nr; ++r) w[r] = int32_t(pk.wanted[size_t(r)][3]);
-    if (nr) OMG_HIP(hipMemcpyAsync(wanted_.p, w, size_t(nr) * 4, hipMemcpyHostToDevice, stream_));
-    off += size_t(max_rows_) * 4;
-    // Attention work lists for both layer types.
-    for (int kind = 0; kind < 2; ++kind) {
-        AttnWork w;
+    // Attention work lists for both layer types (host only).
+    for (int kind = 0; kind < 2; ++kind)
         attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), kind == 0 ? int(cfg_.window) : 0,
-                       attn_chunk_[kind], w);
-        // The stream is idle here (synchronised above): buffers can grow.
-        if (w.items.size() * 16 > attn_items_[kind].bytes) attn_items_[kind] = DevBuf(w.items.size() * 16);
-        if (w.merges.size() * 16 > attn_merges_[kind].bytes) attn_merges_[kind] = DevBuf(w.merges.size() * 16);
+                       attn_chunk_[kind], work_[kind]);
+    // The pass's inputs go to the device in two copies: the cache metadata
+    // of its rows, and one block [ids | wanted rows | labels | per layer
+    // type: work items, merges] (16-byte aligned parts).
+    auto a16 = [](size_t n) { return (n + 15) / 16 * 16; };
+    size_t in_bytes = 0;
+    auto part = [&](size_t n) {
+        const size_t o = in_bytes;
+        in_bytes += a16(n);
+        return o;
+    };
+    const size_t o_ids = part(size_t(t) * 4), o_wanted = part(size_t(nr) * 4), o_labels = part(size_t(nlabels) * 4);
+    size_t o_items[2], o_merges[2];
+    for (int kind = 0; kind < 2; ++kind) {
+        o_items[kind] = part(work_[kind].items.size() * 16);
+        o_merges[kind] = part(work_[kind].merges.size() * 16);
+    }
+    const size_t meta_bytes = a16(size_t(t) * 16);
+    // The previous pass may still read the staging buffer; from here the
+    // stream is idle, so buffers can grow.
+    OMG_HIP(hipStreamSynchronize(stream_));
+    if (meta_bytes + in_bytes > h_in_bytes_) {
+        OMG_HIP(hipHostFree(h_in_));
+        h_in_ = nullptr;
+        h_in_bytes_ = 0;
+        OMG_HIP(hipHostMalloc(&h_in_, (meta_bytes + in_bytes) * 2, hipHostMallocDefault));
+        h_in_bytes_ = (meta_bytes + in_bytes) * 2;
+    }
+    if (in_bytes > in_bytes_) {
+        in_ = DevBuf(in_bytes * 2);
+        in_bytes_ = in_bytes * 2;
+    }
+    for (int kind = 0; kind < 2; ++kind) {
+        const AttnWork& w = work_[kind];
         if (w.slots > part_slots_) {
             part_slots_ = w.slots;
             const size_t rows = size_t(part_slots_ * cfg_.kv_heads * attention_rows());
@@ -471,14 +482,28 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         }
         n_items_[kind] = int64_t(w.items.size());
         n_merges_[kind] = int64_t(w.merges.size());
-        if (!w.items.empty())
-            OMG_HIP(hipMemcpy(attn_items_[kind].p, w.items.data(), w.items.size() * 16, hipMemcpyHostToDevice));
-        if (!w.merges.empty())
-            OMG_HIP(hipMemcpy(attn_merges_[kind].p, w.merges.data(), w.merges.size() * 16, hipMemcpyHostToDevice));
     }
-    if (nlabels > 0) {
-        std::memcpy(h + off, labels, size_t(nlabels) * 4);
-        OMG_HIP(hipMemcpyAsync(labels_.p, h + off, size_t(nlabels) * 4, hipMemcpyHostToDevice, stream_));
+    uint8_t* h = static_cast<uint8_t*>(h_in_);
+    std::memcpy(h, pk.meta.data(), size_t(t) * 16);
+    uint8_t* hb = h + meta_bytes;
+    std::memcpy(hb + o_ids, pk.ids.data(), size_t(t) * 4);
+    int32_t* w = reinterpret_cast<int32_t*>(hb + o_wanted);
+    for (int64_t r = 0; r < nr; ++r) w[r] = int32_t(pk.wanted[size_t(r)][3]);
+    if (nlabels > 0) std::memcpy(hb + o_labels, labels, size_t(nlabels) * 4);
+    for (int kind = 0; kind < 2; ++kind) {
+        const AttnWork& wk = work_[kind];
+        if (!wk.items.empty()) std::memcpy(hb + o_items[kind], wk.items.data(), wk.items.size() * 16);
+        if (!wk.merges.empty()) std::memcpy(hb + o_merges[kind], wk.merges.data(), wk.merges.size() * 16);
+    }
+    OMG_HIP(hipMemcpyAsync(meta_.as<uint8_t>() + pk.base * 16, h, size_t(t) * 16, hipMemcpyHostToDevice, stream_));
+    OMG_HIP(hipMemcpyAsync(in_.p, hb, in_bytes, hipMemcpyHostToDevice, stream_));
+    uint8_t* d = in_.as<uint8_t>();
+    d_ids_ = reinterpret_cast<const uint32_t*>(d + o_ids);
+    d_wanted_ = reinterpret_cast<const int32_t*>(d + o_wanted);
+    d_labels_ = reinterpret_cast<const uint32_t*>(d + o_labels);
+    for (int kind = 0; kind < 2; ++kind) {
+        d_items_[kind] = reinterpret_cast<const int4*>(d + o_items[kind]);
+        d_merges_[kind] = reinterpret_cast<const int4*>(d + o_merges[kind]);
     }
 }
 
@@ -507,7 +532,7 @@ void Engine::forward(int64_t t, int64_t base) {
     const Config& c = cfg_;
     const int64_t d = c.d;
     step("embed_norm", [&] {
-        launch_embed_norm(stream_, embed_.w, ids_.as<uint32_t>(), t, std::sqrt(float(d)),
+        launch_embed_norm(stream_, embed_.w, d_ids_, t, std::sqrt(float(d)),
                           layers_[0].attn_norm.as<float>(), c.eps, x_.as<float>(), hn_.as<half_t>());
     });
     const int64_t P = c.per_layer_dim;
@@ -518,7 +543,7 @@ void Engine::forward(int64_t t, int64_t base) {
             launch_gemm(stream_, x16_.as<half_t>(), d, pl_model_proj_.w, pli_.as<float>(), P * c.layers, t);
         });
         step("pl_combine", [&] {
-            launch_pl_combine(stream_, pl_table_.w, ids_.as<uint32_t>(), pl_proj_norm_.as<float>(), pli_.as<float>(),
+            launch_pl_combine(stream_, pl_table_.w, d_ids_, pl_proj_norm_.as<float>(), pli_.as<float>(),
                               t, P, c.layers, c.eps, 1.0f / std::sqrt(float(d)), std::sqrt(float(P)),
                               1.0f / std::sqrt(2.0f));
         });
@@ -572,10 +597,10 @@ void Engine::forward(int64_t t, int64_t base) {
         att.part_o = part_o_.as<half_t>();
         att.part_ml = part_ml_.as<float>();
         const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
-        step("attention", [&] { launch_attention(stream_, att, attn_items_[kind].as<int4>(), n_items_[kind]); });
+        step("attention", [&] { launch_attention(stream_, att, d_items_[kind], n_items_[kind]); });
         if (n_merges_[kind] > 0)
             step("attention_merge",
-                 [&] { launch_attention_merge(stream_, att, attn_merges_[kind].as<int4>(), n_merges_[kind]); });
+                 [&] { launch_attention_merge(stream_, att, d_merges_[kind], n_merges_[kind]); });
         const int so = ksplit(c.heads * hd, d), sd = ksplit(ff, d);
         const int64_t pstride = slots_ * d;
         step("mm_o", [&] {
@@ -623,7 +648,7 @@ void Engine::readout(const PassPlan& p) {
     if (p.nrows == 0) return;
     const Config& c = cfg_;
     step("final_rows", [&] {
-        launch_final_rows(stream_, x_.as<float>(), wanted_.as<int32_t>(), p.nrows, c.d, final_norm_.as<float>(),
+        launch_final_rows(stream_, x_.as<float>(), d_wanted_, p.nrows, c.d, final_norm_.as<float>(),
                           c.eps, rows_.as<float>());
     });
     if (p.want == WANT_LOGITS) {
@@ -633,7 +658,7 @@ void Engine::readout(const PassPlan& p) {
         });
     } else if (p.want == WANT_LABELS) {
         step("logits", [&] {
-            launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, labels_.as<uint32_t>(), p.nlabels,
+            launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, d_labels_, p.nlabels,
                           c.softcap, logits_.as<float>());
         });
     } else if (p.want == WANT_LABELS_LSE) {
@@ -646,7 +671,7 @@ void Engine::readout(const PassPlan& p) {
         });
         step("label_lse", [&] {
             launch_label_lse(stream_, logits_.as<float>(), p.nrows, c.vocab, lse_part_.as<float2>(),
-                             logits_blocks(c.vocab), labels_.as<uint32_t>(), p.nlabels, label_lse_.as<float>());
+                             logits_blocks(c.vocab), d_labels_, p.nlabels, label_lse_.as<float>());
         });
     }
 }

@@ -168,15 +168,24 @@ class Engine {
     std::vector<int> rope_of_;
     int64_t rope_rows_ = 0;
     // workspace
-    DevBuf ids_, meta_, x_, hn_, qkv_, q16_, attn_, a_, act_, rows_, logits_, wanted_, labels_, kv_stage_;
+    DevBuf meta_, x_, hn_, qkv_, q16_, attn_, a_, act_, rows_, logits_, kv_stage_;
+    // the pass's inputs in one block (upload): token ids, wanted rows, label ids, work lists
+    DevBuf in_;
+    size_t in_bytes_ = 0;
+    const uint32_t* d_ids_ = nullptr;
+    const int32_t* d_wanted_ = nullptr;
+    const uint32_t* d_labels_ = nullptr;
+    const int4* d_items_[2] = {nullptr, nullptr};
+    const int4* d_merges_[2] = {nullptr, nullptr};
     // Label logits + full-row log-sum-exp per wanted row (WANT_LABELS_LSE),
     // and the logits kernel's per-workgroup (max, sum of exp) pairs.
     DevBuf label_lse_, lse_part_;
     DevBuf x16_, pli_, plg_, pl16_;  // per-layer inputs: f16(x), [t][layers x P] f32, gate f32, gated f16
     // attention work lists of the current pass: [0] sliding layers, [1] global
     int attn_chunk_[2] = {0, 0};
-    DevBuf attn_items_[2], attn_merges_[2], part_o_, part_ml_;
+    DevBuf part_o_, part_ml_;
     int64_t n_items_[2] = {0, 0}, n_merges_[2] = {0, 0};
+    AttnWork work_[2];  // host side of the lists (capacity reused from pass to pass)
     int64_t part_slots_ = 0;  // chunk partial slots part_o_ / part_ml_ hold
     std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
     // pinned host staging
