@@ -12,7 +12,9 @@ captured once into a HIP graph; `value` takes the faster, both are
 reported under `launch`.  A step is one cold pass (state + branches, T = 2,384) with
 the token ids and metadata already in HBM; the warm pass (branches only on
 the resident state, T = 384) and the API wall times (host upload and
-readback included) are reported beside it.
+readback included: `api_ms` cold / warm are medians of the C ABI call on
+arguments marshalled once, `python_*` one call through the Python
+wrapper) are reported beside it.
 
 `--config c4` measures BASELINE.json configs[3] instead: the Laya encoder
 path over 192 sequences of 256 tokens (see bench_encoder).  `--config e2b`
@@ -134,6 +136,36 @@ def profiled_traffic(config: str, kernel: str):
     return None
 
 
+def c_api_ms(eng, groups, labels, reps: int = 15) -> dict:
+    """Medians of the C ABI's omg_evaluate_groups on arguments marshalled
+    once (what a compiled caller pays: host ids in, label logits and the
+    log-sum-exp out, synchronised): cold with the resident prefix evicted
+    first, warm on the resident state."""
+    import ctypes as C
+    from grande_amd import Want, _lib as L
+    from grande_amd.engine import _CGroups, _u32
+    cg, lab = _CGroups(groups), _u32(labels)
+    rows = sum(len(b.want) for gr in groups for b in gr.branches)
+    out = np.zeros((rows, lab.size + 1), np.float32)
+    src = (C.c_int * len(groups))()
+    lib = L.lib()
+
+    def call() -> float:
+        t = time.perf_counter()
+        L.check(lib.omg_evaluate_groups(eng._h, cg.arr, cg.n, int(Want.LABELS_LSE),
+                                        lab.ctypes.data_as(C.POINTER(C.c_uint32)), lab.size,
+                                        out.ctypes.data_as(C.POINTER(C.c_float)), out.size, src))
+        return time.perf_counter() - t
+
+    cold, warm = [], []
+    for _ in range(reps):
+        eng.evict_resident()
+        cold.append(call())
+        warm.append(call())
+    return {"cold": round(float(np.median(cold)) * 1e3, 3), "warm": round(float(np.median(warm)) * 1e3, 3),
+            "reps": reps, "calls": "C ABI, arguments marshalled once"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,6 +234,7 @@ def main() -> int:
     warm_rows = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     api_warm_ms = (time.perf_counter() - t) * 1e3
     assert eng.prefix_source() == g.PrefixSource.RESIDENT
+    c_api = c_api_ms(eng, [Group(prefix, branches)], labels)
     # (one untimed save and restore first: their first calls load the
     # gather / scatter kernels and touch the pinned staging pages)
     eng.restore_state(eng.save_state(prefix, "bench"), "bench")
@@ -341,7 +374,8 @@ def main() -> int:
         "warm_ms": round(warm_s * 1e3, 4),
         "warm_questions_per_s": round(NB / warm_s, 2),
         "warm_tok_per_s": round(NB * BT / warm_s, 1),
-        "api_ms": {"cold": round(api_cold_ms, 3), "warm": round(api_warm_ms, 3), "state_save": round(save_ms, 3),
+        "api_ms": {**c_api, "python_cold": round(api_cold_ms, 3), "python_warm": round(api_warm_ms, 3),
+                   "state_save": round(save_ms, 3),
                    "state_restore": round(restore_ms, 3), "state_bytes": len(state)},
         "restored_bit_equal": bool(restored_equal),
         "warm_vs_cold_max_abs_logit": warm_equal_cold,

@@ -401,37 +401,47 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
                     o[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[tt][c], pb[b][tt], o[b][c], 0, 0, 0);
     }
 
+    // The output goes out through LDS: each wave stages a 16-row block row
+    // by row (rows padded by 16 bytes), then writes each row's VD columns
+    // as whole 16-byte chunks, two rows per store instruction (lanes 0-31
+    // one row, 32-63 the next), instead of 32-byte pieces of 16 rows.  The
+    // K / V buffers hold the staging: every wave is past its last read of
+    // them, and no tile load is in flight after the loop.
+    static_assert(VD == 256, "32 lanes per staged row");
+    constexpr int SROW = VD + 8;  // staged row, halves
+    static_assert(A_NW * 16 * SROW * 2 <= int(sizeof(SM)), "staging fits the tile buffers");
+    __syncthreads();
+    half_t* stage = reinterpret_cast<half_t*>(smem_raw) + wave * 16 * SROW;
 #pragma unroll
     for (int b = 0; b < QB; ++b) {
         float l = l_run[b] + __shfl_xor(l_run[b], 16, WAVE);
         l += __shfl_xor(l, 32, WAVE);
-        const int row = (wave * QB + b) * 16 + lr;
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        if (slot >= 0) {
-            // Partial result of this chunk: O / l rounded to f16 exactly as
-            // an unsplit tile's output, and the chunk's max and sum.
-            const int64_t prow = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row;
-            half_t* op = a.part_o + prow * HD + ch * VD + G * 4;
+        // O / l rounded to f16; a split item's partial is rounded exactly
+        // as an unsplit tile's output.
 #pragma unroll
-            for (int c = 0; c < CT; ++c) {
-                const half4 v = {half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
-                                 half_t(o[b][c][3] * inv)};
-                *reinterpret_cast<half4*>(op + c * 16) = v;
-            }
-            if (G == 0 && ch == 0) {
-                a.part_ml[prow * 2] = m_run[b];
-                a.part_ml[prow * 2 + 1] = l;
-            }
-            continue;
+        for (int c = 0; c < CT; ++c)
+            *reinterpret_cast<half4*>(stage + lr * SROW + c * 16 + G * 4) =
+                half4{half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
+                      half_t(o[b][c][3] * inv)};
+        const int row0 = (wave * QB + b) * 16;  // the block's first row of the item
+        const int64_t prow0 = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row0;
+        if (slot >= 0 && G == 0 && ch == 0) {
+            // the chunk's max and sum
+            a.part_ml[(prow0 + lr) * 2] = m_run[b];
+            a.part_ml[(prow0 + lr) * 2 + 1] = l;
         }
-        const int64_t tq = tok0 + b * TPQ + u_lane;
-        if (tq < a.t) {
-            half_t* dst = a.out + (tq * H + head) * HD + ch * VD + G * 4;
+        const int cc = (lane % 32) * 8;
 #pragma unroll
-            for (int c = 0; c < CT; ++c) {
-                const half4 v = {half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
-                                 half_t(o[b][c][3] * inv)};
-                *reinterpret_cast<half4*>(dst + c * 16) = v;
+        for (int i = 0; i < 8; ++i) {
+            const int r = 2 * i + lane / 32;
+            const half8 v = *reinterpret_cast<const half8*>(stage + r * SROW + cc);
+            if (slot >= 0) {
+                *reinterpret_cast<half8*>(a.part_o + (prow0 + r) * HD + ch * VD + cc) = v;
+            } else {
+                const int64_t tq = tok0 + b * TPQ + r / HPG;
+                if (tq < a.t)
+                    *reinterpret_cast<half8*>(a.out + (tq * H + g * HPG + r % HPG) * HD + ch * VD + cc) = v;
             }
         }
     }
