@@ -13,6 +13,7 @@ E_INVALID, E_CAPACITY, E_DEVICE, E_STATE, E_IO, E_MISSING = -1, -2, -3, -4, -5, 
 DTYPE_F16, DTYPE_Q8, DTYPE_Q4 = 0, 1, 2
 WANT_LOGITS, WANT_HIDDEN, WANT_LABELS, WANT_LABELS_LSE = 0, 1, 2, 3
 SRC_NONE, SRC_RESIDENT, SRC_RAM, SRC_DISK, SRC_DECODED = 0, 1, 2, 3, 4
+ROLE_NONE, ROLE_OPT, ROLE_DECIDE = 0, 1, 2
 
 
 class OmgError(RuntimeError):
@@ -77,6 +78,10 @@ _SIGS = {
     "omg_warmup": (C.c_int, [_P]),
     "omg_evaluate_groups": (C.c_int, [_P, C.POINTER(omg_group), C.c_size_t, C.c_int, C.POINTER(C.c_uint32),
                                       C.c_size_t, C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_int)]),
+    "omg_set_pointer_head": (C.c_int, [_P, C.c_size_t, C.c_size_t, C.POINTER(C.c_float), C.POINTER(C.c_float),
+                                       C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+    "omg_evaluate_pointer": (C.c_int, [_P, C.POINTER(omg_group), C.c_size_t, C.POINTER(C.c_uint8), C.c_size_t,
+                                       C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_size_t), C.POINTER(C.c_int)]),
     "omg_evaluate": (C.c_int, [_P, C.POINTER(C.c_uint32), C.c_size_t, C.POINTER(omg_branch), C.c_size_t, C.c_int,
                                C.POINTER(C.c_uint32), C.c_size_t, C.POINTER(C.c_float), C.c_size_t]),
     "omg_prefix_source": (C.c_int, [_P]),

@@ -63,6 +63,9 @@ int guard(F&& f) {
     }
 }
 
+static_assert(OMG_ROLE_NONE == omg::ROLE_NONE && OMG_ROLE_OPT == omg::ROLE_OPT && OMG_ROLE_DECIDE == omg::ROLE_DECIDE,
+              "pointer roles");
+
 struct Groups {
     std::vector<std::vector<omg::BranchIn>> branches;
     std::vector<omg::GroupIn> groups;
@@ -279,6 +282,22 @@ int omg_evaluate_groups(omg_engine* e, const omg_group* groups, size_t ngroups, 
         if (!out && out_floats) omg::fail(omg::E_INVALID, "null output");
         eng(e).evaluate_groups(g.groups.data(), int64_t(ngroups), want, label_ids, int64_t(nlabels), out,
                                int64_t(out_floats), prefix_sources);
+    });
+}
+
+int omg_set_pointer_head(omg_engine* e, size_t d, size_t dp, const float* w_q, const float* b_q, const float* w_k,
+                         const float* b_k) {
+    return guard([&] { eng(e).set_pointer_head(int64_t(d), int64_t(dp), w_q, b_q, w_k, b_k); });
+}
+
+int omg_evaluate_pointer(omg_engine* e, const omg_group* groups, size_t ngroups, const uint8_t* roles,
+                         size_t nroles, float* out, size_t out_floats, size_t* written, int* prefix_sources) {
+    return guard([&] {
+        Groups g = convert(groups, ngroups);
+        if (!out && out_floats) omg::fail(omg::E_INVALID, "null output");
+        const int64_t k = eng(e).evaluate_pointer(g.groups.data(), int64_t(ngroups), roles, int64_t(nroles), out,
+                                                  int64_t(out_floats), prefix_sources);
+        if (written) *written = size_t(k);
     });
 }
 

@@ -311,6 +311,7 @@ Engine::~Engine() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (h_in_) (void)hipHostFree(h_in_);
     if (h_out_) (void)hipHostFree(h_out_);
+    if (h_ptr_) (void)hipHostFree(h_ptr_);
     if (h_state_) (void)hipHostFree(h_state_);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
@@ -676,36 +677,43 @@ void Engine::readout(const PassPlan& p) {
     }
 }
 
-void Engine::evaluate_groups(const GroupIn* groups, int64_t n, int want, const uint32_t* labels,
-                             int64_t nlabels, float* out, int64_t out_floats, int* sources) {
-    if (n <= 0) fail(E_INVALID, "empty request");
-    if (want != WANT_LOGITS && want != WANT_HIDDEN && want != WANT_LABELS && want != WANT_LABELS_LSE)
-        fail(E_INVALID, "unknown want");
-    const bool by_label = want == WANT_LABELS || want == WANT_LABELS_LSE;
-    if (by_label && (nlabels <= 0 || !labels)) fail(E_INVALID, "label readout without label ids");
+Engine::Run Engine::run_pass(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
+                             int64_t out_floats_needed, int64_t out_floats) {
+    Run run;
     auto [first, source] = admit(groups, n);
-    Packed pk = pack_checked(groups, n, first, source != SRC_NONE);
-    const int64_t width = want == WANT_HIDDEN   ? cfg_.d
-                          : want == WANT_LOGITS ? cfg_.vocab
-                          : want == WANT_LABELS ? nlabels
-                                                : nlabels + 1;
-    const int64_t nrows = int64_t(pk.wanted.size());
-    if (nrows * width > out_floats)
+    run.first = first;
+    run.source = source;
+    run.pk = pack_checked(groups, n, first, source != SRC_NONE);
+    if (out_floats_needed > out_floats)
         fail(E_INVALID, "output buffer holds " + std::to_string(out_floats) + " floats, " +
-                            std::to_string(nrows * width) + " needed");
-    upload(pk, labels, by_label ? nlabels : 0);
-    const int64_t t = pk.total - pk.base;
-    forward(t, pk.base);
-    PassPlan plan{t, pk.base, nrows, nlabels, want};
-    readout(plan);
-    if (nrows) {
-        const DevBuf& src = want == WANT_HIDDEN ? rows_ : want == WANT_LABELS_LSE ? label_lse_ : logits_;
-        OMG_HIP(hipMemcpyAsync(h_out_, src.p, size_t(nrows * width) * 4, hipMemcpyDeviceToHost, stream_));
-    }
-    sync();
-    // Dense output in the caller's (group, branch, want) order.
-    std::vector<int64_t> goff(static_cast<size_t>(n) + 1, 0);
-    std::vector<std::vector<int64_t>> boff(static_cast<size_t>(n));
+                            std::to_string(out_floats_needed) + " needed");
+    const bool by_label = want == WANT_LABELS || want == WANT_LABELS_LSE;
+    upload(run.pk, labels, by_label ? nlabels : 0);
+    const int64_t t = run.pk.total - run.pk.base;
+    forward(t, run.pk.base);
+    readout(PassPlan{t, run.pk.base, int64_t(run.pk.wanted.size()), nlabels, want});
+    return run;
+}
+
+void Engine::finish_pass(const GroupIn* groups, int64_t n, const Run& run, int* sources) {
+    // engine.rs:1928-1939: cache rows 0..p0 now hold the first group's
+    // prefix; every prefix decoded here goes to the state cache.
+    const GroupIn& g0 = groups[run.first];
+    resident_ = std::vector<uint32_t>(g0.prefix, g0.prefix + g0.prefix_len);
+    for (const auto& dgrp : run.pk.decoded)
+        remember(groups[dgrp.first].prefix, groups[dgrp.first].prefix_len, dgrp.second);
+    const int source = run.source == SRC_NONE ? SRC_DECODED : run.source;
+    if (sources)
+        for (int64_t g = 0; g < n; ++g) sources[g] = g == run.first ? source : SRC_DECODED;
+    last_source_ = source;
+}
+
+// Offsets of each group's and branch's first wanted row in the caller's
+// (group, branch, want) order.
+static void want_offsets(const GroupIn* groups, int64_t n, std::vector<int64_t>& goff,
+                         std::vector<std::vector<int64_t>>& boff) {
+    goff.assign(static_cast<size_t>(n) + 1, 0);
+    boff.assign(static_cast<size_t>(n), {});
     for (int64_t g = 0; g < n; ++g) {
         int64_t acc = 0;
         for (int64_t b = 0; b < groups[g].nbranches; ++b) {
@@ -714,21 +722,135 @@ void Engine::evaluate_groups(const GroupIn* groups, int64_t n, int want, const u
         }
         goff[size_t(g) + 1] = goff[size_t(g)] + acc;
     }
+}
+
+void Engine::evaluate_groups(const GroupIn* groups, int64_t n, int want, const uint32_t* labels,
+                             int64_t nlabels, float* out, int64_t out_floats, int* sources) {
+    if (n <= 0) fail(E_INVALID, "empty request");
+    if (want != WANT_LOGITS && want != WANT_HIDDEN && want != WANT_LABELS && want != WANT_LABELS_LSE)
+        fail(E_INVALID, "unknown want");
+    const bool by_label = want == WANT_LABELS || want == WANT_LABELS_LSE;
+    if (by_label && (nlabels <= 0 || !labels)) fail(E_INVALID, "label readout without label ids");
+    const int64_t width = want == WANT_HIDDEN   ? cfg_.d
+                          : want == WANT_LOGITS ? cfg_.vocab
+                          : want == WANT_LABELS ? nlabels
+                                                : nlabels + 1;
+    int64_t nwant = 0;
+    for (int64_t g = 0; g < n; ++g)
+        for (int64_t b = 0; b < groups[g].nbranches; ++b) nwant += groups[g].branches[b].nwant;
+    const Run run = run_pass(groups, n, want, labels, nlabels, nwant * width, out_floats);
+    const Packed& pk = run.pk;
+    const int64_t nrows = int64_t(pk.wanted.size());
+    if (nrows) {
+        const DevBuf& src = want == WANT_HIDDEN ? rows_ : want == WANT_LABELS_LSE ? label_lse_ : logits_;
+        OMG_HIP(hipMemcpyAsync(h_out_, src.p, size_t(nrows * width) * 4, hipMemcpyDeviceToHost, stream_));
+    }
+    sync();
+    // Dense output in the caller's (group, branch, want) order.
+    std::vector<int64_t> goff;
+    std::vector<std::vector<int64_t>> boff;
+    want_offsets(groups, n, goff, boff);
     const float* h = static_cast<const float*>(h_out_);
     for (int64_t r = 0; r < nrows; ++r) {
         const auto& w = pk.wanted[size_t(r)];
         const int64_t dst = goff[size_t(w[0])] + boff[size_t(w[0])][size_t(w[1])] + w[2];
         std::memcpy(out + dst * width, h + r * width, size_t(width) * 4);
     }
-    // engine.rs:1928-1939: cache rows 0..p0 now hold the first group's
-    // prefix; every prefix decoded here goes to the state cache.
-    resident_ = std::vector<uint32_t>(groups[first].prefix, groups[first].prefix + groups[first].prefix_len);
-    for (const auto& dgrp : pk.decoded)
-        remember(groups[dgrp.first].prefix, groups[dgrp.first].prefix_len, dgrp.second);
-    if (source == SRC_NONE) source = SRC_DECODED;
-    if (sources)
-        for (int64_t g = 0; g < n; ++g) sources[g] = g == first ? source : SRC_DECODED;
-    last_source_ = source;
+    finish_pass(groups, n, run, sources);
+}
+
+void Engine::set_pointer_head(int64_t d, int64_t dp, const float* w_q, const float* b_q, const float* w_k,
+                              const float* b_k) {
+    if (!w_q) {  // no head
+        ptr_dp_ = 0;
+        return;
+    }
+    if (!b_q || !w_k || !b_k) fail(E_INVALID, "pointer head: null weight");
+    if (d != cfg_.d) fail(E_INVALID, "pointer head: input width " + std::to_string(d) + ", model width " +
+                                         std::to_string(cfg_.d));
+    if (dp <= 0 || dp > 65536) fail(E_INVALID, "pointer head: projection width out of range");
+    OMG_HIP(hipStreamSynchronize(stream_));  // a pass may still read the old head
+    const size_t wb = size_t(dp * d) * 4, bb = size_t(dp) * 4;
+    ptr_w_ = DevBuf(2 * wb);
+    ptr_b_ = DevBuf(2 * bb);
+    ptr_proj_ = DevBuf(size_t(max_rows_ * dp) * 4);
+    if (!ptr_plan_.p) {
+        const size_t plan = size_t((max_rows_ + 1) / 2 * 2) * 4 + size_t(max_rows_) * 8;
+        ptr_plan_ = DevBuf(plan);
+        ptr_out_ = DevBuf(size_t(max_rows_) * 4);
+        OMG_HIP(hipHostMalloc(&h_ptr_, plan, hipHostMallocDefault));
+    }
+    OMG_HIP(hipMemcpy(ptr_w_.p, w_q, wb, hipMemcpyHostToDevice));
+    OMG_HIP(hipMemcpy(ptr_w_.as<uint8_t>() + wb, w_k, wb, hipMemcpyHostToDevice));
+    OMG_HIP(hipMemcpy(ptr_b_.p, b_q, bb, hipMemcpyHostToDevice));
+    OMG_HIP(hipMemcpy(ptr_b_.as<uint8_t>() + bb, b_k, bb, hipMemcpyHostToDevice));
+    ptr_dp_ = dp;
+}
+
+int64_t Engine::evaluate_pointer(const GroupIn* groups, int64_t n, const uint8_t* roles, int64_t nroles,
+                                 float* out, int64_t out_floats, int* sources) {
+    if (ptr_dp_ <= 0) fail(E_INVALID, "pointer readout without a pointer head");
+    if (n <= 0) fail(E_INVALID, "empty request");
+    std::vector<int64_t> goff;
+    std::vector<std::vector<int64_t>> boff;
+    want_offsets(groups, n, goff, boff);
+    const int64_t nwant = goff[size_t(n)];
+    if (nroles != nwant || (nwant && !roles))
+        fail(E_INVALID, "pointer readout: " + std::to_string(nroles) + " roles for " + std::to_string(nwant) +
+                            " wanted rows");
+    // readout.rs:149-173 per branch: the `</opt>` rows in order and exactly
+    // one `<decide>` row.
+    int64_t nlogits = 0;
+    for (int64_t g = 0; g < n; ++g)
+        for (int64_t b = 0; b < groups[g].nbranches; ++b) {
+            const uint8_t* r = roles + goff[size_t(g)] + boff[size_t(g)][size_t(b)];
+            int decide = 0;
+            for (int64_t s = 0; s < groups[g].branches[b].nwant; ++s) {
+                if (r[s] > ROLE_DECIDE) fail(E_INVALID, "pointer readout: unknown role");
+                decide += r[s] == ROLE_DECIDE;
+                nlogits += r[s] == ROLE_OPT;
+            }
+            if (decide != 1) fail(E_INVALID, decide ? "pointer readout: more than one decide row" : "no decide row");
+        }
+    const Run run = run_pass(groups, n, WANT_HIDDEN, nullptr, 0, nlogits, out_floats);
+    const Packed& pk = run.pk;
+    const int64_t nrows = int64_t(pk.wanted.size());
+    // The plan: per wanted row (workspace order) its map (0 = q for the
+    // decide row, 1 = k for an option, -1 = none); per logit (caller order)
+    // the option row and its branch's decide row.
+    int32_t* mat = static_cast<int32_t*>(h_ptr_);
+    const int64_t mat_slots = (max_rows_ + 1) / 2 * 2;  // the pairs start 8-byte aligned
+    int2* pairs = reinterpret_cast<int2*>(mat + mat_slots);
+    std::vector<int32_t> ws_row(size_t(nwant), -1);  // caller index -> workspace row
+    for (int64_t r = 0; r < nrows; ++r) {
+        const auto& w = pk.wanted[size_t(r)];
+        const int64_t c = goff[size_t(w[0])] + boff[size_t(w[0])][size_t(w[1])] + w[2];
+        ws_row[size_t(c)] = int32_t(r);
+        mat[r] = roles[c] == ROLE_DECIDE ? 0 : roles[c] == ROLE_OPT ? 1 : -1;
+    }
+    int64_t k = 0;
+    for (int64_t g = 0; g < n; ++g)
+        for (int64_t b = 0; b < groups[g].nbranches; ++b) {
+            const int64_t c0 = goff[size_t(g)] + boff[size_t(g)][size_t(b)], nw = groups[g].branches[b].nwant;
+            int32_t decide = -1;
+            for (int64_t s = 0; s < nw; ++s)
+                if (roles[c0 + s] == ROLE_DECIDE) decide = ws_row[size_t(c0 + s)];
+            for (int64_t s = 0; s < nw; ++s)
+                if (roles[c0 + s] == ROLE_OPT) pairs[k++] = int2{ws_row[size_t(c0 + s)], decide};
+        }
+    int32_t* d_mat = ptr_plan_.as<int32_t>();
+    int2* d_pairs = reinterpret_cast<int2*>(d_mat + mat_slots);
+    OMG_HIP(hipMemcpyAsync(d_mat, mat, size_t(nrows) * 4, hipMemcpyHostToDevice, stream_));
+    if (nlogits) OMG_HIP(hipMemcpyAsync(d_pairs, pairs, size_t(nlogits) * 8, hipMemcpyHostToDevice, stream_));
+    step("pointer", [&] {
+        launch_pointer(stream_, rows_.as<float>(), nrows, cfg_.d, ptr_w_.as<float>(), ptr_b_.as<float>(), ptr_dp_,
+                       d_mat, ptr_proj_.as<float>(), d_pairs, nlogits, ptr_out_.as<float>());
+    });
+    if (nlogits) OMG_HIP(hipMemcpyAsync(h_out_, ptr_out_.p, size_t(nlogits) * 4, hipMemcpyDeviceToHost, stream_));
+    sync();
+    if (nlogits) std::memcpy(out, h_out_, size_t(nlogits) * 4);
+    finish_pass(groups, n, run, sources);
+    return nlogits;
 }
 
 void Engine::warmup() {

@@ -24,6 +24,9 @@ namespace omg {
 
 enum WantKind { WANT_LOGITS = 0, WANT_HIDDEN = 1, WANT_LABELS = 2, WANT_LABELS_LSE = 3 };
 enum Source { SRC_NONE = 0, SRC_RESIDENT = 1, SRC_RAM = 2, SRC_DISK = 3, SRC_DECODED = 4 };
+// readout.rs Mark: a wanted row that is none of these (Mark::Last), an
+// option's `</opt>` (Mark::OptEnd) or the `<decide>` row (Mark::Decide).
+enum Role { ROLE_NONE = 0, ROLE_OPT = 1, ROLE_DECIDE = 2 };
 
 // Owned device allocation.
 struct DevBuf {
@@ -93,6 +96,18 @@ class Engine {
                          float* out, int64_t out_floats, int* sources);
     void warmup();  // engine.rs:1356-1366
 
+    // Readout::Pointer (omg-core readout.rs:17-44, 149-173) on the device:
+    // the head's two affine maps d -> dp (row-major [dp][d] and [dp], f32).
+    void set_pointer_head(int64_t d, int64_t dp, const float* w_q, const float* b_q, const float* w_k,
+                          const float* b_k);
+    // A hidden-state pass whose wanted rows are scored by the head: roles
+    // (one per wanted row, (group, branch, want) order) mark each row as an
+    // option end (ROLE_OPT), the decide row (ROLE_DECIDE, one per branch) or
+    // neither; out gets each branch's option logits in want order, branch
+    // after branch.  Returns the logits written.
+    int64_t evaluate_pointer(const GroupIn* groups, int64_t n, const uint8_t* roles, int64_t nroles, float* out,
+                             int64_t out_floats, int* sources);
+
     void set_state_cache(size_t bytes, const std::string& dir, const std::string& model_id);
     SavedState save_state(const uint32_t* prefix, int64_t n) { return save_state_at(prefix, n, 0); }
     // The same state serialised straight from the pinned staging buffer as
@@ -134,6 +149,16 @@ class Engine {
     size_t stage_state(int64_t p, int64_t row0);
     std::pair<int64_t, int64_t> state_rows(int64_t layer, int64_t p) const;
     Packed pack_checked(const GroupIn* groups, int64_t n, int64_t first, bool resident) const;
+    // A request's pass up to its readout, enqueued (admit, pack, upload,
+    // forward, readout of `want`), and the bookkeeping after it ran.
+    struct Run {
+        Packed pk;
+        int64_t first = 0;
+        int source = SRC_NONE;
+    };
+    Run run_pass(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
+                 int64_t out_floats_needed, int64_t out_floats);
+    void finish_pass(const GroupIn* groups, int64_t n, const Run& run, int* sources);
     void upload(const Packed& pk, const uint32_t* labels, int64_t nlabels);
     void forward(int64_t t, int64_t base);
     void readout(const PassPlan& plan);
@@ -193,6 +218,10 @@ class Engine {
     size_t h_in_bytes_ = 0;
     void* h_out_ = nullptr;
     size_t h_out_bytes_ = 0;
+    // pointer head ([q; k] maps) and its per-pass plan / projections
+    int64_t ptr_dp_ = 0;
+    DevBuf ptr_w_, ptr_b_, ptr_plan_, ptr_proj_, ptr_out_;
+    void* h_ptr_ = nullptr;  // pinned plan staging: max_rows row matrices + max_rows row pairs
     // pinned staging of a whole state's K/V rows (save / restore), sized
     // at finish for a state of `capacity` tokens
     void* h_state_ = nullptr;

@@ -123,6 +123,12 @@ int64_t label_readout_scratch_floats();
 // out [nrows][nlabels + 1].
 void launch_label_lse(hipStream_t s, const float* logits, int64_t nrows, int64_t vocab, const float2* part,
                       int64_t nblocks, const uint32_t* labels, int64_t nlabels, float* out);
+// Readout::Pointer (readout.rs:30-44): proj[r] = W_m h_r + b_m for each row
+// r of `rows` with a map m = mat[r] (0: the q map, 1: the k map, -1: none),
+// w = [W_q; W_k] row-major [2][dp][d], b = [b_q; b_k]; then for each pair i
+// (option row, decide row) out[i] = proj[option] . proj[decide] / sqrt(dp).
+void launch_pointer(hipStream_t s, const float* rows, int64_t nrows, int64_t d, const float* w, const float* b,
+                    int64_t dp, const int32_t* mat, float* proj, const int2* pairs, int64_t npairs, float* out);
 // K/V cache rows <-> the reference's state row format [K heads | V heads] f16.
 void launch_kv_gather(hipStream_t s, const half_t* kc, const half_t* vt, int64_t cap_pad, int kv_heads,
                       int hd, int64_t row0, int64_t rows, half_t* out);

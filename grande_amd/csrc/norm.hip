@@ -703,6 +703,60 @@ void launch_label_lse(hipStream_t s, const float* logits, int64_t nrows, int64_t
     OMG_HIP(hipGetLastError());
 }
 
+// ------------------------------------------------------ pointer readout
+
+// readout.rs:30-36 (PointerHead::project) for the rows that have a map: one
+// workgroup per row, the row in LDS, each wave one output at a time (its
+// weight row read once, coalesced, and summed across the wave).
+__global__ __launch_bounds__(256) void pointer_project_kernel(const float* __restrict__ rows, int64_t d,
+                                                              const float* __restrict__ w,
+                                                              const float* __restrict__ b, int64_t dp,
+                                                              const int32_t* __restrict__ mat,
+                                                              float* __restrict__ proj) {
+    extern __shared__ float h[];
+    const int64_t r = blockIdx.x;
+    const int m = mat[r];
+    if (m < 0) return;
+    const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
+    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) h[i] = rows[r * d + i];
+    __syncthreads();
+    const float* W = w + int64_t(m) * dp * d;
+    for (int64_t o = wave; o < dp; o += blockDim.x / WAVE) {
+        float acc = 0.0f;
+        for (int64_t i = lane; i < d; i += WAVE) acc += W[o * d + i] * h[i];
+        acc = wave_sum(acc);
+        if (lane == 0) proj[r * dp + o] = acc + b[int64_t(m) * dp + o];
+    }
+}
+
+// readout.rs:37-44 (PointerHead::logits): one wave per (option, decide) pair.
+__global__ __launch_bounds__(256) void pointer_logits_kernel(const float* __restrict__ proj, int64_t dp,
+                                                             const int2* __restrict__ pairs, int64_t npairs,
+                                                             float scale, float* __restrict__ out) {
+    const int64_t i = int64_t(blockIdx.x) * (blockDim.x / WAVE) + int(threadIdx.x) / WAVE;
+    if (i >= npairs) return;
+    const int lane = int(threadIdx.x) % WAVE;
+    const int2 pr = pairs[i];
+    const float* k = proj + int64_t(pr.x) * dp;
+    const float* q = proj + int64_t(pr.y) * dp;
+    float acc = 0.0f;
+    for (int64_t j = lane; j < dp; j += WAVE) acc += k[j] * q[j];
+    acc = wave_sum(acc);
+    if (lane == 0) out[i] = acc * scale;
+}
+
+void launch_pointer(hipStream_t s, const float* rows, int64_t nrows, int64_t d, const float* w, const float* b,
+                    int64_t dp, const int32_t* mat, float* proj, const int2* pairs, int64_t npairs, float* out) {
+    if (nrows <= 0) return;
+    if (d <= 0 || d > 16384 || dp <= 0) fail(E_INVALID, "pointer: width out of range");
+    pointer_project_kernel<<<dim3(unsigned(nrows)), dim3(256), size_t(d) * 4, s>>>(rows, d, w, b, dp, mat, proj);
+    OMG_HIP(hipGetLastError());
+    if (npairs <= 0) return;
+    const float scale = 1.0f / std::sqrt(float(dp));
+    pointer_logits_kernel<<<dim3(unsigned((npairs + 3) / 4)), dim3(256), 0, s>>>(proj, dp, pairs, npairs, scale, out);
+    OMG_HIP(hipGetLastError());
+}
+
 // ------------------------------------------- readout without allocation
 
 // Scratch of launch_label_readout_noalloc: the full logits rows, then the

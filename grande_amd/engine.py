@@ -44,6 +44,80 @@ class PrefixSource(enum.IntEnum):
     DECODED = L.SRC_DECODED
 
 
+class Role(enum.IntEnum):
+    """readout.rs Mark, for the pointer readout: a wanted row that is not
+    scored (Mark::Last), an option's `</opt>` row (Mark::OptEnd) or the
+    `<decide>` row (Mark::Decide)."""
+
+    NONE = L.ROLE_NONE
+    OPT = L.ROLE_OPT
+    DECIDE = L.ROLE_DECIDE
+
+
+@dataclass
+class PointerHead:
+    """readout.rs:17-44 PointerHead: two affine maps d -> dp (weights
+    row-major [dp, d], biases [dp]), option logits k_i . q / sqrt(dp) with
+    q = W_q h_decide + b_q and k_i = W_k h_i + b_k."""
+
+    w_q: np.ndarray
+    b_q: np.ndarray
+    w_k: np.ndarray
+    b_k: np.ndarray
+
+    @property
+    def dp(self) -> int:
+        return int(self.w_q.shape[0])
+
+    @property
+    def d(self) -> int:
+        return int(self.w_q.shape[1])
+
+    @classmethod
+    def load(cls, src: "str | Path | bytes") -> "PointerHead":
+        """readout.rs:208-345: `head.safetensors` with q.weight [dp, d],
+        q.bias [dp], k.weight, k.bias in F32, F16 or BF16."""
+        data = src if isinstance(src, (bytes, bytearray)) else Path(src).read_bytes()
+        if len(data) < 8:
+            raise ValueError("head.safetensors: too short")
+        n = int.from_bytes(data[:8], "little")
+        if 8 + n > len(data):
+            raise ValueError("head.safetensors: header")
+        import json
+
+        header = json.loads(data[8:8 + n])
+        base = 8 + n
+
+        def tensor(name: str) -> np.ndarray:
+            t = header.get(name)
+            if t is None:
+                raise ValueError(f"head.safetensors: missing tensor {name}")
+            lo, hi = (int(v) for v in t["data_offsets"])
+            shape = [int(v) for v in t["shape"]]
+            if not 0 <= lo <= hi <= len(data) - base:
+                raise ValueError(f"head.safetensors: {name} data out of range")
+            raw = np.frombuffer(data[base + lo:base + hi], np.uint8)
+            kind = t["dtype"]
+            if kind == "F32":
+                v = raw.view("<f4").astype(np.float32)
+            elif kind == "F16":
+                v = raw.view("<f2").astype(np.float32)
+            elif kind == "BF16":
+                v = (raw.view("<u2").astype(np.uint32) << 16).view(np.float32)
+            else:
+                raise ValueError(f"head.safetensors: {name} dtype {kind}")
+            if v.size != int(np.prod(shape)):
+                raise ValueError(f"head.safetensors: {name} size")
+            return v.reshape(shape)
+
+        w_q, b_q, w_k, b_k = (tensor(x) for x in ("q.weight", "q.bias", "k.weight", "k.bias"))
+        if w_q.ndim != 2 or w_q.shape != w_k.shape:
+            raise ValueError(f"head.safetensors: weight shapes {w_q.shape} / {w_k.shape}")
+        if b_q.shape != (w_q.shape[0],) or b_k.shape != (w_q.shape[0],):
+            raise ValueError("head.safetensors: bias shape")
+        return cls(w_q, b_q, w_k, b_k)
+
+
 @dataclass
 class BranchTokens:
     """backend.rs:22-30: branch tokens + ascending wanted indices."""
@@ -192,6 +266,40 @@ class Engine:
                 bo.append(BranchOutput(rows=[out[r + s, :width].copy() for s in range(len(b.want))]))
                 r += len(b.want)
             res.append(GroupOutput(branches=bo, prefix_source=PrefixSource(src[gi])))
+        return res
+
+    def set_pointer_head(self, head: "PointerHead | None") -> None:
+        """The head omg_evaluate_pointer scores with (None clears it)."""
+        if head is None:
+            L.check(L.lib().omg_set_pointer_head(self._h, 0, 0, None, None, None, None))
+            return
+        ts = [np.ascontiguousarray(x, np.float32) for x in (head.w_q, head.b_q, head.w_k, head.b_k)]
+        ptr = [x.ctypes.data_as(C.POINTER(C.c_float)) for x in ts]
+        L.check(L.lib().omg_set_pointer_head(self._h, head.d, head.dp, *ptr))
+
+    def evaluate_pointer(self, groups: Sequence[Group], roles: Sequence[Sequence[Sequence[int]]]
+                         ) -> list[list[np.ndarray]]:
+        """readout.rs:149-173 on the device: per group, per branch, the
+        option logits of the rows marked Role.OPT (in want order) against
+        the branch's Role.DECIDE row.  roles[g][b] has one Role per wanted
+        row of branch b of group g."""
+        cg = _CGroups(groups)
+        flat = np.array([r for gr in roles for br in gr for r in br], np.uint8)
+        k = sum(1 for gr in roles for br in gr for r in br if r == Role.OPT)
+        out = np.zeros(max(k, 1), np.float32)
+        written = C.c_size_t(0)
+        src = (C.c_int * max(1, len(groups)))()
+        L.check(L.lib().omg_evaluate_pointer(self._h, cg.arr, cg.n, flat.ctypes.data_as(C.POINTER(C.c_uint8)),
+                                             flat.size, out.ctypes.data_as(C.POINTER(C.c_float)), out.size,
+                                             C.byref(written), src))
+        res, i = [], 0
+        for gr in roles:
+            gout = []
+            for br in gr:
+                n = sum(1 for r in br if r == Role.OPT)
+                gout.append(out[i:i + n].copy())
+                i += n
+            res.append(gout)
         return res
 
     def evaluate(self, prefix: Sequence[int], branches: Sequence[BranchTokens], want: Want,

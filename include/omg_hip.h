@@ -147,6 +147,24 @@ int omg_warmup(omg_engine *e);
 int omg_evaluate_groups(omg_engine *e, const omg_group *groups, size_t ngroups, int want,
                         const uint32_t *label_ids, size_t nlabels, float *out, size_t out_floats,
                         int *prefix_sources);
+/* Readout::Pointer's head (omg-core readout.rs:17-29, PointerHead): two
+ * affine maps d -> dp, weights row-major [dp][d] and biases [dp], f32; the
+ * engine keeps a device copy.  w_q = NULL clears it. */
+int omg_set_pointer_head(omg_engine *e, size_t d, size_t dp, const float *w_q, const float *b_q,
+                         const float *w_k, const float *b_k);
+/* The roles of wanted rows for omg_evaluate_pointer (readout.rs Mark). */
+#define OMG_ROLE_NONE 0   /* Mark::Last: not scored */
+#define OMG_ROLE_OPT 1    /* Mark::OptEnd: an option's `</opt>` row */
+#define OMG_ROLE_DECIDE 2 /* Mark::Decide: the `<decide>` row */
+/* Readout::distribution's pointer branch (readout.rs:149-173) on the
+ * device: omg_evaluate_groups with Want::Hidden whose rows are scored by the
+ * pointer head (readout.rs:37-44) instead of read back.  roles: one per
+ * wanted row in (group, branch, want) order, each branch with exactly one
+ * OMG_ROLE_DECIDE row ("no decide row" otherwise).  out: each branch's
+ * option logits (its OMG_ROLE_OPT rows in want order), branch after branch
+ * in (group, branch) order; *written (may be NULL) = their count. */
+int omg_evaluate_pointer(omg_engine *e, const omg_group *groups, size_t ngroups, const uint8_t *roles,
+                         size_t nroles, float *out, size_t out_floats, size_t *written, int *prefix_sources);
 /* Engine::evaluate (engine.rs:1386-1396): one group. */
 int omg_evaluate(omg_engine *e, const uint32_t *prefix, size_t prefix_len, const omg_branch *branches,
                  size_t nbranches, int want, const uint32_t *label_ids, size_t nlabels, float *out,

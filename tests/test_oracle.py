@@ -394,6 +394,27 @@ def test_pointer_identity_is_scaled_dot():
     assert z[0] > z[1] and abs(z[0] - 0.5) < 1e-6
 
 
+def test_pointer_closed_forms():
+    """readout.rs:30-44 forms a plausible slip breaks: with a zero k map
+    every option scores b_k . q / sqrt(dp) whatever its row; q is the decide
+    row's map (not an option's); the scale is 1 / sqrt(dp), not 1 / dp."""
+    rng = np.random.default_rng(3)
+    d, dp = 12, 9
+    w_q, w_k = rng.standard_normal((dp, d)), rng.standard_normal((dp, d))
+    b_q, b_k = rng.standard_normal(dp), rng.standard_normal(dp)
+    decide, opts = rng.standard_normal(d), rng.standard_normal((3, d))
+    q = w_q.astype(np.float32) @ decide.astype(np.float32) + b_q.astype(np.float32)
+    z0 = oracle.pointer_logits(w_q, b_q, np.zeros((dp, d)), b_k, decide, opts)
+    assert np.allclose(z0, float(b_k.astype(np.float32) @ q) / 3.0, rtol=1e-5)
+    # swapping the decide row for an option's changes every logit
+    z = oracle.pointer_logits(w_q, b_q, w_k, b_k, decide, opts)
+    zs = oracle.pointer_logits(w_q, b_q, w_k, b_k, opts[0], opts)
+    assert np.all(np.abs(z - zs) > 1e-6)
+    # doubling both maps' weights and biases quadruples the logits
+    z2 = oracle.pointer_logits(2 * w_q, 2 * b_q, 2 * w_k, 2 * b_k, decide, opts)
+    assert np.allclose(z2, 4 * z, rtol=1e-5)
+
+
 def test_label_readout_picks_label_columns():
     row = np.arange(10, dtype=np.float32)
     logits, probs, mass = oracle.label_readout(row, [7, 2, 9])
