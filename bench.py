@@ -92,6 +92,27 @@ def pass_bytes(cfg, dtype, prefix: int, nb: int, bt: int, pattern: int = 6) -> d
     return {"weights": w, "embedding": emb, "kv": kv, "total": w + emb + kv}
 
 
+def kernel_bytes(cfg, dtype, m: int) -> dict:
+    """Algorithmic HBM bytes of one launch of each linear product and of the
+    residual norm over m rows: the weight once, the f16 activations in, the
+    outputs (f32 split-K partials of the o / down products, two at these
+    shapes; f16 q rows and K / V cache rows; f16 gated activations; the
+    norm's stream read and written with its f16 output)."""
+    d, ff, H, KV, hd = cfg["d"], cfg["ff"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    s = storage_bytes_per_elem(dtype)
+
+    def splits(k, n):  # the engine's K split of the o / down products at these shapes
+        return 2 if n <= 1280 and k >= 1024 else 1
+
+    return {
+        "mm_qkv": (H + 2 * KV) * hd * d * s + m * d * 2 + m * (H + 2 * KV) * hd * 2,
+        "mm_o": d * H * hd * s + m * H * hd * 2 + m * d * 4 * splits(H * hd, d),
+        "mm_gate_up": 2 * ff * d * s + m * d * 2 + m * ff * 2,
+        "mm_down": d * ff * s + m * ff * 2 + m * d * 4 * splits(ff, d),
+        "norm": m * d * (4 * 2 + 4 * 2 + 2),
+    }
+
+
 class MallFlush:
     """Evicts the MALL between timed reps: one device-to-device copy of
     `nbytes` (reads nbytes, writes nbytes), through the HIP runtime the
@@ -326,6 +347,14 @@ def main() -> int:
                  "hbm_peak_gb_per_s": HBM_PEAK_GBS, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                  "kernels": {name: {"launches_per_step": n // 3, "avg_us": round(ms / n * 1e3, 2)}
                              for name, (n, ms) in sprof.items()}}
+        # per-launch algorithmic bytes and rate of the products and the norm
+        # (HIP-event intervals: each includes the dispatch gap before it)
+        for name, nbytes in kernel_bytes(mc, spec["dtype"], BT).items():
+            k = small["kernels"].get(name)
+            if k and k["avg_us"] > 0:
+                k["bytes"] = int(nbytes)
+                k["gb_per_s"] = round(nbytes / (k["avg_us"] * 1e-6) / 1e9, 1)
+                k["hbm_frac"] = round(k["gb_per_s"] / HBM_PEAK_GBS, 4)
 
     kernels = {}
     for name, (n, ms) in prof.items():
