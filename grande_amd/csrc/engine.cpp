@@ -529,6 +529,45 @@ static int ksplit(int64_t k, int64_t n) {
     return s;
 }
 
+// Deep-K products (at least 4,096 K per split, in whole 1,024-wide chunks:
+// the 4B model's down projection) sum K in chunks of 16 stages: each chunk's
+// products accumulate from zero and the chunk sums are added in K order.
+// Long passes fold the chunks in the GEMM's registers; short ones run a
+// chunk per workgroup, which fills the chip, and add the partials in the
+// same order.  A function of the shape, so a row's sums do not depend on
+// the pass.
+constexpr int KFOLD_STAGES = 16;
+constexpr int64_t KFOLD_K = 64 * KFOLD_STAGES, KFOLD_MIN_K = 4096;
+constexpr int64_t CHUNKED_ROWS = 512;  // passes of at most this many rows run a chunk per workgroup
+
+Engine::SplitPlan Engine::split_plan(int64_t k, int64_t n, int64_t t) const {
+    SplitPlan p;
+    p.splits = ksplit(k, n);
+    const int64_t kr = k / p.splits;
+    if (kr < KFOLD_MIN_K || kr % KFOLD_K != 0) return p;
+    const int64_t chunks = kr / KFOLD_K;
+    // chunk partials go above the split partials in a_ (OMG_KSPLIT x slots x n floats)
+    if (t <= CHUNKED_ROWS && int64_t(p.splits) * slots_ + p.splits * chunks * t <= int64_t(OMG_KSPLIT) * slots_)
+        p.chunks = int(chunks);
+    else
+        p.kfold = KFOLD_STAGES;
+    return p;
+}
+
+// y = x . W^T into the split partials a_ + z * slots_ * d (z < splits).
+void Engine::split_product(const char* name, const half_t* x, int64_t k, const DevWeight& w, int64_t t,
+                           const SplitPlan& sp) {
+    const int64_t d = cfg_.d, pstride = slots_ * d;
+    float* a = a_.as<float>();
+    if (sp.chunks <= 1) {
+        step(name, [&] { launch_gemm_splitk(stream_, x, k, w, a, d, t, sp.splits, pstride, sp.kfold); });
+        return;
+    }
+    float* area = a + sp.splits * pstride;  // chunk partials, t x d each
+    step(name, [&] { launch_gemm_splitk(stream_, x, k, w, area, d, t, sp.splits * sp.chunks, t * d); });
+    step("fold", [&] { launch_fold_chunks(stream_, area, t * d, sp.chunks, sp.splits, t * d, a, pstride); });
+}
+
 void Engine::forward(int64_t t, int64_t base) {
     const Config& c = cfg_;
     const int64_t d = c.d;
@@ -602,11 +641,10 @@ void Engine::forward(int64_t t, int64_t base) {
         if (n_merges_[kind] > 0)
             step("attention_merge",
                  [&] { launch_attention_merge(stream_, att, d_merges_[kind], n_merges_[kind]); });
-        const int so = ksplit(c.heads * hd, d), sd = ksplit(ff, d);
+        const SplitPlan po = split_plan(c.heads * hd, d, t), pd = split_plan(ff, d, t);
+        const int so = po.splits, sd = pd.splits;
         const int64_t pstride = slots_ * d;
-        step("mm_o", [&] {
-            launch_gemm_splitk(stream_, attn_.as<half_t>(), c.heads * hd, L.o.w, a_.as<float>(), d, t, so, pstride);
-        });
+        split_product("mm_o", attn_.as<half_t>(), c.heads * hd, L.o.w, t, po);
         step("norm", [&] {
             launch_residual_norm(stream_, a_.as<float>(), L.post_attn_norm.as<float>(), x_.as<float>(),
                                  L.ffn_norm.as<float>(), hn_.as<half_t>(), t, d, c.eps, 1.0f, so, pstride);
@@ -614,9 +652,7 @@ void Engine::forward(int64_t t, int64_t base) {
         step("mm_gate_up", [&] {
             launch_gemm_geglu(stream_, hn_.as<half_t>(), d, L.gate.w, L.up.w, act_.as<half_t>(), ff, t);
         });
-        step("mm_down", [&] {
-            launch_gemm_splitk(stream_, act_.as<half_t>(), ff, L.down.w, a_.as<float>(), d, t, sd, pstride);
-        });
+        split_product("mm_down", act_.as<half_t>(), ff, L.down.w, t, pd);
         // The last layer's stream is normed at the wanted rows only (readout).
         const float* next = l + 1 < c.layers ? layers_[size_t(l + 1)].attn_norm.as<float>() : nullptr;
         half_t* next_hn = next ? hn_.as<half_t>() : nullptr;

@@ -160,6 +160,16 @@ class Engine {
                  int64_t out_floats_needed, int64_t out_floats);
     void finish_pass(const GroupIn* groups, int64_t n, const Run& run, int* sources);
     void upload(const Packed& pk, const uint32_t* labels, int64_t nlabels);
+    // How an o / down product of K k and width n runs in a pass of t rows:
+    // its K splits, and for deep K its 256-wide K chunks — folded in the
+    // GEMM's registers (kfold) or, in short passes, one per workgroup and
+    // added by launch_fold_chunks (chunks > 1).
+    struct SplitPlan {
+        int splits = 1, chunks = 1, kfold = 0;
+    };
+    SplitPlan split_plan(int64_t k, int64_t n, int64_t t) const;
+    void split_product(const char* name, const half_t* x, int64_t k, const DevWeight& w, int64_t t,
+                       const SplitPlan& sp);
     void forward(int64_t t, int64_t base);
     void readout(const PassPlan& plan);
     template <class F>

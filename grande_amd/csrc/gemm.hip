@@ -77,6 +77,9 @@ struct GemmArgs {
     // [z K / ksplit, (z + 1) K / ksplit) into y + z * part_stride.
     int ksplit = 1;
     int64_t part_stride = 0;
+    // gemm32_kernel EPI_F32 with FOLD: K chunks of kfold stages (a power of
+    // two) counted from the split's first stage; see launch_gemm_splitk.
+    int kfold = 0;
     // gemm32_kernel: row tiles start at BM * i - mshift (0 <= mshift < BM)
     int64_t mshift = 0;
 };
@@ -540,9 +543,10 @@ __device__ inline bool run_phases(F& f, std::index_sequence<I...>) {
     return (f(std::integral_constant<int, int(I)>{}) && ...);
 }
 
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_, bool FOLD>
 __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW_>;
+    static_assert(!FOLD || EPI == EPI_F32, "K chunks: f32 products only");
     constexpr bool GATED = P::GATED;
     constexpr int NW = P::NW, BM = P::BM, BN = P::BN, WR = P::WR, PK = P::PK, PM = P::PM, R = P::R;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -640,6 +644,13 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[i][j] = floatx16{};
+    // FOLD: each K chunk's products accumulate from zero in acc and the
+    // chunk sums are added into tot in K order — the sums of a pass that
+    // runs every chunk in a workgroup of its own and adds the partials in
+    // order (fold_chunks).
+    floatx16 tot[FOLD ? MI : 1][FOLD ? NJ : 1];
+    const int kfm = g.kfold - 1;  // chunk mask (FOLD)
+    bool folded = false;
 
     const int lr = lane % 32, lh = lane / 32;
     int foff[4];  // the lane's X fragment offset within a 32-row block, per k-step
@@ -729,11 +740,29 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         if (kt + 1 < nk) read_x(kt + 1, nxt);
         compute(cur, wr[PH % R]);
         issue_w(kt + NS - 1, wr[PH % R]);
+        if constexpr (FOLD) {
+            if (((kt + 1) & kfm) == 0 || kt + 1 == nk) {
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        tot[i][j] = folded ? tot[i][j] + acc[i][j] : acc[i][j];
+                        acc[i][j] = floatx16{};
+                    }
+                folded = true;
+            }
+        }
         return ++kt < nk;
     };
     while (run_phases(step, std::make_index_sequence<P::U>{})) {
     }
     wait_vm<0>();
+    if constexpr (FOLD) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) acc[i][j] = tot[i][j];
+    }
 
     if constexpr (EPI == EPI_QKPREP) {
         // qk_prep.wgsl:66-114 on the tile's rows, without cross-lane
@@ -916,7 +945,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     }
 }
 
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4, bool FOLD = false>
 static void run32(hipStream_t s, const GemmArgs& g) {
     using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW>;
     for (const DevWeight* w : {&g.w0, &g.w1})
@@ -924,7 +953,7 @@ static void run32(hipStream_t s, const GemmArgs& g) {
             fail(E_INVALID, "gemm: weight without stage tiles");
     static bool lds_set = false;
     if (!lds_set) {
-        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW>),
+        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
         lds_set = true;
     }
@@ -932,7 +961,7 @@ static void run32(hipStream_t s, const GemmArgs& g) {
     if (g.mshift < 0 || g.mshift >= P::BM) fail(E_INVALID, "gemm: row tile shift out of range");
     const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + g.mshift + P::BM - 1) / P::BM);
     const dim3 grid(unsigned((tiles + 7) / 8 * 8), unsigned(g.ksplit));
-    gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW><<<grid, dim3(P::T), P::LDS, s>>>(g);
+    gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD><<<grid, dim3(P::T), P::LDS, s>>>(g);
     OMG_HIP(hipGetLastError());
 }
 
@@ -987,6 +1016,10 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         return run32<QUANT, 2, 2, EPI, 4, 4>(s, g);
     } else if constexpr (EPI == EPI_F32) {
         // 32x32x16 tiles (gemm32_kernel) for every M: the same sums per element
+        if (g.kfold > 0) {  // K chunks folded in registers (up to 96-row tiles: the totals fit)
+            if (M <= 512) return run32<QUANT, 1, 1, EPI, 4, 4, true>(s, g);
+            return run32<QUANT, 3, 1, EPI, 4, 4, true>(s, g);
+        }
         if (M <= 512) return run32<QUANT, 1, 1, EPI, 4, 4>(s, g);
         if (M >= 8192) return run32<QUANT, 4, 1, EPI, 3, 4>(s, g);
         if (g.ksplit > 1) return run32<QUANT, 3, 1, EPI, 4, 4>(s, g);  // split K: twice the tiles
@@ -1031,15 +1064,17 @@ void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w
 }
 
 void launch_gemm_splitk(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
-                       int64_t m, int parts, int64_t part_stride) {
+                       int64_t m, int parts, int64_t part_stride, int kfold) {
     check(x, ldx, w, ldy, m);
     if (parts < 1 || (parts > 1 && w.cols % (int64_t(G_BK) * parts) != 0))
         fail(E_INVALID, "gemm_splitk: K must split into parts of whole 64-wide stages");
+    if (kfold < 0 || (kfold & (kfold - 1)) != 0) fail(E_INVALID, "gemm_splitk: K chunk stages must be a power of two");
     if (parts > 1 && part_stride < m * ldy) fail(E_INVALID, "gemm_splitk: partial outputs overlap");
     if (m == 0) return;
     GemmArgs g{x, ldx, m, w, w, y, ldy, nullptr, {}};
     g.ksplit = parts;
     g.part_stride = part_stride;
+    g.kfold = kfold;
     dispatch_dtype<EPI_F32>(s, g);
 }
 

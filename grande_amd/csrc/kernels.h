@@ -162,8 +162,18 @@ void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w
 // partial p (K range p) goes to y + p * part_stride; the sum is the
 // consumer's (launch_residual_norm).  More workgroups for narrow-N, deep-K
 // products; each partial's rows are independent of M.
+// kfold > 0 (a power of two): inside each range the products of every
+// kfold stages (64 K each) accumulate from zero and these chunk sums are
+// added in K order — the sums of ranges of one chunk each added in order
+// by launch_fold_chunks.
 void launch_gemm_splitk(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
-                        int64_t m, int parts, int64_t part_stride);
+                        int64_t m, int parts, int64_t part_stride, int kfold = 0);
+// out + p * out_stride = in[p * chunks] + in[p * chunks + 1] + ... (in this
+// order) for p < parts, over the first n floats of each (n % 4 == 0), with
+// in[c] = in + c * in_stride: the K chunks of a split-K product added as
+// launch_gemm_splitk's kfold adds them.
+void launch_fold_chunks(hipStream_t s, const float* in, int64_t in_stride, int chunks, int parts, int64_t n,
+                        float* out, int64_t out_stride);
 // act[M][F] (f16) = gelu(X . Wg^T) * (X . Wu^T); gelu_tanh, or the exact
 // (erf) form when `erf`.
 void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,

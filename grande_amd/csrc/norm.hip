@@ -703,6 +703,40 @@ void launch_label_lse(hipStream_t s, const float* logits, int64_t nrows, int64_t
     OMG_HIP(hipGetLastError());
 }
 
+// ------------------------------------------------------ K-chunk fold
+
+// A thread per four floats of one output part; the chunks' loads go out
+// eight at a time, the adds stay in chunk order.
+__global__ __launch_bounds__(256) void fold_chunks_kernel(const float* __restrict__ in, int64_t in_stride,
+                                                          int chunks, int64_t n, float* __restrict__ out,
+                                                          int64_t out_stride) {
+    const int64_t q = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (q >= n / 4) return;
+    const int64_t p = blockIdx.y;
+    const float* base = in + p * chunks * in_stride + 4 * q;
+    float4 acc = *reinterpret_cast<const float4*>(base);
+    for (int c0 = 1; c0 < chunks; c0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (c0 + u < chunks) v[u] = *reinterpret_cast<const float4*>(base + (c0 + u) * in_stride);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (c0 + u < chunks) acc.x += v[u].x, acc.y += v[u].y, acc.z += v[u].z, acc.w += v[u].w;
+    }
+    *reinterpret_cast<float4*>(out + p * out_stride + 4 * q) = acc;
+}
+
+void launch_fold_chunks(hipStream_t s, const float* in, int64_t in_stride, int chunks, int parts, int64_t n,
+                        float* out, int64_t out_stride) {
+    if (n <= 0 || parts <= 0) return;
+    if (n % 4 || chunks < 1 || in_stride % 4 || out_stride % 4 || in_stride < n || out_stride < n)
+        fail(E_INVALID, "fold_chunks: shape");
+    fold_chunks_kernel<<<dim3(unsigned((n / 4 + 255) / 256), unsigned(parts)), dim3(256), 0, s>>>(
+        in, in_stride, chunks, n, out, out_stride);
+    OMG_HIP(hipGetLastError());
+}
+
 // ------------------------------------------------------ pointer readout
 
 // readout.rs:30-36 (PointerHead::project) for the rows that have a map: one

@@ -121,6 +121,28 @@ def test_resident_prefix_matches_full_pass():
             assert all(np.array_equal(x, y) for x, y in zip(a.rows, b.rows))
 
 
+def test_deep_k_chunks_same_rows_in_long_and_short_passes():
+    """A down projection deep enough to sum K in 1,024-wide chunks (width
+    2,304 > 2,048: one split of K 4,096, 4 chunks): the long cold pass folds
+    the chunks in the GEMM's registers, the short warm pass on the resident
+    prefix runs a chunk per workgroup and adds the partials in order —
+    bit-equal rows, and within the f32 oracle's reach."""
+    cfg = gemma3_tiny(d=2304, ff=4096, layers=1, sliding=[False])
+    eng, plain, _, _ = build(cfg, 21, g.Q4, g.F16, capacity=1024)
+    rng = np.random.default_rng(21)
+    prefix = rng.integers(0, 40, 520).tolist()
+    branches = [BranchTokens(rng.integers(0, 40, 12).tolist(), [3, 11]), BranchTokens(rng.integers(0, 40, 9).tolist(), [8])]
+    eng.evict_resident()
+    cold = eng.evaluate(prefix, branches, Want.HIDDEN)  # 541 rows: folded in registers
+    assert eng.prefix_source() == PrefixSource.DECODED
+    warm = eng.evaluate(prefix, branches, Want.HIDDEN)  # 21 rows: a chunk per workgroup
+    assert eng.prefix_source() == PrefixSource.RESIDENT
+    for a, b in zip(cold, warm):
+        assert all(np.array_equal(x, y) for x, y in zip(a.rows, b.rows))
+    ref = oracle_rows(plain, prefix, branches)
+    assert max(rel_diff(x, y) for a, b in zip(cold, ref) for x, y in zip(a.rows, b)) < 2e-2
+
+
 def test_state_cache_restores_exactly(tmp_path):
     """reference.rs:482-522: RAM cache and GRWS1 bytes restore bit-equal rows;
     a foreign model id is refused."""
