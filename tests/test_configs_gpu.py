@@ -137,6 +137,14 @@ def test_c5_4b_q4_full_pass_properties():
               for i, b in enumerate(branches)]
     mixed = eng.evaluate(prefix, others, Want.LABELS, LABELS)
     assert all(np.array_equal(a.rows[0], b.rows[0]) for i, (a, b) in enumerate(zip(cold, mixed)) if i % 2 == 0)
+    # the first questions alone on the resident state (their rows keep their
+    # cache rows): 40- and 120-row passes, whose deep-K down products run a
+    # K chunk per workgroup (the long passes above fold the chunks in
+    # registers) — the same rows
+    for n in (1, 3):
+        few = eng.evaluate(prefix, branches[:n], Want.LABELS, LABELS)
+        assert eng.prefix_source() == g.PrefixSource.RESIDENT
+        assert all(np.array_equal(a.rows[0], b.rows[0]) for a, b in zip(few, cold[:n])), n
     k = 4  # options per question; 4 orders each
     orders = np.array(oracle.option_orders(k, 4))
     logits = np.stack([b.rows[0][:k] for b in cold]).reshape(52, 4, k)
