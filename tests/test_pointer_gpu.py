@@ -12,7 +12,7 @@ import pytest
 
 import grande_amd as g
 import oracle
-from tests.common import build, gemma3_tiny, oracle_rows
+from tests.common import build, gemma3_tiny, gemma4_tiny, oracle_rows
 from grande_amd import BranchTokens, Group, OmgError, PointerHead, Role, Want
 
 pytestmark = pytest.mark.gpu
@@ -47,9 +47,10 @@ def expected(hd: PointerHead, rows_of, roles):
     return out
 
 
-def test_pointer_matches_oracle_on_the_engines_rows_and_the_f32_forward():
+@pytest.mark.parametrize("family", ["gemma3", "gemma4"])
+def test_pointer_matches_oracle_on_the_engines_rows_and_the_f32_forward(family):
     rng = np.random.default_rng(5)
-    cfg = gemma3_tiny()
+    cfg = gemma3_tiny() if family == "gemma3" else gemma4_tiny()
     eng, plain, _, w = build(cfg, 7, g.Q8, g.F16)
     hd = head(rng, 64)
     eng.set_pointer_head(hd)
