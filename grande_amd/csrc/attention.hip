@@ -42,15 +42,16 @@
 
 namespace omg {
 
-// Geometry: A_KT keys per K/V tile, A_NW waves of A_QB 16-row query blocks
-// per work item.
+// Geometry: A_KT keys per K/V tile, NW waves of A_QB 16-row query blocks
+// per work item: A_NW (4) in long passes, 2 in short ones, where twice the
+// items fill more of the chip (a row's sums do not depend on NW, see
+// attention_work).
 constexpr int A_KT = 32;
-constexpr int A_NW = 4;
+constexpr int A_NW = 4;  // the most waves per item (buffers are sized for it)
 // One block per wave measured faster than two on MI355X (two need about 270
 // registers per lane: one wave per SIMD).
 constexpr int A_QB = 1;  // 16-row query blocks per wave
-constexpr int A_THREADS = A_NW * 64;
-constexpr int A_ROWS = A_NW * 16 * A_QB;  // query rows per work item
+constexpr int A_ROWS = A_NW * 16 * A_QB;  // query rows per work item, at most
 constexpr int A_KB = A_KT / 16;    // 16-key MFMA blocks per tile
 constexpr int A_TT = A_KT / 32;    // 32-key MFMA steps of the O product per tile
 static_assert(A_KT == 32 || A_KT == 64, "key tile");
@@ -94,11 +95,11 @@ __device__ inline __amdgpu_buffer_rsrc_t attn_rsrc(const void* base, int64_t byt
 // is applied.  The lane offsets are the same for every tile (the compiler
 // keeps them out of the loop); the tile's position rides in the scalar
 // offset.
-template <int HD>
+template <int HD, int NW>
 struct TileDma {
-    static constexpr int KROW = HD / 8;                       // 16 B chunks per K row
-    static constexpr int KINS = A_KT * HD / 8 / WAVE / A_NW;  // instructions per wave for K
-    static constexpr int VINS = (HD / attn_col_splits<HD>()) * A_KT / 8 / WAVE / A_NW;
+    static constexpr int KROW = HD / 8;                     // 16 B chunks per K row
+    static constexpr int KINS = A_KT * HD / 8 / WAVE / NW;  // instructions per wave for K
+    static constexpr int VINS = (HD / attn_col_splits<HD>()) * A_KT / 8 / WAVE / NW;
 };
 
 // exp2(s log2(e) - m) for a whole-number m (as the integer mi), as
@@ -117,12 +118,13 @@ __device__ inline float prob(float s, int mi) {
     return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(__builtin_amdgcn_fractf(x)), xi - mi);
 }
 
-// One work item per workgroup: A_ROWS query rows (TPW tokens x HPG heads
-// per wave in QB blocks of 16 rows, A_NW waves) against key tiles [tb, te)
+// One work item per workgroup: NW * 16 query rows (TPW tokens x HPG heads
+// per wave in QB blocks of 16 rows, NW waves) against key tiles [tb, te)
 // of the KV head blockIdx.y, output columns [256 z, 256 z + 256) for
 // z = blockIdx.z when HD > 256.
-template <int HD, int HPG>
-__global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const int4* __restrict__ items) {
+template <int HD, int HPG, int NW>
+__global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a, const int4* __restrict__ items) {
+    constexpr int ROWS = NW * 16 * A_QB;  // query rows of the item
     using SM = AttnSmem<HD>;
     constexpr int DS = HD / 32;  // MFMA steps over the head dim
     constexpr int KG = DS < 8 ? DS : 8;  // K fragments in registers at once (per 16-key block)
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     constexpr int VD = HD / NCS;  // output columns of this workgroup
     constexpr int CT = VD / 16;   // 16-wide output column tiles
     constexpr int QB = A_QB, TPQ = 16 / HPG;  // tokens per 16-row block
-    constexpr int TPW = QB * TPQ, TPB = A_NW * TPW;
+    constexpr int TPW = QB * TPQ, TPB = NW * TPW;
     constexpr float LOG2E = 1.4426950408889634f;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     SM& sm = *reinterpret_cast<SM*>(smem_raw);
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 
     const half_t* kbase = a.kc + int64_t(g) * a.cap_pad * HD;
     const half_t* vbase = a.vt + int64_t(g) * (a.cap_pad / 64) * HD * 64;
-    using TD = TileDma<HD>;
+    using TD = TileDma<HD, NW>;
     const int64_t cache_bytes = a.cap_pad * HD * 2;
     // Issue this wave's share of key tile `tile` into buffer `buf`.
     auto issue = [&](int tile, int buf) {
@@ -409,7 +411,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
     // them, and no tile load is in flight after the loop.
     static_assert(VD == 256, "32 lanes per staged row");
     constexpr int SROW = VD + 8;  // staged row, halves
-    static_assert(A_NW * 16 * SROW * 2 <= int(sizeof(SM)), "staging fits the tile buffers");
+    static_assert(NW * 16 * SROW * 2 <= int(sizeof(SM)), "staging fits the tile buffers");
     __syncthreads();
     half_t* stage = reinterpret_cast<half_t*>(smem_raw) + wave * 16 * SROW;
 #pragma unroll
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
                 half4{half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
                       half_t(o[b][c][3] * inv)};
         const int row0 = (wave * QB + b) * 16;  // the block's first row of the item
-        const int64_t prow0 = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row0;
+        const int64_t prow0 = (int64_t(slot) * a.kv_heads + g) * ROWS + row0;
         if (slot >= 0 && G == 0 && ch == 0) {
             // the chunk's max and sum
             a.part_ml[(prow0 + lr) * 2] = m_run[b];
@@ -457,23 +459,24 @@ __global__ __launch_bounds__(A_THREADS) void attention_kernel(AttnArgs a, const 
 // partial row are one contiguous 512-byte wave load.
 // The statistics and partial rows of up to MAXC chunks are loaded together
 // (one round trip after the merge record).
-template <int HD>
+template <int HD, int NW>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const int4* __restrict__ merges) {
+    constexpr int ROWS = NW * 16 * A_QB;  // query rows of a work item
     static_assert(HD == 256 || HD == 512, "half4 column groups per lane");
     constexpr int NQ = HD / 256;
     constexpr int MAXC = 8;  // chunks loaded per round
-    const int4 mg = merges[blockIdx.x / (A_ROWS / 4)];
+    const int4 mg = merges[blockIdx.x / (ROWS / 4)];
     const int qtile = mg.x, slot0 = mg.y, n = mg.z;
     const int g = int(blockIdx.y);
     const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
-    const int row = int(blockIdx.x % (A_ROWS / 4)) * 4 + wave;
+    const int row = int(blockIdx.x % (ROWS / 4)) * 4 + wave;
     // Row r of a work item: 16-row block r / 16 (wave-major), 16 / hpg tokens
     // per block, the lane's token (r % 16) / hpg within it.
-    const int hpg = a.heads / a.kv_heads, tpq = 16 / hpg, tpb = A_NW * A_QB * tpq;
+    const int hpg = a.heads / a.kv_heads, tpq = 16 / hpg, tpb = NW * A_QB * tpq;
     const int64_t tq = int64_t(qtile) * tpb + (row / 16) * tpq + (row % 16) / hpg;
     if (tq >= a.t) return;
     const int head = g * hpg + (row % 16) % hpg;
-    auto base = [&](int c) { return (int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row; };
+    auto base = [&](int c) { return (int64_t(slot0 + c) * a.kv_heads + g) * ROWS + row; };
     // Running merge over rounds of MAXC chunks (one round for n <= MAXC):
     // (M, L, acc) rescaled when a later round raises the max.
     float M = -INFINITY, L = 0.0f;
@@ -539,11 +542,14 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
     }
 }
 
-void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk,
+void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk, int nw,
                     AttnWork& w) {
     w.items.clear();
     w.merges.clear();
-    const int hpg = heads / kv_heads, tpb = A_NW * A_QB * (16 / hpg);
+    if (nw != 2 && nw != A_NW) fail(E_INVALID, "attention_work: waves per item must be 2 or 4");
+    const int hpg = heads / kv_heads, tpb = nw * A_QB * (16 / hpg);
+    w.nw = nw;
+    w.aligned = true;
     int slot = 0;
     // A query tile's key range, one span per group among its tokens (in
     // key order: groups are laid out one after another).  Padding rows
@@ -577,6 +583,7 @@ void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int
         // otherwise from cache row 0 over the tile's whole range.
         bool aligned = true;
         for (const Span& sp : spans) aligned = aligned && sp.row_lo % A_KT == 0;
+        w.aligned = w.aligned && aligned;
         if (!aligned) {
             int64_t lo = INT64_MAX, hi = 0;
             for (const Span& sp : spans) {
@@ -639,21 +646,30 @@ void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int
         for (size_t i = 0; i < runs[size_t(x)].size(); ++i) w.items[i * NXCD + size_t(x)] = runs[size_t(x)][i];
 }
 
-template <int HD, int HPG>
-static void run_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, size_t smem) {
+template <int HD, int HPG, int NW>
+static void run_attention_nw(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, size_t smem) {
     static bool attr_set = false;  // once per instantiation (per process)
     if (!attr_set) {
-        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<HD, HPG>),
+        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<HD, HPG, NW>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));
         attr_set = true;
     }
-    attention_kernel<HD, HPG><<<dim3(unsigned(nitems), unsigned(a.kv_heads), unsigned(attn_col_splits<HD>())),
-                                dim3(A_THREADS), smem, s>>>(a, items);
+    attention_kernel<HD, HPG, NW><<<dim3(unsigned(nitems), unsigned(a.kv_heads), unsigned(attn_col_splits<HD>())),
+                                    dim3(NW * 64), smem, s>>>(a, items);
     OMG_HIP(hipGetLastError());
 }
 
-void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems) {
+template <int HD, int HPG>
+static void run_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, size_t smem, int nw) {
+    if (nw == 2)
+        run_attention_nw<HD, HPG, 2>(s, a, items, nitems, smem);
+    else
+        run_attention_nw<HD, HPG, A_NW>(s, a, items, nitems, smem);
+}
+
+void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, int nw) {
     if (a.t <= 0 || nitems <= 0) return;
+    if (nw != 2 && nw != A_NW) fail(E_INVALID, "attention: waves per item must be 2 or 4");
     if (a.hd != 256 && a.hd != 512) fail(E_INVALID, "attention: head_dim must be 256 or 512");
     if (a.kv_heads <= 0 || a.heads % a.kv_heads) fail(E_INVALID, "attention: heads / kv_heads");
     const int hpg = a.heads / a.kv_heads;
@@ -663,33 +679,37 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
     if (a.hd == 512) {
         const size_t smem = sizeof(AttnSmem<512>);
         switch (hpg) {
-            case 1: run_attention<512, 1>(s, a, items, nitems, smem); break;
-            case 2: run_attention<512, 2>(s, a, items, nitems, smem); break;
-            case 4: run_attention<512, 4>(s, a, items, nitems, smem); break;
-            case 8: run_attention<512, 8>(s, a, items, nitems, smem); break;
-            default: run_attention<512, 16>(s, a, items, nitems, smem); break;
+            case 1: run_attention<512, 1>(s, a, items, nitems, smem, nw); break;
+            case 2: run_attention<512, 2>(s, a, items, nitems, smem, nw); break;
+            case 4: run_attention<512, 4>(s, a, items, nitems, smem, nw); break;
+            case 8: run_attention<512, 8>(s, a, items, nitems, smem, nw); break;
+            default: run_attention<512, 16>(s, a, items, nitems, smem, nw); break;
         }
         return;
     }
     const size_t smem = sizeof(AttnSmem<256>);
     switch (hpg) {
-        case 1: run_attention<256, 1>(s, a, items, nitems, smem); break;
-        case 2: run_attention<256, 2>(s, a, items, nitems, smem); break;
-        case 4: run_attention<256, 4>(s, a, items, nitems, smem); break;
-        case 8: run_attention<256, 8>(s, a, items, nitems, smem); break;
-        default: run_attention<256, 16>(s, a, items, nitems, smem); break;
+        case 1: run_attention<256, 1>(s, a, items, nitems, smem, nw); break;
+        case 2: run_attention<256, 2>(s, a, items, nitems, smem, nw); break;
+        case 4: run_attention<256, 4>(s, a, items, nitems, smem, nw); break;
+        case 8: run_attention<256, 8>(s, a, items, nitems, smem, nw); break;
+        default: run_attention<256, 16>(s, a, items, nitems, smem, nw); break;
     }
 }
 
-void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges) {
+void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges, int nw) {
     if (a.t <= 0 || nmerges <= 0) return;
-    const dim3 grid(unsigned(nmerges * (A_ROWS / 4)), unsigned(a.kv_heads));
-    if (a.hd == 512)
-        attention_merge_kernel<512><<<grid, dim3(256), 0, s>>>(a, merges);
-    else if (a.hd == 256)
-        attention_merge_kernel<256><<<grid, dim3(256), 0, s>>>(a, merges);
+    if (nw != 2 && nw != A_NW) fail(E_INVALID, "attention_merge: waves per item must be 2 or 4");
+    const dim3 grid(unsigned(nmerges * (nw * 16 * A_QB / 4)), unsigned(a.kv_heads));
+    if (a.hd != 512 && a.hd != 256) fail(E_INVALID, "attention_merge: head_dim must be 256 or 512");
+    if (a.hd == 512 && nw == 2)
+        attention_merge_kernel<512, 2><<<grid, dim3(256), 0, s>>>(a, merges);
+    else if (a.hd == 512)
+        attention_merge_kernel<512, A_NW><<<grid, dim3(256), 0, s>>>(a, merges);
+    else if (nw == 2)
+        attention_merge_kernel<256, 2><<<grid, dim3(256), 0, s>>>(a, merges);
     else
-        fail(E_INVALID, "attention_merge: head_dim must be 256 or 512");
+        attention_merge_kernel<256, A_NW><<<grid, dim3(256), 0, s>>>(a, merges);
     OMG_HIP(hipGetLastError());
 }
 

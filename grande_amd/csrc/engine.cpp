@@ -421,6 +421,9 @@ Packed Engine::pack_checked(const GroupIn* groups, int64_t n, int64_t first, boo
     return pk;
 }
 
+// Passes of at most this many tokens run 2-wave attention items.
+constexpr int64_t SHORT_ATTN_ROWS = 1024;
+
 void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     const int64_t t = pk.total - pk.base, nr = int64_t(pk.wanted.size());
     // Everything that can reject the request is checked before the first
@@ -438,10 +441,18 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     if (resident_ && int64_t(resident_->size()) > pk.base) resident_.reset();
     // A captured pass reads the work lists and buffers this upload may move.
     drop_graph();
-    // Attention work lists for both layer types (host only).
-    for (int kind = 0; kind < 2; ++kind)
-        attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), kind == 0 ? int(cfg_.window) : 0,
-                       attn_chunk_[kind], work_[kind]);
+    // Attention work lists for both layer types (host only).  Short passes
+    // run 2-wave items (twice the items: more of the chip busy) when every
+    // query tile is aligned, which keeps each row's chunk boundaries, and
+    // so its sums, those of 4-wave items.
+    for (int kind = 0; kind < 2; ++kind) {
+        const int window = kind == 0 ? int(cfg_.window) : 0;
+        attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind],
+                       t <= SHORT_ATTN_ROWS ? 2 : 4, work_[kind]);
+        if (work_[kind].nw == 2 && !work_[kind].aligned)
+            attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind], 4,
+                           work_[kind]);
+    }
     // The pass's inputs go to the device in two copies: the cache metadata
     // of its rows, and one block [ids | wanted rows | labels | per layer
     // type: work items, merges] (16-byte aligned parts).
@@ -637,10 +648,10 @@ void Engine::forward(int64_t t, int64_t base) {
         att.part_o = part_o_.as<half_t>();
         att.part_ml = part_ml_.as<float>();
         const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
-        step("attention", [&] { launch_attention(stream_, att, d_items_[kind], n_items_[kind]); });
+        step("attention", [&] { launch_attention(stream_, att, d_items_[kind], n_items_[kind], work_[kind].nw); });
         if (n_merges_[kind] > 0)
             step("attention_merge",
-                 [&] { launch_attention_merge(stream_, att, d_merges_[kind], n_merges_[kind]); });
+                 [&] { launch_attention_merge(stream_, att, d_merges_[kind], n_merges_[kind], work_[kind].nw); });
         const SplitPlan po = split_plan(c.heads * hd, d, t), pd = split_plan(ff, d, t);
         const int so = po.splits, sd = pd.splits;
         const int64_t pstride = slots_ * d;

@@ -233,18 +233,25 @@ struct AttnArgs {
 struct AttnWork {
     std::vector<int4> items, merges;
     int slots = 0;
+    int nw = 4;           // waves (16-row query blocks) per work item
+    bool aligned = true;  // every query tile's groups start on a key tile
 };
 // Geometry of the attention work: keys per K/V tile (the unit of chunk and
-// of the items' key tile ranges) and query rows per work item.
+// of the items' key tile ranges) and query rows per work item (at most:
+// 4 waves of 16 rows).
 int attention_key_tile();
 int attention_rows();
 // Build the work of one layer type from the pass's per-token metadata
 // (4 ints per token of this pass, in workspace order).  chunk = key tiles
-// per split (0 = never split).
-void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk,
+// per split (0 = never split); nw = waves per work item (2 or 4).  A row's
+// sums depend on the chunk boundaries alone, which count from its group's
+// first key row when its query tile's groups all start on a key tile
+// (w.aligned) and from cache row 0 otherwise; with every tile aligned they
+// are the same for either nw.
+void attention_work(const int32_t* meta, int64_t t, int heads, int kv_heads, int window, int chunk, int nw,
                     AttnWork& w);
-void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems);
+void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64_t nitems, int nw);
 // The chunk merges of the split query tiles (after launch_attention).
-void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges);
+void launch_attention_merge(hipStream_t s, const AttnArgs& a, const int4* merges, int64_t nmerges, int nw);
 
 }  // namespace omg
