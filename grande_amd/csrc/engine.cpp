@@ -167,6 +167,12 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.slots_ = capacity + (E.align_ - 1) * max_rows;
     E.cap_pad_ = (E.slots_ + 63) / 64 * 64;
     OMG_HIP(hipStreamCreateWithFlags(&E.stream_, hipStreamNonBlocking));
+    {
+        int dev = 0, cus = 0;
+        OMG_HIP(hipGetDevice(&dev));
+        OMG_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        E.cus_ = cus > 0 ? cus : 256;
+    }
     auto take_lin = [&](const std::string& n) { return std::move(linears_.at(n)); };
     auto take_norm = [&](const std::string& n) { return std::move(norms_.at(n)); };
     if (linears_.count("embed") == 0) fail(E_INVALID, "embed must be a 2-D tensor");
@@ -444,14 +450,17 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     // Attention work lists for both layer types (host only).  Short passes
     // run 2-wave items (twice the items: more of the chip busy) when every
     // query tile is aligned, which keeps each row's chunk boundaries, and
-    // so its sums, those of 4-wave items.
+    // so its sums, those of 4-wave items, and when the 2-wave workgroups
+    // number no more than the CUs: an item's K / V buffers take the same
+    // LDS at either width (a CU holds two at head_dim 256, one at 512), so
+    // 2-wave workgroups that have to share CUs run half the waves per CU.
     for (int kind = 0; kind < 2; ++kind) {
         const int window = kind == 0 ? int(cfg_.window) : 0;
+        AttnWork& w = work_[kind];
         attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind],
-                       t <= SHORT_ATTN_ROWS ? 2 : 4, work_[kind]);
-        if (work_[kind].nw == 2 && !work_[kind].aligned)
-            attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind], 4,
-                           work_[kind]);
+                       t <= SHORT_ATTN_ROWS ? 2 : 4, w);
+        if (w.nw == 2 && (!w.aligned || int64_t(w.items.size()) * cfg_.kv_heads > cus_))
+            attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind], 4, w);
     }
     // The pass's inputs go to the device in two copies: the cache metadata
     // of its rows, and one block [ids | wanted rows | labels | per layer

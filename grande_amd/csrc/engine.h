@@ -182,6 +182,7 @@ class Engine {
     // (align_groups), for up to max_rows groups.
     int64_t slots_ = 0, align_ = 1;
     hipStream_t stream_ = nullptr;
+    int64_t cus_ = 256;  // compute units of the device
     DevTensor embed_;
     DevBuf final_norm_;
     struct Layer {
