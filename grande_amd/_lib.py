@@ -25,13 +25,15 @@ class OmgError(RuntimeError):
         self.message = message
 
 
+# The uint32 pointers are declared void* here (same ABI): the wrapper sets
+# them from array addresses, which is much cheaper than typed pointers.
 class omg_branch(C.Structure):
-    _fields_ = [("tokens", C.POINTER(C.c_uint32)), ("ntokens", C.c_size_t),
-                ("want", C.POINTER(C.c_uint32)), ("nwant", C.c_size_t)]
+    _fields_ = [("tokens", C.c_void_p), ("ntokens", C.c_size_t),
+                ("want", C.c_void_p), ("nwant", C.c_size_t)]
 
 
 class omg_group(C.Structure):
-    _fields_ = [("prefix", C.POINTER(C.c_uint32)), ("prefix_len", C.c_size_t),
+    _fields_ = [("prefix", C.c_void_p), ("prefix_len", C.c_size_t),
                 ("branches", C.POINTER(omg_branch)), ("nbranches", C.c_size_t)]
 
 

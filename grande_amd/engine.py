@@ -12,6 +12,7 @@ library's message, where the reference returns anyhow errors.
 from __future__ import annotations
 
 import ctypes as C
+import itertools
 import enum
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -154,7 +155,10 @@ def _u32(xs) -> np.ndarray:
 
 
 class _CGroups:
-    """C views of a list of Groups; keeps the backing arrays alive."""
+    """C views of a list of Groups; keeps the backing arrays alive.  Each
+    group's branch tokens form one array and its wanted rows another; every
+    omg_branch points into them by address (one conversion per group rather
+    than two per branch)."""
 
     def __init__(self, groups: Sequence[Group]):
         self.keep = []
@@ -162,19 +166,34 @@ class _CGroups:
         self.n = len(groups)
         for gi, g in enumerate(groups):
             p = _u32(g.prefix)
-            br = (L.omg_branch * max(1, len(g.branches)))()
-            for bi, b in enumerate(g.branches):
-                t, w = _u32(b.tokens), _u32(b.want)
-                self.keep += [t, w]
-                br[bi].tokens = t.ctypes.data_as(C.POINTER(C.c_uint32))
-                br[bi].ntokens = t.size
-                br[bi].want = w.ctypes.data_as(C.POINTER(C.c_uint32))
-                br[bi].nwant = w.size
-            self.keep += [p, br]
-            self.arr[gi].prefix = p.ctypes.data_as(C.POINTER(C.c_uint32))
-            self.arr[gi].prefix_len = p.size
-            self.arr[gi].branches = br
-            self.arr[gi].nbranches = len(g.branches)
+            nb = len(g.branches)
+            br = (L.omg_branch * max(1, nb))()
+            nt = [len(b.tokens) for b in g.branches]
+            nw = [len(b.want) for b in g.branches]
+            t = _u32_joined([b.tokens for b in g.branches], sum(nt))
+            w = _u32_joined([b.want for b in g.branches], sum(nw))
+            ta, wa = _addr(t), _addr(w)
+            for bi in range(nb):
+                c = br[bi]
+                c.tokens, c.ntokens, c.want, c.nwant = ta, nt[bi], wa, nw[bi]
+                ta += 4 * nt[bi]
+                wa += 4 * nw[bi]
+            self.keep += [p, t, w, br]
+            a = self.arr[gi]
+            a.prefix, a.prefix_len, a.branches, a.nbranches = _addr(p), p.size, br, nb
+
+
+def _u32_joined(seqs: Sequence, total: int) -> np.ndarray:
+    """The sequences one after another as uint32 (as _u32 converts each)."""
+    if total == 0:
+        return np.zeros(1, np.uint32)
+    if all(isinstance(x, np.ndarray) for x in seqs):
+        return _u32(np.concatenate([np.asarray(x, dtype=np.int64).ravel() for x in seqs]))
+    return np.fromiter(itertools.chain.from_iterable(seqs), np.int64, total).astype(np.uint32)
+
+
+def _addr(a: np.ndarray) -> int:
+    return a.__array_interface__["data"][0]
 
 
 class EngineBuilder:
