@@ -273,7 +273,7 @@ class Engine:
         width = {Want.HIDDEN: self.d, Want.LOGITS: self.vocab, Want.LABELS: lab.size,
                  Want.LABELS_LSE: lab.size + 1}[Want(want)]
         rows = sum(len(b.want) for g in groups for b in g.branches)
-        out = np.zeros((max(rows, 1), max(width, 1)), np.float32)
+        out = np.empty((max(rows, 1), max(width, 1)), np.float32)  # every returned row is written
         src = (C.c_int * max(1, len(groups)))()
         L.check(L.lib().omg_evaluate_groups(self._h, cg.arr, cg.n, int(want),
                                             lab.ctypes.data_as(C.POINTER(C.c_uint32)), lab.size,
