@@ -157,6 +157,20 @@ def profiled_traffic(config: str, kernel: str):
     return None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo, as lscpu reports it) and
+    the logical CPUs this process may run on."""
+    name = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return f"{name}; {len(os.sched_getaffinity(0))} logical CPUs available"
+
+
 def c_api_ms(eng, groups, labels, reps: int = 15) -> dict:
     """Medians of the C ABI's omg_evaluate_groups on arguments marshalled
     once (what a compiled caller pays: host ids in, label logits and the
@@ -196,6 +210,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--small-reps", type=int, default=10,
                     help="reps of the small-batch leg (one branch on the resident state, MALL flushed)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="eager launches only (no HIP graph capture or replay): for runs under rocprofv3, whose "
+                         "kernel tracing faulted inside hipGraphLaunch")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device to device three times (calibrates the HBM byte counters)")
     args = ap.parse_args()
@@ -289,10 +306,10 @@ def main() -> int:
 
     eng.evict_resident()
     cold_eager_s = timed(False, args.steps, args.warmup)
-    cold_graph_s = timed(False, args.steps, args.warmup, graph=True)
+    cold_graph_s = cold_eager_s if args.no_graph else timed(False, args.steps, args.warmup, graph=True)
     eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)  # leaves the state resident
     warm_eager_s = timed(True, args.steps, args.warmup)
-    warm_graph_s = timed(True, args.steps, args.warmup, graph=True)
+    warm_graph_s = warm_eager_s if args.no_graph else timed(True, args.steps, args.warmup, graph=True)
     cold_s, warm_s = min(cold_eager_s, cold_graph_s), min(warm_eager_s, warm_graph_s)
 
     # Per-kernel HIP-event times over a second timed region of cold steps,
@@ -320,7 +337,8 @@ def main() -> int:
         one = branches[:1]
         eng.evaluate(prefix, one, Want.LABELS_LSE, labels)  # resident state stays
         eng.prepare([Group(prefix, one)], Want.LABELS_LSE, labels, first_resident=True)
-        eng.graph(True)
+        if not args.no_graph:
+            eng.graph(True)
         eng.launch()
         eng.sync()
         flush = MallFlush(512 << 20)
@@ -401,7 +419,8 @@ def main() -> int:
                                "26 label logits + full-row log-sum-exp readout", "tokens": T, "state_tokens": P, "branches": NB,
                    "branch_tokens": BT},
         "launch": {"cold_eager_ms": round(cold_eager_s * 1e3, 4), "cold_graph_ms": round(cold_graph_s * 1e3, 4),
-                   "warm_eager_ms": round(warm_eager_s * 1e3, 4), "warm_graph_ms": round(warm_graph_s * 1e3, 4)},
+                   "warm_eager_ms": round(warm_eager_s * 1e3, 4), "warm_graph_ms": round(warm_graph_s * 1e3, 4),
+                   "graphs": not args.no_graph},
         "cold_tok_per_s": round(T / cold_s, 1),
         "warm_ms": round(warm_s * 1e3, 4),
         "warm_questions_per_s": round(NB / warm_s, 2),
@@ -455,6 +474,7 @@ def main() -> int:
             dmass = max(dmass, abs(mass_g - mass_c))
             argmax_same &= int(np.argmax(pg)) == int(np.argmax(pc))
         out["cpu_baseline"] = {"value": round(NB / cpu_s, 4), "unit": "questions/s", "cores": threads,
+                               "cpu_model": cpu_model(),
                                "kind": "port", "sample": f"{passes} full cold passes of the same workload ({T} tokens, "
                                f"{mc['layers']} layers) + label readout, f32 C restatement of the reference CPU "
                                f"forward, OpenMP; value from the mean pass", "seconds": round(cpu_s * passes, 3),
@@ -713,7 +733,7 @@ def bench_encoder(args) -> int:
         scores = [orc.score(r) for r in rows]
         cpu_s = time.perf_counter() - t
         worst = max(float(np.max(np.abs(o.logits - sc[0]))) for o, sc in zip(outs, scores))
-        out["cpu_baseline"] = {"value": round(len(sample) / cpu_s, 4), "unit": "questions/s", "cores": threads,
+        out["cpu_baseline"] = {"value": round(len(sample) / cpu_s, 4), "unit": "questions/s", "cores": threads, "cpu_model": cpu_model(),
                                "kind": "port", "sample": f"{len(sample)} of the {nq} questions (256 tokens each, "
                                "22 + 2 layers) + scorer, C restatement with the GPU path's rounding points, OpenMP",
                                "seconds": round(cpu_s, 3), "gpu_speedup": round((nq / step_s) / (len(sample) / cpu_s), 1)}

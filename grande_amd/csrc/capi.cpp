@@ -477,11 +477,13 @@ int omg_dev_label_readout(const omg_weight* embed, const float* rows, int64_t nr
         const hipStream_t s = static_cast<hipStream_t>(stream);
         const int64_t vocab = embed->t.w.rows, nb = omg::logits_blocks(vocab);
         // scratch: the full logits rows, then the per-workgroup partials
-        const size_t bytes = size_t(nrows * vocab) * 4 + size_t(nb * nrows) * 8;
+        // (float2, on an 8-byte boundary)
+        const int64_t nlog = (nrows * vocab + 1) / 2 * 2;
+        const size_t bytes = size_t(nlog) * 4 + size_t(nb * nrows) * 8;
         void* scratch = nullptr;
         OMG_HIP(hipMallocAsync(&scratch, bytes, s));
         float* logits = static_cast<float*>(scratch);
-        float2* part = reinterpret_cast<float2*>(logits + nrows * vocab);
+        float2* part = reinterpret_cast<float2*>(logits + nlog);
         try {
             omg::launch_logits(s, embed->t.w, rows, nrows, nullptr, vocab, softcap, logits, part);
             omg::launch_label_lse(s, logits, nrows, vocab, part, nb, labels, nlabels, out);

@@ -736,6 +736,10 @@ void Engine::readout(const PassPlan& p) {
 Engine::Run Engine::run_pass(const GroupIn* groups, int64_t n, int want, const uint32_t* labels, int64_t nlabels,
                              int64_t out_floats_needed, int64_t out_floats) {
     Run run;
+    // This pass's upload moves the inputs a prepared pass reads (ids, meta,
+    // work lists, labels): that pass is gone, and launching or reading it
+    // fails until the next prepare.
+    prepared_ = PassPlan{};
     auto [first, source] = admit(groups, n);
     run.first = first;
     run.source = source;
@@ -1109,9 +1113,12 @@ void Engine::restore_state(const SavedState& s) {
     size_t total = 0;
     for (const SavedState::Layer& L : s.layers) total += L.bytes.size();
     if (total > h_state_bytes_) fail(E_STATE, "state larger than the staging buffer");
-    // The cache rows change from here on: no prefix is resident until the
-    // restore completes.
+    // The cache rows and their metadata change from here on: no prefix is
+    // resident until the restore completes, and a prepared pass (which may
+    // read those rows) is gone.
     resident_.reset();
+    prepared_ = PassPlan{};
+    drop_graph();
     size_t off = 0;
     for (const SavedState::Layer& L : s.layers) {
         std::memcpy(static_cast<uint8_t*>(h_state_) + off, L.bytes.data(), L.bytes.size());

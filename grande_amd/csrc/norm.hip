@@ -614,7 +614,9 @@ __global__ __launch_bounds__(256) void logits_kernel(DevWeight E, const float* _
         }
         if (row_ok) {
             float* dst = out + (r0 + lr) * ncols + jd;
-            if (jd + 3 < ncols) {
+            // (rows of a width that is not a multiple of 4 start off the
+            // 16-byte grid: those go out as single floats)
+            if (jd + 3 < ncols && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
                 *reinterpret_cast<float4*>(dst) = make_float4(z[0], z[1], z[2], z[3]);
             } else {
 #pragma unroll
@@ -649,6 +651,9 @@ void launch_logits(hipStream_t s, const DevWeight& E, const float* rows, int64_t
                    int64_t ncols, float softcap, float* out, float2* part) {
     if (nrows <= 0 || ncols <= 0) return;
     if (E.cols % 32 != 0) fail(E_INVALID, "logits: width must be a multiple of 32");
+    if (reinterpret_cast<uintptr_t>(rows) % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(part) % 8 != 0)
+        fail(E_INVALID, "logits: rows must be 16-byte aligned, the output 4-byte and the partials 8-byte aligned");
     const dim3 grid(unsigned((ncols + WAVE - 1) / WAVE)), block(256);
     switch (E.dtype) {
         case F16_DT: logits_kernel<F16_DT><<<grid, block, 0, s>>>(E, rows, nrows, cols, ncols, softcap, out, part); break;
@@ -666,6 +671,9 @@ int64_t logits_blocks(int64_t ncols) { return (ncols + WAVE - 1) / WAVE; }
 // lse = M + log(sum_b s_b exp(m_b - M)), in f32 (the reference sums the
 // row in f64 on the host; over 25,000 terms the two agree to a few 1e-7
 // relative).  One workgroup per row, the pairs summed in a fixed order.
+// A label id outside the vocabulary reads nothing and gives NaN (the
+// engine refuses such ids on the host; device-resident ids of the
+// kernel-level entry point are not checked before the launch).
 __global__ __launch_bounds__(256) void label_lse_kernel(const float* __restrict__ logits, int64_t vocab,
                                                         const float2* __restrict__ part, int64_t nblocks,
                                                         int64_t nrows, const uint32_t* __restrict__ labels,
@@ -690,7 +698,10 @@ __global__ __launch_bounds__(256) void label_lse_kernel(const float* __restrict_
     __syncthreads();
     const float* row = logits + r * vocab;
     float* o = out + r * (nlabels + 1);
-    for (int64_t i = tid; i < nlabels; i += 256) o[i] = row[labels[i]];
+    for (int64_t i = tid; i < nlabels; i += 256) {
+        const uint32_t c = labels[i];
+        o[i] = int64_t(c) < vocab ? row[c] : __builtin_nanf("");
+    }
     if (tid == 0) o[nlabels] = m + logf((red[0] + red[1]) + (red[2] + red[3]));
 }
 

@@ -213,7 +213,12 @@ Packed align_groups(const Packed& pk, int64_t align, int64_t rows) {
         out.meta[size_t(4 * j + 3)] = int32_t(row + 1);
     }
     for (const auto& w : pk.wanted) out.wanted.push_back({w[0], w[1], w[2], at[size_t(w[3])]});
-    for (const auto& d : pk.decoded) out.decoded.push_back({d.first, pk.base + at[size_t(d.second - pk.base)]});
+    // A group with no tokens at the end of the pass records the row past
+    // the last token: it maps to the row past the new layout.
+    for (const auto& d : pk.decoded) {
+        const int64_t i = d.second - pk.base;
+        out.decoded.push_back({d.first, pk.base + (i < n ? at[size_t(i)] : used)});
+    }
     return out;
 }
 

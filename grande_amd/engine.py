@@ -66,6 +66,17 @@ class PointerHead:
     w_k: np.ndarray
     b_k: np.ndarray
 
+    def __post_init__(self) -> None:
+        # The library copies dp x d and dp floats from each array: the four
+        # shapes must agree before any pointer is passed.
+        self.w_q, self.b_q, self.w_k, self.b_k = (np.ascontiguousarray(x, np.float32)
+                                                  for x in (self.w_q, self.b_q, self.w_k, self.b_k))
+        if self.w_q.ndim != 2 or self.w_q.shape != self.w_k.shape:
+            raise ValueError(f"pointer head: weight shapes {self.w_q.shape} / {self.w_k.shape}")
+        dp = self.w_q.shape[0]
+        if self.b_q.shape != (dp,) or self.b_k.shape != (dp,):
+            raise ValueError(f"pointer head: bias shapes {self.b_q.shape} / {self.b_k.shape}, expected ({dp},)")
+
     @property
     def dp(self) -> int:
         return int(self.w_q.shape[0])
@@ -112,11 +123,10 @@ class PointerHead:
             return v.reshape(shape)
 
         w_q, b_q, w_k, b_k = (tensor(x) for x in ("q.weight", "q.bias", "k.weight", "k.bias"))
-        if w_q.ndim != 2 or w_q.shape != w_k.shape:
-            raise ValueError(f"head.safetensors: weight shapes {w_q.shape} / {w_k.shape}")
-        if b_q.shape != (w_q.shape[0],) or b_k.shape != (w_q.shape[0],):
-            raise ValueError("head.safetensors: bias shape")
-        return cls(w_q, b_q, w_k, b_k)
+        try:
+            return cls(w_q, b_q, w_k, b_k)
+        except ValueError as e:
+            raise ValueError(f"head.safetensors: {e}") from None
 
 
 @dataclass
@@ -292,7 +302,8 @@ class Engine:
         if head is None:
             L.check(L.lib().omg_set_pointer_head(self._h, 0, 0, None, None, None, None))
             return
-        ts = [np.ascontiguousarray(x, np.float32) for x in (head.w_q, head.b_q, head.w_k, head.b_k)]
+        head.__post_init__()  # fields may have been reassigned since construction
+        ts = [head.w_q, head.b_q, head.w_k, head.b_k]
         ptr = [x.ctypes.data_as(C.POINTER(C.c_float)) for x in ts]
         L.check(L.lib().omg_set_pointer_head(self._h, head.d, head.dp, *ptr))
 

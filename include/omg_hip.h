@@ -218,7 +218,11 @@ int omg_state_check(const uint8_t *bytes, size_t len, const char *model_id, size
 /* Pack + upload one request whose first group's prefix is resident (or not)
  * and keep it for omg_pass_launch, which replays the pass's device work
  * (forward + readout at the wanted rows) on the engine's stream with no host
- * transfer.  omg_sync waits for it. */
+ * transfer.  omg_sync waits for it.  Any evaluate (omg_evaluate_groups,
+ * omg_evaluate_pointer) or omg_restore_state in between uploads over the
+ * prepared pass's inputs and cancels it: omg_pass_launch, omg_pass_graph
+ * and omg_pass_read then fail with "no prepared pass" until the next
+ * omg_pass_prepare. */
 int omg_pass_prepare(omg_engine *e, const omg_group *groups, size_t ngroups, int want,
                      const uint32_t *label_ids, size_t nlabels, int first_resident);
 int omg_pass_launch(omg_engine *e);
@@ -252,16 +256,19 @@ int omg_dev_gemm_geglu(const omg_weight *wg, const omg_weight *wu, const void *x
  * readout.rs:124-146 takes from the row): rows f32 [nrows][d] times the
  * embedding `embed` [vocab][d] in f32, softcap applied when > 0, then per
  * row the logits of the device-resident label ids and the log-sum-exp of
- * the full vocabulary row: out f32 [nrows][nlabels + 1].  The full logits
- * and per-workgroup partials live in scratch device memory the call
- * allocates and frees in stream order. */
+ * the full vocabulary row: out f32 [nrows][nlabels + 1].  `rows` must be
+ * 16-byte aligned.  Label ids must be below vocab; the device-resident ids
+ * are not checked before the launch, and an id past the vocabulary gives
+ * NaN in its column.  The full logits and per-workgroup partials live in
+ * scratch device memory the call allocates and frees in stream order. */
 int omg_dev_label_readout(const omg_weight *embed, const float *rows, int64_t nrows, const uint32_t *labels,
                           int64_t nlabels, float softcap, float *out, void *stream);
 /* No counterpart in the reference.  omg_dev_label_readout for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops):
  * same arguments and results, nothing allocated; its scratch is a fixed
  * 16 MiB device array per GPU (4,194,304 floats), which must hold
- * nrows * vocab + 2 * nrows * ceil(vocab / 64) floats, else OMG_E_CAPACITY.
+ * nrows * vocab (rounded up to even) + 2 * nrows * ceil(vocab / 64) floats,
+ * else OMG_E_CAPACITY.
  * Calls that overlap on one GPU share that array and race. */
 int omg_dev_label_readout_noalloc(const omg_weight *embed, const float *rows, int64_t nrows, const uint32_t *labels,
                                   int64_t nlabels, float softcap, float *out, void *stream);

@@ -8,6 +8,7 @@ import pytest
 
 import grande_amd as g
 import oracle
+from grande_amd import _lib as L
 from grande_amd import BranchTokens, Group, PrefixSource, Want
 from tests.common import (assert_close, build, gemma3_tiny, gguf_tiny, oracle_rows, rel_diff, tiled_oracle,
                           worst_rel)
@@ -534,3 +535,35 @@ def test_graph_replay_matches_eager_pass():
     eng.launch()
     short = eng.read_prepared(1 << 12)
     assert not np.array_equal(short, eager)
+
+
+def test_evaluate_cancels_a_prepared_pass():
+    """A prepared pass reads inputs that any evaluate or state restore
+    uploads over: after one, launching, capturing or reading the prepared
+    pass is refused ("no prepared pass") until the next prepare, and the
+    engine still answers correctly."""
+    eng, _, _, _ = build(gguf_tiny(8, 2, window=9), 43, g.Q4, g.Q8, capacity=256, oracle_models=False)
+    rng = np.random.default_rng(8)
+    prefix = rng.integers(0, 64, 40).tolist()
+    branches = [BranchTokens(rng.integers(0, 64, n).tolist(), [n - 1]) for n in (5, 7)]
+    labels = [3, 9, 27]
+    ref = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
+    saved = eng.save_state(prefix, "t")
+    for interrupt in ("evaluate", "restore", "pointer-free evaluate without labels"):
+        eng.evict_resident()
+        eng.prepare([Group(prefix, branches)], Want.LABELS_LSE, labels)
+        eng.launch()
+        assert np.array_equal(eng.read_prepared(64).reshape(2, 4), np.stack([b.rows[0] for b in ref]))
+        if interrupt == "evaluate":
+            eng.evaluate(prefix[:7], branches[:1], Want.LABELS_LSE, labels[:1])
+        elif interrupt == "restore":
+            eng.restore_state(saved, "t")
+        else:
+            eng.evaluate([1, 2], [BranchTokens([3], [0])], Want.HIDDEN)
+        for call in (eng.launch, lambda: eng.graph(True), lambda: eng.read_prepared(64)):
+            with pytest.raises(L.OmgError, match="no prepared pass"):
+                call()
+    eng.evict_resident()
+    again = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
+    for a, b in zip(ref, again):
+        assert np.array_equal(a.rows[0], b.rows[0])

@@ -67,7 +67,8 @@ def engine_of(cfg: str, ts, capacity: int, max_rows: int = 16) -> g.Engine:
     return b.finish(capacity, max_rows)
 
 
-def check_chaotic(out, cfg: str, ts, prefix, branches, capacity: int, what: str):
+def check_chaotic(out, cfg: str, ts, prefix, branches, capacity: int, what: str, tiled_bar: float,
+                  f32_bar: float | None = None):
     """Rows of a long-prefix Gemma 4 pass on the reference's own weight
     distribution.  With query scale 1 and normed q / k over 256 / 512 dims
     the scores reach several tens and near-ties between keys are common
@@ -75,18 +76,24 @@ def check_chaotic(out, cfg: str, ts, prefix, branches, capacity: int, what: str)
     layer: the three CPU forwards that differ only in where they round
     (f32, f16 operands, f16 operands + the flash kernel's rounding) sit up
     to 4e-2 apart here (`rounding_spread`), beyond the reference's 2e-2 bar
-    that holds on its short-prefix tests.  The GPU rows must stay within
-    twice that spread of every one of them, so a real defect (O(1) errors,
-    a lost mask or window) still fails; the depth-limited cases in
+    that holds on its short-prefix tests.  The forward with the kernel's
+    own rounding points is held to a fixed bar (`tiled_bar`); the f32
+    forward to `f32_bar` when given (the reference's 2e-2 where the spread
+    allows it) and the f32 / f16-operand forwards otherwise within twice
+    the CPU spread, so a real defect (O(1) errors, a lost mask or window)
+    fails either way; the depth-limited cases in
     test_gemma4_long_prefix_by_depth hold the reference's 2e-2 bar."""
     f32, f16, tiled, spread = rounding_spread(cfg, ts, prefix, branches, capacity)
     hip = [o.rows for o in out]
     d = {k: worst_rel(hip, v) for k, v in (("f32", f32), ("f16", f16), ("tiled", tiled))}
     print(f"{what}: CPU rounding spread {spread:.2e}; GPU vs f32 {d['f32']:.2e}, "
           f"vs f16 operands {d['f16']:.2e}, vs kernel rounding {d['tiled']:.2e}")
+    assert d["tiled"] < tiled_bar, f"{what}: {d['tiled']} from the kernel-rounding forward (bar {tiled_bar})"
+    if f32_bar is not None:
+        assert d["f32"] < f32_bar, f"{what}: {d['f32']} from the f32 forward (bar {f32_bar})"
     bound = max(2e-2, 2.0 * spread)
-    for k, v in d.items():
-        assert v < bound, f"{what}: {v} from the {k} forward (bound {bound})"
+    for k in ("f32", "f16"):
+        assert d[k] < bound, f"{what}: {d[k]} from the {k} forward (bound {bound})"
 
 
 @pytest.mark.parametrize("capacity", [1024, 8192])
@@ -95,14 +102,17 @@ def test_gemma4_long_prefix_global_key_ranges(capacity, heads, kv):
     """A 700-token prefix on the reference's gemma4 configs and weights
     (reference.rs:66-104, 108-139): at capacity 1024 the head_dim-512 global
     layers' key ranges are cut into 512-key chunks and merged, at 8192 they
-    are not (1024-key chunks)."""
+    are not (1024-key chunks).  Four layers deep the GPU rows stay within
+    1.2e-2 of the forward with the kernel's own rounding points (measured
+    6.4e-3 .. 9.2e-3)."""
     rng = np.random.default_rng(4)
     prefix = rng.integers(0, 64, 700).tolist()
     branches = [BranchTokens(rng.integers(0, 64, 37).tolist(), [0, 20, 36]) for _ in range(3)]
     cfg = gemma4_tiny(heads, kv)
     ts = list(g.Weights.synth(cfg, 13, g.Q4, g.Q8).tensors())
     out = engine_of(cfg, ts, capacity).evaluate(prefix, branches, Want.HIDDEN)
-    check_chaotic(out, cfg, ts, prefix, branches, capacity, f"{heads}/{kv} heads, capacity {capacity}")
+    check_chaotic(out, cfg, ts, prefix, branches, capacity, f"{heads}/{kv} heads, capacity {capacity}",
+                  tiled_bar=1.2e-2)
 
 
 @pytest.mark.parametrize("layers", [1, 2])
@@ -195,11 +205,14 @@ def test_gemma4_open_dir_loads_the_per_layer_table(tmp_path):
 def test_gemma4_every_head_grouping(heads, kv):
     """Every query-heads-per-K/V-head grouping of the head_dim 256 and 512
     kernels (1, 2, 8, 16 per group; 4 is covered above), on a prefix long
-    enough for split key ranges, on the reference's weight distribution."""
+    enough for split key ranges, on the reference's weight distribution:
+    the reference's 2e-2 bar against the f32 forward (measured 3.3e-3 ..
+    7.4e-3) and the same bar against the kernel-rounding forward (measured
+    3.3e-3 .. 1.3e-2)."""
     rng = np.random.default_rng(6)
     prefix = rng.integers(0, 64, 300).tolist()
     branches = [BranchTokens(rng.integers(0, 64, 21).tolist(), [0, 20]) for _ in range(2)]
     cfg = gemma4_tiny(heads, kv)
     ts = list(g.Weights.synth(cfg, 29, g.Q4, g.Q8).tensors())
     out = engine_of(cfg, ts, 512).evaluate(prefix, branches, Want.HIDDEN)
-    check_chaotic(out, cfg, ts, prefix, branches, 512, f"{heads}/{kv} heads")
+    check_chaotic(out, cfg, ts, prefix, branches, 512, f"{heads}/{kv} heads", tiled_bar=2e-2, f32_bar=2e-2)

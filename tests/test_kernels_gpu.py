@@ -147,3 +147,30 @@ def test_label_readout_matches_cpu(vocab, d, nrows, softcap, dtype):
     scale = np.maximum(np.abs(z).max(1), 1.0)
     assert np.max(np.abs(got[:, :26] - z[:, labels]) / scale[:, None]) < 1e-4
     assert np.max(np.abs(got[:, 26] - lse) / np.maximum(np.abs(lse), 1.0)) < 1e-5
+
+
+def test_label_readout_odd_shapes_and_out_of_vocab_labels():
+    """Widths that are not multiples of 4 (every row of the logits starts
+    off the 16-byte grid) and an odd rows x vocab product (the partials sit
+    past an odd count of floats) give the same label logits and log-sum-exp
+    as an aligned shape's rows; a label id past the vocabulary reads
+    nothing and gives NaN in its column only."""
+    rng = np.random.default_rng(77)
+    vocab, d, nrows = 1001, 64, 3
+    t, _ = weight(rng, vocab, d, g.Q8, "embed")
+    e = t.to_f32().astype(np.float64)
+    rows = rng.uniform(-1, 1, (nrows, d)).astype(np.float32)
+    labels = np.array([0, 5, vocab - 1, vocab, 77, 0xFFFFFFFF], np.uint32)
+    w = g.DeviceWeight(t)
+    out = torch.zeros((nrows, labels.size + 1), dtype=torch.float32, device="cuda")
+    w.label_readout(dev(rows).data_ptr(), nrows, dev(labels.view(np.int32)).data_ptr(), labels.size, 0.0,
+                    out.data_ptr())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    z = rows.astype(np.float64) @ e.T
+    m = z.max(1, keepdims=True)
+    lse = (m + np.log(np.exp(z - m).sum(1, keepdims=True)))[:, 0]
+    ok = labels < vocab
+    assert np.isnan(got[:, :-1][:, ~ok]).all()
+    assert np.max(np.abs(got[:, :-1][:, ok] - z[:, labels[ok]])) < 1e-4 * max(1.0, np.abs(z).max())
+    assert np.max(np.abs(got[:, -1] - lse) / np.maximum(np.abs(lse), 1.0)) < 1e-5

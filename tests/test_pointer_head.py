@@ -65,3 +65,23 @@ def test_head_refusals():
     bad = dict(t, **{"q.bias": np.zeros(3)})
     with pytest.raises(ValueError, match="bias shape"):
         g.PointerHead.load(bf16_file(bad))
+
+
+def test_head_shapes_are_checked_on_construction():
+    """A head built from arrays directly is held to the file reader's shape
+    rules before any pointer reaches the library: W_q and W_k [dp, d], both
+    biases [dp]."""
+    rng = np.random.default_rng(3)
+    a = arrays(rng)
+    ok = g.PointerHead(a["q.weight"], a["q.bias"], a["k.weight"], a["k.bias"])
+    assert (ok.d, ok.dp) == (6, 4) and ok.w_q.dtype == np.float32 and ok.w_q.flags.c_contiguous
+    bad = [
+        (a["q.weight"], a["q.bias"], a["k.weight"][:, :5], a["k.bias"]),  # W_k narrower
+        (a["q.weight"], a["q.bias"], a["k.weight"][:3], a["k.bias"]),     # W_k shorter
+        (a["q.weight"], a["q.bias"][:3], a["k.weight"], a["k.bias"]),     # b_q short
+        (a["q.weight"], a["q.bias"], a["k.weight"], np.zeros(5)),        # b_k long
+        (a["q.weight"].ravel(), a["q.bias"], a["k.weight"].ravel(), a["k.bias"]),  # not 2-D
+    ]
+    for args in bad:
+        with pytest.raises(ValueError, match="pointer head"):
+            g.PointerHead(*args)

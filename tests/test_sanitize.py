@@ -136,3 +136,42 @@ def test_config_and_manifest_mutations_under_sanitizers(harness, tmp_path):
         args.append(f"config:{p}")
     lines = run(harness, args)
     assert lines[0].startswith("ok") and lines[1].startswith("ok"), lines[:2]
+
+
+def test_packing_under_sanitizers(harness, tmp_path):
+    """pack_groups + align_groups on request shapes with empty prefixes,
+    empty groups (also last) and branchless groups, at both alignments:
+    every index the layout records stays inside it."""
+    def req(groups, first=0, resident=False, align=32):
+        return {"first": first, "resident": resident, "align": align, "rows": 1 << 20,
+                "groups": [{"prefix": p, "branches": [{"tokens": t, "want": w} for t, w in bs]} for p, bs in groups]}
+
+    shapes = [
+        [([1, 2, 3, 4, 5], [([6, 7, 8], [2])]), ([1, 2, 3], []), ([], [])],  # empty last group
+        [([], [([4, 5], [1])]), ([], []), ([9], [([3], [0])])],
+        [([], []), ([1, 2], [([3], [0])])],
+        [([7] * 40, [([1] * 33, [0, 32])]), ([], []), ([], [])],
+    ]
+    rnd = random.Random(21)
+    for _ in range(60):
+        gs = []
+        for _ in range(rnd.randint(1, 5)):
+            p = [rnd.randrange(100) for _ in range(rnd.choice([0, 0, 1, 3, 33, 70]))]
+            bs = []
+            for _ in range(rnd.choice([0, 1, 2, 3])):
+                n = rnd.choice([1, 2, 17, 40])
+                bs.append(([rnd.randrange(100) for _ in range(n)], sorted({rnd.randrange(n) for _ in range(2)})))
+            gs.append((p, bs))
+        shapes.append(gs)
+    args = []
+    for i, gs in enumerate(shapes):
+        for align in (32, 64):
+            for resident in (False, True):
+                p = tmp_path / f"r{i}_{align}_{int(resident)}.json"
+                p.write_text(json.dumps(req(gs, first=i % len(gs), resident=resident, align=align)))
+                args.append(f"pack:{p}")
+    lines = run(harness, args)
+    # a request whose tokens are all empty is refused ("empty request"); the rest pack
+    assert sum(line.startswith("ok") for line in lines) > len(lines) // 2
+    assert all(line.startswith("ok") or "empty request" in line for line in lines), \
+        [line for line in lines if not line.startswith("ok")][:3]
