@@ -88,7 +88,8 @@ def test_gemm_rows_are_independent_of_m():
     outs = []
     for m in (2384, 384, 17, 1):
         y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
-        w.gemm(dev(x[:m]).data_ptr(), k, m, y.data_ptr(), n)
+        xd = dev(x[:m])  # held until the launch has run
+        w.gemm(xd.data_ptr(), k, m, y.data_ptr(), n)
         torch.cuda.synchronize()
         outs.append(y.cpu().numpy())
     for o in outs[1:]:
@@ -163,8 +164,8 @@ def test_label_readout_odd_shapes_and_out_of_vocab_labels():
     labels = np.array([0, 5, vocab - 1, vocab, 77, 0xFFFFFFFF], np.uint32)
     w = g.DeviceWeight(t)
     out = torch.zeros((nrows, labels.size + 1), dtype=torch.float32, device="cuda")
-    w.label_readout(dev(rows).data_ptr(), nrows, dev(labels.view(np.int32)).data_ptr(), labels.size, 0.0,
-                    out.data_ptr())
+    rd, lab = dev(rows), dev(labels.view(np.int32))  # held until the launch has run
+    w.label_readout(rd.data_ptr(), nrows, lab.data_ptr(), labels.size, 0.0, out.data_ptr())
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     z = rows.astype(np.float64) @ e.T
