@@ -167,6 +167,15 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.slots_ = capacity + (E.align_ - 1) * max_rows;
     E.cap_pad_ = (E.slots_ + 63) / 64 * 64;
     OMG_HIP(hipStreamCreateWithFlags(&E.stream_, hipStreamNonBlocking));
+    // The sub-pass streams (default priority, like stream_) and their
+    // fork / join / K/V-ready events (no timing).
+    E.sub_stream_[0] = E.stream_;
+    for (int k = 1; k < Engine::MAX_SUB; ++k)
+        OMG_HIP(hipStreamCreateWithFlags(&E.sub_stream_[k], hipStreamNonBlocking));
+    OMG_HIP(hipEventCreateWithFlags(&E.ev_fork_, hipEventDisableTiming));
+    for (int k = 0; k < Engine::MAX_SUB; ++k) OMG_HIP(hipEventCreateWithFlags(&E.ev_join_[k], hipEventDisableTiming));
+    E.ev_kv_.assign(size_t(Engine::MAX_SUB * cfg_.layers), nullptr);
+    for (hipEvent_t& ev : E.ev_kv_) OMG_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     {
         int dev = 0, cus = 0;
         OMG_HIP(hipGetDevice(&dev));
@@ -310,11 +319,19 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
 // ---------------------------------------------------------------- engine
 
 Engine::~Engine() {
-    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (hipStream_t s : sub_stream_)
+        if (s) (void)hipStreamSynchronize(s);
     if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-    for (Timed& t : pending_) (void)hipEventDestroy(t.e);
+    for (auto& list : pending_)
+        for (Timed& t : list) (void)hipEventDestroy(t.e);
     for (hipEvent_t ev : event_pool_) (void)hipEventDestroy(ev);
-    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (hipEvent_t ev : ev_kv_)
+        if (ev) (void)hipEventDestroy(ev);
+    for (hipEvent_t ev : ev_join_)
+        if (ev) (void)hipEventDestroy(ev);
+    if (ev_fork_) (void)hipEventDestroy(ev_fork_);
+    for (int k = 1; k < MAX_SUB; ++k)
+        if (sub_stream_[k]) (void)hipStreamDestroy(sub_stream_[k]);
     if (h_in_) (void)hipHostFree(h_in_);
     if (h_out_) (void)hipHostFree(h_out_);
     if (h_ptr_) (void)hipHostFree(h_ptr_);
@@ -322,11 +339,11 @@ Engine::~Engine() {
     if (stream_) (void)hipStreamDestroy(stream_);
 }
 
-// Measurement mode: one event after each launch; a launch's time is the
-// interval since the previous event of the same sequence, so back-to-back
-// launches pay for one event each rather than two.
+// Measurement mode: one event after each launch on its range's stream; a
+// launch's time is the interval since the previous event of the same
+// stream, so back-to-back launches pay for one event each rather than two.
 template <class F>
-void Engine::step(const char* name, F&& f) {
+void Engine::step(const char* name, int k, F&& f) {
     if (!profile_) {
         f();
         return;
@@ -343,27 +360,31 @@ void Engine::step(const char* name, F&& f) {
         event_pool_.pop_back();
         return e;
     };
-    if (pending_.empty()) {
+    const hipStream_t s = sub_stream_[k];
+    std::vector<Timed>& pend = pending_[k];
+    if (pend.empty()) {
         const hipEvent_t start = ev();
-        OMG_HIP(hipEventRecord(start, stream_));
-        pending_.push_back(Timed{nullptr, start});
+        OMG_HIP(hipEventRecord(start, s));
+        pend.push_back(Timed{nullptr, start});
     }
     f();
     const hipEvent_t end = ev();
-    OMG_HIP(hipEventRecord(end, stream_));
-    pending_.push_back(Timed{name, end});
+    OMG_HIP(hipEventRecord(end, s));
+    pend.push_back(Timed{name, end});
 }
 
 void Engine::collect_profile() {
-    for (size_t i = 1; i < pending_.size(); ++i) {
-        float ms = 0.0f;
-        OMG_HIP(hipEventElapsedTime(&ms, pending_[i - 1].e, pending_[i].e));
-        auto& tot = totals_[pending_[i].name];
-        tot.first += 1;
-        tot.second += double(ms);
+    for (auto& pend : pending_) {
+        for (size_t i = 1; i < pend.size(); ++i) {
+            float ms = 0.0f;
+            OMG_HIP(hipEventElapsedTime(&ms, pend[i - 1].e, pend[i].e));
+            auto& tot = totals_[pend[i].name];
+            tot.first += 1;
+            tot.second += double(ms);
+        }
+        for (Timed& t : pend) event_pool_.push_back(t.e);
+        pend.clear();
     }
-    for (Timed& t : pending_) event_pool_.push_back(t.e);
-    pending_.clear();
 }
 
 void Engine::set_profile(bool on) {
@@ -384,8 +405,9 @@ std::string Engine::profile_report() const {
 }
 
 void Engine::sync() {
+    // (every pass joins its ranges' streams into stream_)
     OMG_HIP(hipStreamSynchronize(stream_));
-    if (!pending_.empty()) collect_profile();
+    collect_profile();
 }
 
 std::pair<int64_t, int64_t> Engine::state_rows(int64_t layer, int64_t p) const {
@@ -429,6 +451,15 @@ Packed Engine::pack_checked(const GroupIn* groups, int64_t n, int64_t first, boo
 
 // Passes of at most this many tokens run 2-wave attention items.
 constexpr int64_t SHORT_ATTN_ROWS = 1024;
+// Rows per sub-pass range, at least (Engine::Sub).  Measured (same box):
+// the 4B model's 16,320-token pass in three ranges 169.9 -> 159.0 ms, its
+// 8,320-row warm pass in two 96.3 -> 91.9 ms; the 270M model's 2,384-token
+// pass in two ranges 0.5% slower, in three 6% slower (its kernels are too
+// short for the overlap to pay).
+constexpr int64_t SUB_ROWS = 4096;
+// Passes of at most this many rows run deep-K products a chunk per
+// workgroup (split_plan).
+constexpr int64_t CHUNKED_ROWS = 512;
 
 void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     const int64_t t = pk.total - pk.base, nr = int64_t(pk.wanted.size());
@@ -447,24 +478,61 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     if (resident_ && int64_t(resident_->size()) > pk.base) resident_.reset();
     // A captured pass reads the work lists and buffers this upload may move.
     drop_graph();
-    // Attention work lists for both layer types (host only).  Short passes
-    // run 2-wave items (twice the items: more of the chip busy) when every
+    // Row ranges (Engine::Sub): at least SUB_ROWS rows each, at most
+    // MAX_SUB, cut where a cache row is a multiple of 64 (no V^T tile of the
+    // cache holds rows of two ranges), each longer than CHUNKED_ROWS (no
+    // range takes the short passes' one-chunk-per-workgroup products, whose
+    // partials share one area).  One range while profiling: the kernels'
+    // times are then those of the pass's launches alone.
+    int ns = profile_ ? 1 : int(std::min<int64_t>(MAX_SUB, std::max<int64_t>(1, t / SUB_ROWS)));
+    for (; ns > 1; --ns) {
+        bool ok = true;
+        int64_t prev = 0;
+        for (int k = 1; k <= ns; ++k) {
+            const int64_t r = k == ns ? t : ((pk.base + k * t / ns + 63) / 64 * 64 - pk.base);
+            ok = ok && r - prev > CHUNKED_ROWS && (k == ns || (pk.base + r) % 64 == 0);
+            sub_[k - 1].r0 = prev;
+            sub_[k - 1].r1 = r;
+            prev = r;
+        }
+        if (ok) break;
+    }
+    if (ns == 1) {
+        sub_[0].r0 = 0;
+        sub_[0].r1 = t;
+    }
+    nsub_ = ns;
+    // Attention work lists per range and layer type.  Short ranges run
+    // 2-wave items (twice the items: more of the chip busy) when every
     // query tile is aligned, which keeps each row's chunk boundaries, and
     // so its sums, those of 4-wave items, and when the 2-wave workgroups
     // number no more than the CUs: an item's K / V buffers take the same
     // LDS at either width (a CU holds two at head_dim 256, one at 512), so
     // 2-wave workgroups that have to share CUs run half the waves per CU.
-    for (int kind = 0; kind < 2; ++kind) {
-        const int window = kind == 0 ? int(cfg_.window) : 0;
-        AttnWork& w = work_[kind];
-        attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind],
-                       t <= SHORT_ATTN_ROWS ? 2 : 4, w);
-        if (w.nw == 2 && (!w.aligned || int64_t(w.items.size()) * cfg_.kv_heads > cus_))
-            attention_work(pk.meta.data(), t, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind], 4, w);
+    // The ranges' chunk partials take disjoint slots (they run at once).
+    int64_t slots = 0;
+    for (int k = 0; k < ns; ++k) {
+        Sub& sb = sub_[k];
+        const int64_t rt = sb.r1 - sb.r0;
+        int64_t most = 0;
+        for (int kind = 0; kind < 2; ++kind) {
+            const int window = kind == 0 ? int(cfg_.window) : 0;
+            AttnWork& w = sb.work[kind];
+            const int32_t* meta = pk.meta.data() + 4 * sb.r0;
+            attention_work(meta, rt, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind],
+                           rt <= SHORT_ATTN_ROWS ? 2 : 4, w);
+            if (w.nw == 2 && (!w.aligned || int64_t(w.items.size()) * cfg_.kv_heads > cus_))
+                attention_work(meta, rt, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind], 4, w);
+            for (int4& it : w.items)
+                if (it.w >= 0) it.w += int(slots);
+            for (int4& m : w.merges) m.y += int(slots);
+            most = std::max<int64_t>(most, w.slots);
+        }
+        slots += most;
     }
     // The pass's inputs go to the device in two copies: the cache metadata
-    // of its rows, and one block [ids | wanted rows | labels | per layer
-    // type: work items, merges] (16-byte aligned parts).
+    // of its rows, and one block [ids | wanted rows | labels | per range and
+    // layer type: work items, merges] (16-byte aligned parts).
     auto a16 = [](size_t n) { return (n + 15) / 16 * 16; };
     size_t in_bytes = 0;
     auto part = [&](size_t n) {
@@ -473,14 +541,15 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         return o;
     };
     const size_t o_ids = part(size_t(t) * 4), o_wanted = part(size_t(nr) * 4), o_labels = part(size_t(nlabels) * 4);
-    size_t o_items[2], o_merges[2];
-    for (int kind = 0; kind < 2; ++kind) {
-        o_items[kind] = part(work_[kind].items.size() * 16);
-        o_merges[kind] = part(work_[kind].merges.size() * 16);
-    }
+    size_t o_items[MAX_SUB][2], o_merges[MAX_SUB][2];
+    for (int k = 0; k < ns; ++k)
+        for (int kind = 0; kind < 2; ++kind) {
+            o_items[k][kind] = part(sub_[k].work[kind].items.size() * 16);
+            o_merges[k][kind] = part(sub_[k].work[kind].merges.size() * 16);
+        }
     const size_t meta_bytes = a16(size_t(t) * 16);
     // The previous pass may still read the staging buffer; from here the
-    // stream is idle, so buffers can grow.
+    // stream is idle (its ranges' streams joined it), so buffers can grow.
     OMG_HIP(hipStreamSynchronize(stream_));
     if (meta_bytes + in_bytes > h_in_bytes_) {
         OMG_HIP(hipHostFree(h_in_));
@@ -493,16 +562,11 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         in_ = DevBuf(in_bytes * 2);
         in_bytes_ = in_bytes * 2;
     }
-    for (int kind = 0; kind < 2; ++kind) {
-        const AttnWork& w = work_[kind];
-        if (w.slots > part_slots_) {
-            part_slots_ = w.slots;
-            const size_t rows = size_t(part_slots_ * cfg_.kv_heads * attention_rows());
-            part_o_ = DevBuf(rows * size_t(cfg_.max_head_dim()) * 2);
-            part_ml_ = DevBuf(rows * 2 * 4);
-        }
-        n_items_[kind] = int64_t(w.items.size());
-        n_merges_[kind] = int64_t(w.merges.size());
+    if (slots > part_slots_) {
+        part_slots_ = slots;
+        const size_t rows = size_t(part_slots_ * cfg_.kv_heads * attention_rows());
+        part_o_ = DevBuf(rows * size_t(cfg_.max_head_dim()) * 2);
+        part_ml_ = DevBuf(rows * 2 * 4);
     }
     uint8_t* h = static_cast<uint8_t*>(h_in_);
     std::memcpy(h, pk.meta.data(), size_t(t) * 16);
@@ -511,21 +575,26 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     int32_t* w = reinterpret_cast<int32_t*>(hb + o_wanted);
     for (int64_t r = 0; r < nr; ++r) w[r] = int32_t(pk.wanted[size_t(r)][3]);
     if (nlabels > 0) std::memcpy(hb + o_labels, labels, size_t(nlabels) * 4);
-    for (int kind = 0; kind < 2; ++kind) {
-        const AttnWork& wk = work_[kind];
-        if (!wk.items.empty()) std::memcpy(hb + o_items[kind], wk.items.data(), wk.items.size() * 16);
-        if (!wk.merges.empty()) std::memcpy(hb + o_merges[kind], wk.merges.data(), wk.merges.size() * 16);
-    }
+    for (int k = 0; k < ns; ++k)
+        for (int kind = 0; kind < 2; ++kind) {
+            const AttnWork& wk = sub_[k].work[kind];
+            if (!wk.items.empty()) std::memcpy(hb + o_items[k][kind], wk.items.data(), wk.items.size() * 16);
+            if (!wk.merges.empty()) std::memcpy(hb + o_merges[k][kind], wk.merges.data(), wk.merges.size() * 16);
+        }
     OMG_HIP(hipMemcpyAsync(meta_.as<uint8_t>() + pk.base * 16, h, size_t(t) * 16, hipMemcpyHostToDevice, stream_));
     OMG_HIP(hipMemcpyAsync(in_.p, hb, in_bytes, hipMemcpyHostToDevice, stream_));
     uint8_t* d = in_.as<uint8_t>();
     d_ids_ = reinterpret_cast<const uint32_t*>(d + o_ids);
     d_wanted_ = reinterpret_cast<const int32_t*>(d + o_wanted);
     d_labels_ = reinterpret_cast<const uint32_t*>(d + o_labels);
-    for (int kind = 0; kind < 2; ++kind) {
-        d_items_[kind] = reinterpret_cast<const int4*>(d + o_items[kind]);
-        d_merges_[kind] = reinterpret_cast<const int4*>(d + o_merges[kind]);
-    }
+    for (int k = 0; k < ns; ++k)
+        for (int kind = 0; kind < 2; ++kind) {
+            Sub& sb = sub_[k];
+            sb.d_items[kind] = reinterpret_cast<const int4*>(d + o_items[k][kind]);
+            sb.d_merges[kind] = reinterpret_cast<const int4*>(d + o_merges[k][kind]);
+            sb.n_items[kind] = int64_t(sb.work[kind].items.size());
+            sb.n_merges[kind] = int64_t(sb.work[kind].merges.size());
+        }
 }
 
 // K splits of the o / down products (output width n <= 2048): their tiles
@@ -558,7 +627,6 @@ static int ksplit(int64_t k, int64_t n) {
 // the pass.
 constexpr int KFOLD_STAGES = 16;
 constexpr int64_t KFOLD_K = 64 * KFOLD_STAGES, KFOLD_MIN_K = 4096;
-constexpr int64_t CHUNKED_ROWS = 512;  // passes of at most this many rows run a chunk per workgroup
 
 Engine::SplitPlan Engine::split_plan(int64_t k, int64_t n, int64_t t) const {
     SplitPlan p;
@@ -574,147 +642,187 @@ Engine::SplitPlan Engine::split_plan(int64_t k, int64_t n, int64_t t) const {
     return p;
 }
 
-// y = x . W^T into the split partials a_ + z * slots_ * d (z < splits).
-void Engine::split_product(const char* name, const half_t* x, int64_t k, const DevWeight& w, int64_t t,
-                           const SplitPlan& sp) {
+// Range k's rows [r0, r0 + t) of y = x . W^T (x already offset to the
+// range) into the split partials a_ + z * slots_ * d (z < splits).
+void Engine::split_product(const char* name, int k, const half_t* x, int64_t kdim, const DevWeight& w, int64_t r0,
+                           int64_t t, const SplitPlan& sp) {
     const int64_t d = cfg_.d, pstride = slots_ * d;
-    float* a = a_.as<float>();
+    const hipStream_t s = sub_stream_[k];
+    float* a = a_.as<float>() + r0 * d;
     if (sp.chunks <= 1) {
-        step(name, [&] { launch_gemm_splitk(stream_, x, k, w, a, d, t, sp.splits, pstride, sp.kfold); });
+        step(name, k, [&] { launch_gemm_splitk(s, x, kdim, w, a, d, t, sp.splits, pstride, sp.kfold); });
         return;
     }
-    float* area = a + sp.splits * pstride;  // chunk partials, t x d each
-    step(name, [&] { launch_gemm_splitk(stream_, x, k, w, area, d, t, sp.splits * sp.chunks, t * d); });
-    step("fold", [&] { launch_fold_chunks(stream_, area, t * d, sp.chunks, sp.splits, t * d, a, pstride); });
+    // chunk partials, t x d each, above the split partials (one range: no
+    // range of a split pass is short enough to take this path)
+    float* area = a_.as<float>() + sp.splits * pstride;
+    step(name, k, [&] { launch_gemm_splitk(s, x, kdim, w, area, d, t, sp.splits * sp.chunks, t * d); });
+    step("fold", k, [&] { launch_fold_chunks(s, area, t * d, sp.chunks, sp.splits, t * d, a, pstride); });
 }
 
-void Engine::forward(int64_t t, int64_t base) {
+// The pass's ranges on their streams: the ranges fork from stream_ (whose
+// queue holds the pass's input copies), run layer by layer (host order:
+// layer-major, so every stream has work queued), and join stream_ before
+// the readout.
+void Engine::forward(int64_t base) {
     const Config& c = cfg_;
-    const int64_t d = c.d;
-    step("embed_norm", [&] {
-        launch_embed_norm(stream_, embed_.w, d_ids_, t, std::sqrt(float(d)),
-                          layers_[0].attn_norm.as<float>(), c.eps, x_.as<float>(), hn_.as<half_t>());
-    });
-    const int64_t P = c.per_layer_dim;
-    if (P > 0) {
-        // Per-layer inputs of every layer at once (engine.rs:1651-1666).
-        step("pl_in", [&] { launch_to_f16(stream_, x_.as<float>(), x16_.as<half_t>(), t * d); });
-        step("mm_pl_model_proj", [&] {
-            launch_gemm(stream_, x16_.as<half_t>(), d, pl_model_proj_.w, pli_.as<float>(), P * c.layers, t);
-        });
-        step("pl_combine", [&] {
-            launch_pl_combine(stream_, pl_table_.w, d_ids_, pl_proj_norm_.as<float>(), pli_.as<float>(),
-                              t, P, c.layers, c.eps, 1.0f / std::sqrt(float(d)), std::sqrt(float(P)),
-                              1.0f / std::sqrt(2.0f));
-        });
+    const int64_t d = c.d, P = c.per_layer_dim;
+    const int ns = nsub_;
+    if (ns > 1) {
+        OMG_HIP(hipEventRecord(ev_fork_, stream_));
+        for (int k = 1; k < ns; ++k) OMG_HIP(hipStreamWaitEvent(sub_stream_[k], ev_fork_, 0));
     }
-    for (int64_t l = 0; l < c.layers; ++l) {
-        Layer& L = layers_[size_t(l)];
-        const int64_t hd = c.head_dim[size_t(l)], qw = c.qkv_width(l), ff = c.ff[size_t(l)];
-        const int64_t src = c.kv_source[size_t(l)];
-        QkArgs q{};
-        q.qkv = qkv_.as<float>();
-        q.qkv_stride = qw;
-        q.meta = meta_.as<int32_t>();
-        q.q_norm = L.q_norm.as<float>();
-        q.k_norm = c.has_kv(l) ? L.k_norm.as<float>() : nullptr;
-        q.rope = rope_tabs_[size_t(rope_of_[size_t(l)])].as<float2>();
-        q.rope_rows = rope_rows_;
-        q.rope_dims = c.rope_dims[size_t(l)];
-        q.eps = c.eps;
-        q.q_scale = c.query_scale;
-        q.heads = int(c.heads);
-        q.kv_heads = int(c.kv_heads);
-        q.hd = int(hd);
-        q.has_kv = c.has_kv(l);
-        q.v_norm = c.v_norm;
-        q.t = t;
-        q.base = base;
-        q.cap_pad = cap_pad_;
-        q.q16 = q16_.as<half_t>();
-        q.kc = kc_[size_t(src)].as<half_t>();
-        q.vt = vt_[size_t(src)].as<half_t>();
-        if (hd == 256) {
-            // qk_prep's norms, RoPE and cache writes in the product's epilogue
-            step("mm_qkv", [&] { launch_gemm_qkprep(stream_, hn_.as<half_t>(), d, L.qkv.w, q, t); });
-        } else {
-            step("mm_qkv", [&] { launch_gemm(stream_, hn_.as<half_t>(), d, L.qkv.w, qkv_.as<float>(), qw, t); });
-            step("qk_prep", [&] { launch_qk_prep(stream_, q); });
-        }
-        AttnArgs att{};
-        att.q16 = q16_.as<half_t>();
-        att.kc = kc_[size_t(src)].as<half_t>();
-        att.vt = vt_[size_t(src)].as<half_t>();
-        att.meta = meta_.as<int32_t>();
-        att.out = attn_.as<half_t>();
-        att.t = t;
-        att.base = base;
-        att.cap_pad = cap_pad_;
-        att.heads = int(c.heads);
-        att.kv_heads = int(c.kv_heads);
-        att.hd = int(hd);
-        att.window = c.sliding[size_t(l)] ? int(c.window) : 0;
-        att.part_o = part_o_.as<half_t>();
-        att.part_ml = part_ml_.as<float>();
-        const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
-        step("attention", [&] { launch_attention(stream_, att, d_items_[kind], n_items_[kind], work_[kind].nw); });
-        if (n_merges_[kind] > 0)
-            step("attention_merge",
-                 [&] { launch_attention_merge(stream_, att, d_merges_[kind], n_merges_[kind], work_[kind].nw); });
-        const SplitPlan po = split_plan(c.heads * hd, d, t), pd = split_plan(ff, d, t);
-        const int so = po.splits, sd = pd.splits;
-        const int64_t pstride = slots_ * d;
-        split_product("mm_o", attn_.as<half_t>(), c.heads * hd, L.o.w, t, po);
-        step("norm", [&] {
-            launch_residual_norm(stream_, a_.as<float>(), L.post_attn_norm.as<float>(), x_.as<float>(),
-                                 L.ffn_norm.as<float>(), hn_.as<half_t>(), t, d, c.eps, 1.0f, so, pstride);
+    for (int k = 0; k < ns; ++k) {
+        const Sub& sb = sub_[k];
+        const int64_t r0 = sb.r0, t = sb.r1 - sb.r0;
+        const hipStream_t s = sub_stream_[k];
+        step("embed_norm", k, [&] {
+            launch_embed_norm(s, embed_.w, d_ids_ + r0, t, std::sqrt(float(d)), layers_[0].attn_norm.as<float>(),
+                              c.eps, x_.as<float>() + r0 * d, hn_.as<half_t>() + r0 * d);
         });
-        step("mm_gate_up", [&] {
-            launch_gemm_geglu(stream_, hn_.as<half_t>(), d, L.gate.w, L.up.w, act_.as<half_t>(), ff, t);
-        });
-        split_product("mm_down", act_.as<half_t>(), ff, L.down.w, t, pd);
-        // The last layer's stream is normed at the wanted rows only (readout).
-        const float* next = l + 1 < c.layers ? layers_[size_t(l + 1)].attn_norm.as<float>() : nullptr;
-        half_t* next_hn = next ? hn_.as<half_t>() : nullptr;
-        if (P == 0) {
-            step("norm", [&] {
-                launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), next,
-                                     next_hn, t, d, c.eps, 1.0f, sd, pstride);
+        if (P > 0) {
+            // Per-layer inputs of every layer at once (engine.rs:1651-1666).
+            const int64_t pw = P * c.layers;
+            step("pl_in", k, [&] { launch_to_f16(s, x_.as<float>() + r0 * d, x16_.as<half_t>() + r0 * d, t * d); });
+            step("mm_pl_model_proj", k, [&] {
+                launch_gemm(s, x16_.as<half_t>() + r0 * d, d, pl_model_proj_.w, pli_.as<float>() + r0 * pw, pw, t);
             });
-            continue;
+            step("pl_combine", k, [&] {
+                launch_pl_combine(s, pl_table_.w, d_ids_ + r0, pl_proj_norm_.as<float>(), pli_.as<float>() + r0 * pw,
+                                  t, P, c.layers, c.eps, 1.0f / std::sqrt(float(d)), std::sqrt(float(P)),
+                                  1.0f / std::sqrt(2.0f));
+            });
         }
-        // Per-layer input block (engine.rs:1733-1750): the stream after the
-        // feed-forward, as f16, gates the layer's slice of the inputs.
-        step("norm", [&] {
-            launch_residual_norm(stream_, a_.as<float>(), L.post_ffn_norm.as<float>(), x_.as<float>(), nullptr,
-                                 x16_.as<half_t>(), t, d, c.eps, 1.0f, sd, pstride);
-        });
-        step("mm_pl_gate", [&] { launch_gemm(stream_, x16_.as<half_t>(), d, L.pl_gate.w, plg_.as<float>(), P, t); });
-        step("pl_gate", [&] {
-            launch_pl_gate(stream_, plg_.as<float>(), pli_.as<float>(), pl16_.as<half_t>(), t, P, c.layers, l);
-        });
-        step("mm_pl_proj", [&] { launch_gemm(stream_, pl16_.as<half_t>(), P, L.pl_proj.w, a_.as<float>(), d, t); });
-        step("norm", [&] {
-            launch_residual_norm(stream_, a_.as<float>(), L.pl_norm.as<float>(), x_.as<float>(), next, next_hn, t, d,
-                                 c.eps, L.out_scale);
-        });
     }
+    for (int64_t l = 0; l < c.layers; ++l)
+        for (int k = 0; k < ns; ++k) layer(l, k, base);
+    if (ns > 1) {
+        for (int k = 1; k < ns; ++k) {
+            OMG_HIP(hipEventRecord(ev_join_[k], sub_stream_[k]));
+            OMG_HIP(hipStreamWaitEvent(stream_, ev_join_[k], 0));
+        }
+    }
+}
+
+// Layer l of range k (rows [r0, r1) of the pass, cache rows from base + r0).
+void Engine::layer(int64_t l, int k, int64_t pass_base) {
+    const Config& c = cfg_;
+    const int64_t d = c.d, P = c.per_layer_dim;
+    const Sub& sb = sub_[k];
+    const int64_t r0 = sb.r0, t = sb.r1 - sb.r0, base = pass_base + r0;
+    const hipStream_t s = sub_stream_[k];
+    Layer& L = layers_[size_t(l)];
+    const int64_t hd = c.head_dim[size_t(l)], qw = c.qkv_width(l), ff = c.ff[size_t(l)];
+    const int64_t src = c.kv_source[size_t(l)];
+    half_t* hn = hn_.as<half_t>() + r0 * d;
+    float* x = x_.as<float>() + r0 * d;
+    QkArgs q{};
+    q.qkv = qkv_.as<float>() + r0 * qw;
+    q.qkv_stride = qw;
+    q.meta = meta_.as<int32_t>();
+    q.q_norm = L.q_norm.as<float>();
+    q.k_norm = c.has_kv(l) ? L.k_norm.as<float>() : nullptr;
+    q.rope = rope_tabs_[size_t(rope_of_[size_t(l)])].as<float2>();
+    q.rope_rows = rope_rows_;
+    q.rope_dims = c.rope_dims[size_t(l)];
+    q.eps = c.eps;
+    q.q_scale = c.query_scale;
+    q.heads = int(c.heads);
+    q.kv_heads = int(c.kv_heads);
+    q.hd = int(hd);
+    q.has_kv = c.has_kv(l);
+    q.v_norm = c.v_norm;
+    q.t = t;
+    q.base = base;
+    q.cap_pad = cap_pad_;
+    q.q16 = q16_.as<half_t>() + r0 * c.heads * hd;
+    q.kc = kc_[size_t(src)].as<half_t>();
+    q.vt = vt_[size_t(src)].as<half_t>();
+    if (hd == 256) {
+        // qk_prep's norms, RoPE and cache writes in the product's epilogue
+        step("mm_qkv", k, [&] { launch_gemm_qkprep(s, hn, d, L.qkv.w, q, t); });
+    } else {
+        step("mm_qkv", k, [&] { launch_gemm(s, hn, d, L.qkv.w, qkv_.as<float>() + r0 * qw, qw, t); });
+        step("qk_prep", k, [&] { launch_qk_prep(s, q); });
+    }
+    if (nsub_ > 1) {
+        // This range's K/V rows of layer l are in the cache; the later
+        // ranges' attention reads them.
+        if (k + 1 < nsub_) OMG_HIP(hipEventRecord(ev_kv_[size_t(k * c.layers + l)], s));
+        for (int j = 0; j < k; ++j) OMG_HIP(hipStreamWaitEvent(s, ev_kv_[size_t(j * c.layers + l)], 0));
+    }
+    AttnArgs att{};
+    att.q16 = q.q16;
+    att.kc = q.kc;
+    att.vt = q.vt;
+    att.meta = meta_.as<int32_t>();
+    att.out = attn_.as<half_t>() + r0 * c.heads * hd;
+    att.t = t;
+    att.base = base;
+    att.cap_pad = cap_pad_;
+    att.heads = int(c.heads);
+    att.kv_heads = int(c.kv_heads);
+    att.hd = int(hd);
+    att.window = c.sliding[size_t(l)] ? int(c.window) : 0;
+    att.part_o = part_o_.as<half_t>();
+    att.part_ml = part_ml_.as<float>();
+    const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
+    const int nw = sb.work[kind].nw;
+    step("attention", k, [&] { launch_attention(s, att, sb.d_items[kind], sb.n_items[kind], nw); });
+    if (sb.n_merges[kind] > 0)
+        step("attention_merge", k, [&] { launch_attention_merge(s, att, sb.d_merges[kind], sb.n_merges[kind], nw); });
+    const SplitPlan po = split_plan(c.heads * hd, d, t), pd = split_plan(ff, d, t);
+    const int so = po.splits, sd = pd.splits;
+    const int64_t pstride = slots_ * d;
+    float* a = a_.as<float>() + r0 * d;
+    split_product("mm_o", k, att.out, c.heads * hd, L.o.w, r0, t, po);
+    step("norm", k, [&] {
+        launch_residual_norm(s, a, L.post_attn_norm.as<float>(), x, L.ffn_norm.as<float>(), hn, t, d, c.eps, 1.0f,
+                             so, pstride);
+    });
+    half_t* act = act_.as<half_t>() + r0 * ff;
+    step("mm_gate_up", k, [&] { launch_gemm_geglu(s, hn, d, L.gate.w, L.up.w, act, ff, t); });
+    split_product("mm_down", k, act, ff, L.down.w, r0, t, pd);
+    // The last layer's stream is normed at the wanted rows only (readout).
+    const float* next = l + 1 < c.layers ? layers_[size_t(l + 1)].attn_norm.as<float>() : nullptr;
+    half_t* next_hn = next ? hn : nullptr;
+    if (P == 0) {
+        step("norm", k, [&] {
+            launch_residual_norm(s, a, L.post_ffn_norm.as<float>(), x, next, next_hn, t, d, c.eps, 1.0f, sd, pstride);
+        });
+        return;
+    }
+    // Per-layer input block (engine.rs:1733-1750): the stream after the
+    // feed-forward, as f16, gates the layer's slice of the inputs.
+    half_t* x16 = x16_.as<half_t>() + r0 * d;
+    step("norm", k, [&] {
+        launch_residual_norm(s, a, L.post_ffn_norm.as<float>(), x, nullptr, x16, t, d, c.eps, 1.0f, sd, pstride);
+    });
+    float* plg = plg_.as<float>() + r0 * P;
+    half_t* pl16 = pl16_.as<half_t>() + r0 * P;
+    float* pli = pli_.as<float>() + r0 * P * c.layers;
+    step("mm_pl_gate", k, [&] { launch_gemm(s, x16, d, L.pl_gate.w, plg, P, t); });
+    step("pl_gate", k, [&] { launch_pl_gate(s, plg, pli, pl16, t, P, c.layers, l); });
+    step("mm_pl_proj", k, [&] { launch_gemm(s, pl16, P, L.pl_proj.w, a, d, t); });
+    step("norm", k, [&] {
+        launch_residual_norm(s, a, L.pl_norm.as<float>(), x, next, next_hn, t, d, c.eps, L.out_scale);
+    });
 }
 
 void Engine::readout(const PassPlan& p) {
     if (p.nrows == 0) return;
     const Config& c = cfg_;
-    step("final_rows", [&] {
+    step("final_rows", 0, [&] {
         launch_final_rows(stream_, x_.as<float>(), d_wanted_, p.nrows, c.d, final_norm_.as<float>(),
                           c.eps, rows_.as<float>());
     });
     if (p.want == WANT_LOGITS) {
-        step("logits", [&] {
+        step("logits", 0, [&] {
             launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, nullptr, c.vocab, c.softcap,
                           logits_.as<float>());
         });
     } else if (p.want == WANT_LABELS) {
-        step("logits", [&] {
+        step("logits", 0, [&] {
             launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, d_labels_, p.nlabels,
                           c.softcap, logits_.as<float>());
         });
@@ -722,11 +830,11 @@ void Engine::readout(const PassPlan& p) {
         // Readout::distribution (readout.rs:124-146) needs the label logits
         // and the log-sum-exp of the whole row: every logit is computed,
         // only k + 1 floats per row leave the device.
-        step("logits", [&] {
+        step("logits", 0, [&] {
             launch_logits(stream_, embed_.w, rows_.as<float>(), p.nrows, nullptr, c.vocab, c.softcap,
                           logits_.as<float>(), lse_part_.as<float2>());
         });
-        step("label_lse", [&] {
+        step("label_lse", 0, [&] {
             launch_label_lse(stream_, logits_.as<float>(), p.nrows, c.vocab, lse_part_.as<float2>(),
                              logits_blocks(c.vocab), d_labels_, p.nlabels, label_lse_.as<float>());
         });
@@ -750,7 +858,7 @@ Engine::Run Engine::run_pass(const GroupIn* groups, int64_t n, int want, const u
     const bool by_label = want == WANT_LABELS || want == WANT_LABELS_LSE;
     upload(run.pk, labels, by_label ? nlabels : 0);
     const int64_t t = run.pk.total - run.pk.base;
-    forward(t, run.pk.base);
+    forward(run.pk.base);
     readout(PassPlan{t, run.pk.base, int64_t(run.pk.wanted.size()), nlabels, want});
     return run;
 }
@@ -902,7 +1010,7 @@ int64_t Engine::evaluate_pointer(const GroupIn* groups, int64_t n, const uint8_t
     int2* d_pairs = reinterpret_cast<int2*>(d_mat + mat_slots);
     OMG_HIP(hipMemcpyAsync(d_mat, mat, size_t(nrows) * 4, hipMemcpyHostToDevice, stream_));
     if (nlogits) OMG_HIP(hipMemcpyAsync(d_pairs, pairs, size_t(nlogits) * 8, hipMemcpyHostToDevice, stream_));
-    step("pointer", [&] {
+    step("pointer", 0, [&] {
         launch_pointer(stream_, rows_.as<float>(), nrows, cfg_.d, ptr_w_.as<float>(), ptr_b_.as<float>(), ptr_dp_,
                        d_mat, ptr_proj_.as<float>(), d_pairs, nlogits, ptr_out_.as<float>());
     });
@@ -943,7 +1051,7 @@ void Engine::launch_prepared() {
         OMG_HIP(hipGraphLaunch(graph_exec_, stream_));
         return;
     }
-    forward(prepared_.t, prepared_.base);
+    forward(prepared_.base);
     readout(prepared_);
 }
 
@@ -960,7 +1068,7 @@ void Engine::set_graph(bool on) {
     hipGraph_t g = nullptr;
     OMG_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
     try {
-        forward(prepared_.t, prepared_.base);
+        forward(prepared_.base);
         readout(prepared_);
     } catch (...) {
         (void)hipStreamEndCapture(stream_, &g);

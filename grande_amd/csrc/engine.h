@@ -168,12 +168,13 @@ class Engine {
         int splits = 1, chunks = 1, kfold = 0;
     };
     SplitPlan split_plan(int64_t k, int64_t n, int64_t t) const;
-    void split_product(const char* name, const half_t* x, int64_t k, const DevWeight& w, int64_t t,
-                       const SplitPlan& sp);
-    void forward(int64_t t, int64_t base);
+    void split_product(const char* name, int k, const half_t* x, int64_t kdim, const DevWeight& w, int64_t r0,
+                       int64_t t, const SplitPlan& sp);
+    void forward(int64_t base);
     void readout(const PassPlan& plan);
+    // One profiled launch (or launcher call) on range k's stream.
     template <class F>
-    void step(const char* name, F&& f);
+    void step(const char* name, int k, F&& f);
 
     Config cfg_;
     int64_t capacity_ = 0, max_rows_ = 0, cap_pad_ = 0;
@@ -211,18 +212,33 @@ class Engine {
     const uint32_t* d_ids_ = nullptr;
     const int32_t* d_wanted_ = nullptr;
     const uint32_t* d_labels_ = nullptr;
-    const int4* d_items_[2] = {nullptr, nullptr};
-    const int4* d_merges_[2] = {nullptr, nullptr};
     // Label logits + full-row log-sum-exp per wanted row (WANT_LABELS_LSE),
     // and the logits kernel's per-workgroup (max, sum of exp) pairs.
     DevBuf label_lse_, lse_part_;
     DevBuf x16_, pli_, plg_, pl16_;  // per-layer inputs: f16(x), [t][layers x P] f32, gate f32, gated f16
-    // attention work lists of the current pass: [0] sliding layers, [1] global
+    // attention chunk lengths in key tiles: [0] sliding layers, [1] global
     int attn_chunk_[2] = {0, 0};
     DevBuf part_o_, part_ml_;
-    int64_t n_items_[2] = {0, 0}, n_merges_[2] = {0, 0};
-    AttnWork work_[2];  // host side of the lists (capacity reused from pass to pass)
     int64_t part_slots_ = 0;  // chunk partial slots part_o_ / part_ml_ hold
+    // Sub-passes: a long pass runs as up to MAX_SUB consecutive row ranges,
+    // each on a stream of its own, layer by layer; a range's attention at
+    // layer l waits for the K/V rows the earlier ranges write at layer l
+    // (a row sees only rows before it), so the ranges' kernels overlap and
+    // every row's arithmetic is that of the whole pass.
+    static constexpr int MAX_SUB = 3;
+    struct Sub {
+        int64_t r0 = 0, r1 = 0;  // pass-relative rows [r0, r1)
+        AttnWork work[2];        // host side of its attention lists per layer type
+        const int4* d_items[2] = {nullptr, nullptr};
+        const int4* d_merges[2] = {nullptr, nullptr};
+        int64_t n_items[2] = {0, 0}, n_merges[2] = {0, 0};
+    };
+    Sub sub_[MAX_SUB];
+    int nsub_ = 1;
+    hipStream_t sub_stream_[MAX_SUB] = {};  // [0] is stream_
+    hipEvent_t ev_fork_ = nullptr, ev_join_[MAX_SUB] = {};
+    std::vector<hipEvent_t> ev_kv_;  // [range][layer]: the range's K/V rows of the layer are in the cache
+    void layer(int64_t l, int k, int64_t base);
     std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
     // pinned host staging
     void* h_in_ = nullptr;
@@ -252,7 +268,7 @@ class Engine {
         const char* name;  // null for the sequence's start event
         hipEvent_t e;
     };
-    std::vector<Timed> pending_;
+    std::vector<Timed> pending_[MAX_SUB];  // per range's stream
     std::vector<hipEvent_t> event_pool_;
     std::map<std::string, std::pair<int64_t, double>> totals_;
     void collect_profile();

@@ -567,3 +567,38 @@ def test_evaluate_cancels_a_prepared_pass():
     again = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
     for a, b in zip(ref, again):
         assert np.array_equal(a.rows[0], b.rows[0])
+
+
+@pytest.mark.parametrize("prefix_len", [8300, 12400])
+def test_pass_split_over_streams_is_bit_equal(prefix_len):
+    """A long pass runs as consecutive row ranges on streams of their own
+    (two ranges from 8,192 rows, three from 12,288), each range's attention
+    waiting for the earlier ranges' K/V of the same layer.  Its rows are bit
+    for bit those of the same pass as one range (profiling runs passes as
+    one range), of the branches over the resident prefix, and of a captured
+    graph of the split pass replayed several times."""
+    cfg = gguf_tiny(8, 2, window=37, vocab=64)
+    eng, _, _, _ = build(cfg, 47, g.Q4, g.Q8, capacity=prefix_len + 256, oracle_models=False)
+    rng = np.random.default_rng(prefix_len)
+    prefix = rng.integers(0, 64, prefix_len).tolist()
+    branches = [BranchTokens(rng.integers(0, 64, n).tolist(), [0, n - 1]) for n in (9, 40, 17)]
+    split = eng.evaluate(prefix, branches, Want.HIDDEN)
+    assert eng.prefix_source() == PrefixSource.DECODED
+    eng.evict_resident()
+    eng.profile(True)
+    one = eng.evaluate(prefix, branches, Want.HIDDEN)
+    eng.profile(False)
+    warm = eng.evaluate(prefix, branches, Want.HIDDEN)
+    assert eng.prefix_source() == PrefixSource.RESIDENT
+    for a, b, c in zip(split, one, warm):
+        for x, y, z in zip(a.rows, b.rows, c.rows):
+            assert np.array_equal(x, y), "split pass differs from the one-range pass"
+            assert np.array_equal(x, z), "split pass differs from the branches over the resident prefix"
+    eng.evict_resident()
+    eng.prepare([Group(prefix, branches)], Want.HIDDEN)
+    eng.graph(True)
+    exp = np.concatenate([r for b in split for r in b.rows])
+    for rep in range(3):
+        eng.launch()
+        got = eng.read_prepared(1 << 14)
+        assert np.array_equal(got, exp), f"graph replay {rep}"
