@@ -9,7 +9,7 @@
 // blocks of 16 rows, and every K / V fragment read from LDS feeds the
 // MFMAs of all of them) and a range of 32-key tiles; the host builds the item lists from the pass's metadata
 // (AttnWork).  A tile's key range is cut at fixed multiples of `chunk`
-// tiles (sliding layers: 256 keys; global layers: 512 keys or more) and the
+// tiles (sliding layers: 256 keys; global layers: 384 keys or more) and the
 // per-chunk partial results are merged in key order by attention_merge.
 // Because chunk boundaries are absolute cache rows and a tile that a query
 // cannot see leaves its state exactly unchanged, each query's arithmetic
@@ -60,8 +60,12 @@ int attention_key_tile() { return A_KT; }
 int attention_rows() { return A_ROWS; }
 
 // V^T tile rows hold A_KT keys (A_KT / 8 chunks of 16 B); the chunk swizzle
-// spreads 16 consecutive rows over distinct banks.
-__device__ inline int vt_swz(int row) { return A_KT == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
+// spreads the rows a 16-byte fragment read serves at once over distinct
+// banks.  Measured on the 32-key tiles (rocprofv3 SQ_LDS_BANK_CONFLICT /
+// SQ_LDS_IDX_ACTIVE, C2 cold pass): (row >> 2) & 3 left 33.5% of the LDS
+// cycles in bank conflicts, (row >> 1) & 3 7.3% (attention 19.6 -> 19.0 us);
+// row & 3 and (row ^ (row >> 2)) & 3 no better than the first.
+__device__ inline int vt_swz(int row) { return A_KT == 64 ? ((row >> 1) & 7) : ((row >> 1) & 3); }
 
 
 // LDS of one work item.  K and V^T tiles are stored without padding; the

@@ -703,15 +703,17 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     int qpos[QK_PASSES];
     if constexpr (EPI == EPI_QKPREP) {
         const QkArgs& a = g.qk;
+        const bool qk_head = n0 / 256 < a.heads + a.kv_heads;
 #pragma unroll
         for (int p = 0; p < QK_PASSES; ++p) {
+            // Every thread loads the position of a row of the pass (its own
+            // row, clamped into the pass), so the loads go out back to back
+            // with no branch between them; rows outside the pass and the v
+            // head take position 0.
             const int r = p * 8 + tid / 32;
-            int pos = 0;
-            if (n0 / 256 < a.heads + a.kv_heads && row_ok(r)) {
-                pos = a.meta[4 * (a.base + m0 + r)];
-                pos = pos < 0 ? 0 : (pos >= a.rope_rows ? int(a.rope_rows - 1) : pos);
-            }
-            qpos[p] = pos;
+            const int64_t m = m0 + r < 0 ? 0 : (m0 + r < M ? m0 + r : M - 1);
+            const int pos = a.meta[4 * (a.base + m)];
+            qpos[p] = qk_head && row_ok(r) ? (pos < 0 ? 0 : (pos >= a.rope_rows ? int(a.rope_rows - 1) : pos)) : 0;
         }
     }
 
@@ -811,12 +813,16 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
             }
         }
         lds_barrier();
-        auto row_inv = [&](int r) {
+        // Each row's scale once, from the sum of its eight partials in
+        // order; the passes below read it.
+        float* rinv = ssp + BM * 8;  // [BM] row scales
+        if (tid < BM) {
             float ss = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ss += ssp[r * 8 + k];
-            return 1.0f / sqrtf(ss / float(HD) + a.eps);
-        };
+            for (int k = 0; k < 8; ++k) ss += ssp[tid * 8 + k];
+            rinv[tid] = 1.0f / sqrtf(ss / float(HD) + a.eps);
+        }
+        lds_barrier();
         if (!is_v) {
             const bool is_q = slot < H;
             const int head = is_q ? slot : slot - H;
@@ -829,7 +835,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
             for (int p = 0; p < QK_PASSES; ++p) {
                 const int r = p * 8 + tid / 32;
                 if (!row_ok(r)) continue;
-                const float inv = row_inv(r);
+                const float inv = rinv[r];
                 const float4 vl = *reinterpret_cast<const float4*>(T + r * TS + d0);
                 const float4 vh = *reinterpret_cast<const float4*>(T + r * TS + HALF + d0);
                 const float v_lo[4] = {vl.x, vl.y, vl.z, vl.w}, v_hi[4] = {vh.x, vh.y, vh.z, vh.w};
@@ -860,11 +866,6 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         // 256 dims x 4 chunks; chunk 4 hf + cc of a 64-key cache tile holds
         // keys 32 hf + 4 cc + {0..3, 16..19} (vt_col).
         const int head = slot - H - KV;
-        float* rinv = ssp + BM * 8;  // [BM] row scales (v_norm)
-        if (a.v_norm) {
-            if (tid < BM) rinv[tid] = row_inv(tid);
-            lds_barrier();
-        }
 #pragma unroll
         for (int hh = 0; hh < BM / 32; ++hh) {
             const int64_t kh = a.base + m0 + 32 * hh;  // first cache row of this half (a multiple of 32)

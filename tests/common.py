@@ -96,12 +96,12 @@ def tiled_oracle(cfg: str, tensors, capacity: int) -> oracle.Model:
     """The f16-rounding oracle with the HIP attention kernel's own rounding
     points too (32-key tiles, lazily moved whole-power-of-two max, P in f16,
     f16 chunk partials at the engine's chunk lengths for this capacity:
-    256 keys on sliding layers, max(512 keys, an eighth of the cache) on
+    256 keys on sliding layers, max(384 keys, an eighth of the cache) on
     global ones)."""
     kt = 32
     cap_pad = (capacity + 63) // 64 * 64
     return oracle.Model(cfg, tensors, gpu_rounding=True).set_attention_tiles(
-        kt, 256 // kt, max(512 // kt, (cap_pad // kt + 7) // 8))
+        kt, 256 // kt, max(384 // kt, (cap_pad // kt + 7) // 8))
 
 
 def worst_rel(a, b) -> float:

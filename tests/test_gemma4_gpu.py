@@ -101,7 +101,7 @@ def check_chaotic(out, cfg: str, ts, prefix, branches, capacity: int, what: str,
 def test_gemma4_long_prefix_global_key_ranges(capacity, heads, kv):
     """A 700-token prefix on the reference's gemma4 configs and weights
     (reference.rs:66-104, 108-139): at capacity 1024 the head_dim-512 global
-    layers' key ranges are cut into 512-key chunks and merged, at 8192 they
+    layers' key ranges are cut into 384-key chunks and merged, at 8192 they
     are not (1024-key chunks).  Four layers deep the GPU rows stay within
     1.2e-2 of the forward with the kernel's own rounding points (measured
     6.4e-3 .. 9.2e-3)."""
