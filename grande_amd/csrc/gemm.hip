@@ -543,7 +543,11 @@ __device__ inline bool run_phases(F& f, std::index_sequence<I...>) {
     return (f(std::integral_constant<int, int(I)>{}) && ...);
 }
 
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_, bool FOLD>
+// XR (resident X): the workgroup's whole X tile (BM rows x its K range)
+// lands in LDS in the prologue, one slot per stage, and the K loop runs
+// with no barrier and no X wait (the weights are each wave's own).  Same
+// MFMA sequence, same sums; chosen per launch when the tile fits.
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_, bool FOLD, bool XR>
 __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW_>;
     static_assert(!FOLD || EPI == EPI_F32, "K chunks: f32 products only");
@@ -597,7 +601,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     // Stages past the end repeat the last one (in range, never consumed),
     // so the resources and lane offsets stay the same for every stage and
     // only the scalar stage offset moves.
-    auto slot_base = [&](int s) { return smem + (unsigned(s) % unsigned(NS)) * P::X_BYTES; };
+    auto slot_base = [&](int s) { return smem + (XR ? unsigned(s) : unsigned(s) % unsigned(NS)) * P::X_BYTES; };
     const int last = nk - 1;
     const int64_t xbytes = M * g.ldx * 2;
     const bool ktail = (K32 & (G_BK - 1)) != 0;  // K % 64 == 32: the last stage masks lanes
@@ -717,10 +721,48 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         }
     }
 
-    // Prologue: stages 0 .. NS - 2 in the same order as the loop issues
-    // them (X, then weights), then stage 0's X fragments.
     WRegs wr[R];
     XRegs xa, xb;
+    int kt = 0;
+    if constexpr (XR) {
+        // Prologue: every stage's X, then weight stages 0 .. R - 1; all of
+        // it landed (everyone's X: one barrier), then stage 0's fragments.
+        for (int s = 0; s < nk; ++s) issue_x(s);
+#pragma unroll
+        for (int s = 0; s < R; ++s) issue_w(s, wr[s]);
+        wait_vm<0>();
+        lds_barrier();
+        read_x(0, xa);
+        auto xstep = [&](auto phase) {
+            constexpr int PH = decltype(phase)::value;
+            XRegs& cur = PH % 2 == 0 ? xa : xb;
+            XRegs& nxt = PH % 2 == 0 ? xb : xa;
+            // Stage kt's weights (issued R iterations ago) landed: at most
+            // the R - 1 later stages' loads are still out.
+            wait_vm<(R - 1) * P::WL>();
+            if (kt + 1 < nk) read_x(kt + 1, nxt);
+            compute(cur, wr[PH % R]);
+            issue_w(kt + R, wr[PH % R]);
+            if constexpr (FOLD) {
+                if (((kt + 1) & kfm) == 0 || kt + 1 == nk) {
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j) {
+                            tot[i][j] = folded ? tot[i][j] + acc[i][j] : acc[i][j];
+                            acc[i][j] = floatx16{};
+                        }
+                    folded = true;
+                }
+            }
+            return ++kt < nk;
+        };
+        while (run_phases(xstep, std::make_index_sequence<P::U>{})) {
+        }
+    }
+    // Prologue: stages 0 .. NS - 2 in the same order as the loop issues
+    // them (X, then weights), then stage 0's X fragments.
+    if constexpr (!XR) {
 #pragma unroll
     for (int s = 0; s < R; ++s) {
         issue_x(s);
@@ -729,7 +771,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     wait_vm<P::WL + (NS - 2) * P::C>();
     lds_barrier();
     read_x(0, xa);
-    int kt = 0;
+    }
     auto step = [&](auto phase) {
         constexpr int PH = decltype(phase)::value;
         XRegs& cur = PH % 2 == 0 ? xa : xb;
@@ -756,7 +798,9 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         }
         return ++kt < nk;
     };
-    while (run_phases(step, std::make_index_sequence<P::U>{})) {
+    if constexpr (!XR) {
+        while (run_phases(step, std::make_index_sequence<P::U>{})) {
+        }
     }
     wait_vm<0>();
     if constexpr (FOLD) {
@@ -946,6 +990,10 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     }
 }
 
+// Resident X tiles up to this many bytes of LDS (one workgroup per CU
+// above half of it).
+constexpr int XR_MAX_LDS = 96 * 1024;
+
 template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4, bool FOLD = false>
 static void run32(hipStream_t s, const GemmArgs& g) {
     using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW>;
@@ -954,15 +1002,26 @@ static void run32(hipStream_t s, const GemmArgs& g) {
             fail(E_INVALID, "gemm: weight without stage tiles");
     static bool lds_set = false;
     if (!lds_set) {
-        OMG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
+        OMG_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, false>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
+        OMG_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, true>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, XR_MAX_LDS > P::QK_LDS ? XR_MAX_LDS : P::QK_LDS));
         lds_set = true;
     }
     const int64_t N = g.w0.rows;
     if (g.mshift < 0 || g.mshift >= P::BM) fail(E_INVALID, "gemm: row tile shift out of range");
     const int64_t tiles = ((N + P::BN - 1) / P::BN) * ((g.m + g.mshift + P::BM - 1) / P::BM);
     const dim3 grid(unsigned((tiles + 7) / 8 * 8), unsigned(g.ksplit));
-    gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD><<<grid, dim3(P::T), P::LDS, s>>>(g);
+    const int64_t nk = (g.w0.cols / g.ksplit + G_BK - 1) / G_BK;
+    const int64_t xr_lds = nk * P::X_BYTES;
+    if (xr_lds <= XR_MAX_LDS) {
+        const int lds = int(xr_lds > P::QK_LDS ? xr_lds : P::QK_LDS);
+        gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, true><<<grid, dim3(P::T), lds, s>>>(g);
+    } else {
+        gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, false><<<grid, dim3(P::T), P::LDS, s>>>(g);
+    }
     OMG_HIP(hipGetLastError());
 }
 
