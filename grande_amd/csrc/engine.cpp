@@ -460,7 +460,7 @@ constexpr int64_t SHORT_ATTN_ROWS = 1024;
 // pass in two ranges 0.5% slower, in three 6% slower (its kernels are too
 // short for the overlap to pay).
 constexpr int64_t SUB_ROWS = 4096;
-// Passes of at most this many rows run deep-K products a chunk per
+// Passes of at most this many rows run deep-K products a piece per
 // workgroup (split_plan).
 constexpr int64_t CHUNKED_ROWS = 512;
 
@@ -621,46 +621,59 @@ static int ksplit(int64_t k, int64_t n) {
     return s;
 }
 
-// Deep-K products (at least 4,096 K per split, in whole 1,024-wide chunks:
-// the 4B model's down projection) sum K in chunks of 16 stages: each chunk's
-// products accumulate from zero and the chunk sums are added in K order.
-// Long passes fold the chunks in the GEMM's registers; short ones run a
-// chunk per workgroup, which fills the chip, and add the partials in the
-// same order.  A function of the shape, so a row's sums do not depend on
-// the pass.
-constexpr int KFOLD_STAGES = 16;
-constexpr int64_t KFOLD_K = 64 * KFOLD_STAGES, KFOLD_MIN_K = 4096;
+// K pieces of the o / down products, a function of the shape only: a
+// split of deep K (at least 4,096, in whole 1,024-wide pieces: the 4B
+// model's down projection) is cut into `group` pieces whose products
+// accumulate from zero; the pieces' sums are added in K order, then the
+// splits' sums in order.  Long passes add a split's pieces in the GEMM's
+// registers (kfold, one partial per split); short ones run a piece per
+// workgroup, which fills the chip (10 x 20 x 2 = 400 workgroups at the 4B
+// one-branch pass instead of 40), and the residual norm adds the pieces in
+// the same runs — bit-equal rows either way.
+// Measured and not kept (same box): pieces of 8 stages for every split of
+// at least 32 (the 4B and E2B o, the E2B down): the 4B one-branch pass
+// 4.08 -> 3.79 ms (o 13.8 -> 7.3 us), but adding pieces in registers
+// drains the MFMA pipeline at every piece boundary: the 4B cold pass
+// 155.9 -> 160.8 ms, E2B cold 16.55 -> 16.71 ms, warm 7.58 -> 7.67 ms;
+// pieces of 4 stages on the 270M model's o and down: its cold pass 1.0 and
+// 1.3 us slower per product, its warm pass 0.5 and 1.1 us faster.
+constexpr int64_t DEEP_PIECE_K = 1024, DEEP_MIN_K = 4096;
 
 Engine::SplitPlan Engine::split_plan(int64_t k, int64_t n, int64_t t) const {
     SplitPlan p;
     p.splits = ksplit(k, n);
     const int64_t kr = k / p.splits;
-    if (kr < KFOLD_MIN_K || kr % KFOLD_K != 0) return p;
-    const int64_t chunks = kr / KFOLD_K;
-    // chunk partials go above the split partials in a_ (OMG_KSPLIT x slots x n floats)
-    if (t <= CHUNKED_ROWS && int64_t(p.splits) * slots_ + p.splits * chunks * t <= int64_t(OMG_KSPLIT) * slots_)
-        p.chunks = int(chunks);
-    else
-        p.kfold = KFOLD_STAGES;
+    if (kr < DEEP_MIN_K || kr % DEEP_PIECE_K != 0) return p;
+    p.group = int(kr / DEEP_PIECE_K);
+    p.kfold = int(DEEP_PIECE_K / 64);
+    // a piece per workgroup: the parts (t x n floats each) fit in a_
+    // (OMG_KSPLIT x slots x n floats); one range (ranges are longer)
+    p.pieces = t <= CHUNKED_ROWS && nsub_ == 1 && int64_t(p.splits) * p.group * t <= int64_t(OMG_KSPLIT) * slots_;
     return p;
 }
 
 // Range k's rows [r0, r0 + t) of y = x . W^T (x already offset to the
-// range) into the split partials a_ + z * slots_ * d (z < splits).
+// range) into the parts of a_ that norm_parts describes.
 void Engine::split_product(const char* name, int k, const half_t* x, int64_t kdim, const DevWeight& w, int64_t r0,
                            int64_t t, const SplitPlan& sp) {
-    const int64_t d = cfg_.d, pstride = slots_ * d;
+    const int64_t d = cfg_.d;
     const hipStream_t s = sub_stream_[k];
-    float* a = a_.as<float>() + r0 * d;
-    if (sp.chunks <= 1) {
-        step(name, k, [&] { launch_gemm_splitk(s, x, kdim, w, a, d, t, sp.splits, pstride, sp.kfold); });
+    if (sp.pieces) {
+        float* a = a_.as<float>();  // one range: r0 = 0
+        step(name, k, [&] { launch_gemm_splitk(s, x, kdim, w, a, d, t, sp.splits * sp.group, t * d); });
         return;
     }
-    // chunk partials, t x d each, above the split partials (one range: no
-    // range of a split pass is short enough to take this path)
-    float* area = a_.as<float>() + sp.splits * pstride;
-    step(name, k, [&] { launch_gemm_splitk(s, x, kdim, w, area, d, t, sp.splits * sp.chunks, t * d); });
-    step("fold", k, [&] { launch_fold_chunks(s, area, t * d, sp.chunks, sp.splits, t * d, a, pstride); });
+    float* a = a_.as<float>() + r0 * d;
+    step(name, k, [&] { launch_gemm_splitk(s, x, kdim, w, a, d, t, sp.splits, slots_ * d, sp.kfold); });
+}
+
+// Where split_product left a product's parts for the residual norm: a_
+// offset to the range's rows, the part count and stride, and the run
+// length the norm adds first.
+Engine::NormParts Engine::norm_parts(const SplitPlan& sp, int64_t r0, int64_t t) const {
+    const int64_t d = cfg_.d;
+    if (sp.pieces) return NormParts{a_.as<float>(), sp.splits * sp.group, t * d, sp.group};
+    return NormParts{a_.as<float>() + r0 * d, sp.splits, slots_ * d, 1};
 }
 
 // The pass's ranges on their streams: the ranges fork from stream_ (whose
@@ -775,13 +788,11 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     if (sb.n_merges[kind] > 0)
         step("attention_merge", k, [&] { launch_attention_merge(s, att, sb.d_merges[kind], sb.n_merges[kind], nw); });
     const SplitPlan po = split_plan(c.heads * hd, d, t), pd = split_plan(ff, d, t);
-    const int so = po.splits, sd = pd.splits;
-    const int64_t pstride = slots_ * d;
-    float* a = a_.as<float>() + r0 * d;
+    const NormParts no = norm_parts(po, r0, t), nd = norm_parts(pd, r0, t);
     split_product("mm_o", k, att.out, c.heads * hd, L.o.w, r0, t, po);
     step("norm", k, [&] {
-        launch_residual_norm(s, a, L.post_attn_norm.as<float>(), x, L.ffn_norm.as<float>(), hn, t, d, c.eps, 1.0f,
-                             so, pstride);
+        launch_residual_norm(s, no.a, L.post_attn_norm.as<float>(), x, L.ffn_norm.as<float>(), hn, t, d, c.eps, 1.0f,
+                             no.parts, no.stride, no.group);
     });
     half_t* act = act_.as<half_t>() + r0 * ff;
     step("mm_gate_up", k, [&] { launch_gemm_geglu(s, hn, d, L.gate.w, L.up.w, act, ff, t); });
@@ -791,7 +802,8 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     half_t* next_hn = next ? hn : nullptr;
     if (P == 0) {
         step("norm", k, [&] {
-            launch_residual_norm(s, a, L.post_ffn_norm.as<float>(), x, next, next_hn, t, d, c.eps, 1.0f, sd, pstride);
+            launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), x, next, next_hn, t, d, c.eps, 1.0f, nd.parts,
+                                 nd.stride, nd.group);
         });
         return;
     }
@@ -799,13 +811,15 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     // feed-forward, as f16, gates the layer's slice of the inputs.
     half_t* x16 = x16_.as<half_t>() + r0 * d;
     step("norm", k, [&] {
-        launch_residual_norm(s, a, L.post_ffn_norm.as<float>(), x, nullptr, x16, t, d, c.eps, 1.0f, sd, pstride);
+        launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), x, nullptr, x16, t, d, c.eps, 1.0f, nd.parts,
+                             nd.stride, nd.group);
     });
     float* plg = plg_.as<float>() + r0 * P;
     half_t* pl16 = pl16_.as<half_t>() + r0 * P;
     float* pli = pli_.as<float>() + r0 * P * c.layers;
     step("mm_pl_gate", k, [&] { launch_gemm(s, x16, d, L.pl_gate.w, plg, P, t); });
     step("pl_gate", k, [&] { launch_pl_gate(s, plg, pli, pl16, t, P, c.layers, l); });
+    float* a = a_.as<float>() + r0 * d;
     step("mm_pl_proj", k, [&] { launch_gemm(s, pl16, P, L.pl_proj.w, a, d, t); });
     step("norm", k, [&] {
         launch_residual_norm(s, a, L.pl_norm.as<float>(), x, next, next_hn, t, d, c.eps, L.out_scale);

@@ -161,15 +161,23 @@ class Engine {
     void finish_pass(const GroupIn* groups, int64_t n, const Run& run, int* sources);
     void upload(const Packed& pk, const uint32_t* labels, int64_t nlabels);
     // How an o / down product of K k and width n runs in a pass of t rows:
-    // its K splits, and for deep K its 256-wide K chunks — folded in the
-    // GEMM's registers (kfold) or, in short passes, one per workgroup and
-    // added by launch_fold_chunks (chunks > 1).
+    // its K splits, each split's K pieces (group, kfold stages each), and
+    // whether the pieces run a workgroup each (short passes) or are added
+    // in the GEMM's registers.
     struct SplitPlan {
-        int splits = 1, chunks = 1, kfold = 0;
+        int splits = 1, group = 1, kfold = 0;
+        bool pieces = false;
     };
     SplitPlan split_plan(int64_t k, int64_t n, int64_t t) const;
     void split_product(const char* name, int k, const half_t* x, int64_t kdim, const DevWeight& w, int64_t r0,
                        int64_t t, const SplitPlan& sp);
+    struct NormParts {
+        float* a;
+        int parts;
+        int64_t stride;
+        int group;
+    };
+    NormParts norm_parts(const SplitPlan& sp, int64_t r0, int64_t t) const;
     void forward(int64_t base);
     void readout(const PassPlan& plan);
     // One profiled launch (or launcher call) on range k's stream.

@@ -77,8 +77,8 @@ struct GemmArgs {
     // [z K / ksplit, (z + 1) K / ksplit) into y + z * part_stride.
     int ksplit = 1;
     int64_t part_stride = 0;
-    // gemm32_kernel EPI_F32 with FOLD: K chunks of kfold stages (a power of
-    // two) counted from the split's first stage; see launch_gemm_splitk.
+    // gemm32_kernel EPI_F32 with FOLD: K pieces of kfold stages counted
+    // from the split's first stage; see launch_gemm_splitk.
     int kfold = 0;
     // gemm32_kernel: row tiles start at BM * i - mshift (0 <= mshift < BM)
     int64_t mshift = 0;
@@ -648,13 +648,23 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[i][j] = floatx16{};
-    // FOLD: each K chunk's products accumulate from zero in acc and the
-    // chunk sums are added into tot in K order — the sums of a pass that
-    // runs every chunk in a workgroup of its own and adds the partials in
-    // order (fold_chunks).
+    // FOLD: the products of each K piece (g.kfold stages) accumulate from
+    // zero in acc and the piece sums are added into tot in K order — the
+    // sums of a pass that runs every piece in a workgroup of its own and
+    // adds the partials in order (the residual norm's runs).
     floatx16 tot[FOLD ? MI : 1][FOLD ? NJ : 1];
-    const int kfm = g.kfold - 1;  // chunk mask (FOLD)
+    int kleft = g.kfold;  // stages left in the current piece (FOLD)
     bool folded = false;
+    auto fold = [&] {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                tot[i][j] = folded ? tot[i][j] + acc[i][j] : acc[i][j];
+                acc[i][j] = floatx16{};
+            }
+        folded = true;
+    };
 
     const int lr = lane % 32, lh = lane / 32;
     int foff[4];  // the lane's X fragment offset within a 32-row block, per k-step
@@ -744,15 +754,9 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
             compute(cur, wr[PH % R]);
             issue_w(kt + R, wr[PH % R]);
             if constexpr (FOLD) {
-                if (((kt + 1) & kfm) == 0 || kt + 1 == nk) {
-#pragma unroll
-                    for (int i = 0; i < MI; ++i)
-#pragma unroll
-                        for (int j = 0; j < NJ; ++j) {
-                            tot[i][j] = folded ? tot[i][j] + acc[i][j] : acc[i][j];
-                            acc[i][j] = floatx16{};
-                        }
-                    folded = true;
+                if (--kleft == 0 || kt + 1 == nk) {
+                    kleft = g.kfold;
+                    fold();
                 }
             }
             return ++kt < nk;
@@ -785,15 +789,9 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         compute(cur, wr[PH % R]);
         issue_w(kt + NS - 1, wr[PH % R]);
         if constexpr (FOLD) {
-            if (((kt + 1) & kfm) == 0 || kt + 1 == nk) {
-#pragma unroll
-                for (int i = 0; i < MI; ++i)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        tot[i][j] = folded ? tot[i][j] + acc[i][j] : acc[i][j];
-                        acc[i][j] = floatx16{};
-                    }
-                folded = true;
+            if (--kleft == 0 || kt + 1 == nk) {
+                kleft = g.kfold;
+                fold();
             }
         }
         return ++kt < nk;
@@ -1078,7 +1076,7 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         return run32<QUANT, 2, 2, EPI, 4, 4>(s, g);
     } else if constexpr (EPI == EPI_F32) {
         // 32x32x16 tiles (gemm32_kernel) for every M: the same sums per element
-        if (g.kfold > 0) {  // K chunks folded in registers (up to 96-row tiles: the totals fit)
+        if (g.kfold > 0) {  // K pieces added in registers (up to 96-row tiles: the totals fit)
             if (M <= 512) return run32<QUANT, 1, 1, EPI, 4, 4, true>(s, g);
             return run32<QUANT, 3, 1, EPI, 4, 4, true>(s, g);
         }
@@ -1130,7 +1128,7 @@ void launch_gemm_splitk(hipStream_t s, const half_t* x, int64_t ldx, const DevWe
     check(x, ldx, w, ldy, m);
     if (parts < 1 || (parts > 1 && w.cols % (int64_t(G_BK) * parts) != 0))
         fail(E_INVALID, "gemm_splitk: K must split into parts of whole 64-wide stages");
-    if (kfold < 0 || (kfold & (kfold - 1)) != 0) fail(E_INVALID, "gemm_splitk: K chunk stages must be a power of two");
+    if (kfold < 0) fail(E_INVALID, "gemm_splitk: negative K piece length");
     if (parts > 1 && part_stride < m * ldy) fail(E_INVALID, "gemm_splitk: partial outputs overlap");
     if (m == 0) return;
     GemmArgs g{x, ldx, m, w, w, y, ldy, nullptr, {}};

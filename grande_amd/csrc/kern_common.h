@@ -63,6 +63,15 @@ __device__ inline float wave_sum(float v) {
     return sum_lanes_16_32(v);
 }
 
+// f16 of an f32 value that is first rounded to f32: the empty asm hides
+// the producing multiply from the conversion, which the compiler may
+// otherwise fuse into one mixed-precision FMA (a single rounding to f16)
+// in some template instances and not in others.
+__device__ inline half_t f16_rounded(float v) {
+    asm("" : "+v"(v));
+    return half_t(v);
+}
+
 __device__ inline float half_bits_to_f32(uint16_t h) {
     return float(__builtin_bit_cast(half_t, h));
 }

@@ -61,10 +61,12 @@ void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, i
                        float embed_scale, const float* w, float eps, float* x, half_t* hn);
 // y = rmsnorm(a[r]) * w1;  x[r] = (y + x[r]) * scale;  if w2: hn[r] = f16(rmsnorm(x[r]) * w2),
 // else if hn: hn[r] = f16(x[r]).  With parts > 1, a[r] is the sum of the
-// split-K partials a[p * part_stride + r] in order p = 0, 1, ...
+// split-K parts a[z * part_stride + r]: each run of `group` consecutive
+// parts added in order (z = 0, 1, ...), then the runs' sums in order
+// (parts a multiple of group).
 void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float* x, const float* w2,
                           half_t* hn, int64_t t, int64_t d, float eps, float scale, int parts = 1,
-                          int64_t part_stride = 0);
+                          int64_t part_stride = 0, int group = 1);
 // Gemma 4 per-layer inputs (engine.rs:1651-1666, 1728-1750).  pl holds
 // f16(x) . pl_model_proj^T as [t][layers x P] and is replaced by
 // (rmsnorm(pl * proj_scale) * w + f16(table[ids[t], :]) * emb_scale) * out_scale.
@@ -162,18 +164,12 @@ void launch_gemm(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w
 // partial p (K range p) goes to y + p * part_stride; the sum is the
 // consumer's (launch_residual_norm).  More workgroups for narrow-N, deep-K
 // products; each partial's rows are independent of M.
-// kfold > 0 (a power of two): inside each range the products of every
-// kfold stages (64 K each) accumulate from zero and these chunk sums are
-// added in K order — the sums of ranges of one chunk each added in order
-// by launch_fold_chunks.
+// kfold > 0: inside each range the products of every kfold stages (64 K
+// each; the last piece may be shorter) accumulate from zero and these
+// piece sums are added in K order — what ranges of one piece each give
+// when launch_residual_norm adds them in runs of the pieces per range.
 void launch_gemm_splitk(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& w, float* y, int64_t ldy,
                         int64_t m, int parts, int64_t part_stride, int kfold = 0);
-// out + p * out_stride = in[p * chunks] + in[p * chunks + 1] + ... (in this
-// order) for p < parts, over the first n floats of each (n % 4 == 0), with
-// in[c] = in + c * in_stride: the K chunks of a split-K product added as
-// launch_gemm_splitk's kfold adds them.
-void launch_fold_chunks(hipStream_t s, const float* in, int64_t in_stride, int chunks, int parts, int64_t n,
-                        float* out, int64_t out_stride);
 // act[M][F] (f16) = gelu(X . Wg^T) * (X . Wu^T); gelu_tanh, or the exact
 // (erf) form when `erf`.
 void launch_gemm_geglu(hipStream_t s, const half_t* x, int64_t ldx, const DevWeight& wg,

@@ -65,74 +65,124 @@ void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, i
 
 // rmsnorm.wgsl:41-68 in residual mode with the fused second norm: the
 // post-attention / post-feedforward norm of `a` is added into the stream x,
-// then the norm that reads x next writes its f16 input hn.  One wave per
-// row holding the row in registers (NV float4 per lane, element
-// 4 * (lane + 64 j)): every load, the PARTS split-K partials included, is
-// issued before the first reduction; the partials are then added in
-// order p = 0, 1, ...  (PARTS = 0: a runtime count, one partial at a time,
-// for the widest rows with many splits.)
-template <int NV, int PARTS>
+// then the norm that reads x next writes its f16 input hn.  W waves per row
+// (1 up to 768 wide, 2 up to 1,536, 4 above: a function of the width, so
+// a row's sums do not depend on the pass), the row in registers: lane l of
+// the row's wave s holds float4 q = 64 (s + W j) + l, NV of them.  A row's
+// sums of squares are each wave's wave_sum, added in wave order.
+// `a` may come in parts (the K pieces of a split product): part z at
+// a + z * part_stride.  Consecutive runs of `group` parts are added in
+// order into one sum each, and those sums in order into the total:
+//   ((p0 + p1) + ...) + ((p_G + p_G+1) + ...) + ...
+// which is what a product that adds each run in its registers and writes
+// one part per run gives with group 1 — the same bits either way.  The
+// parts are loaded RP at a time (RP: the part count rounded up to a power
+// of two, at most 24 / NV), the first round together with the row and the
+// norm weights, before the first reduction.
+template <int NV, int RP, int W>
 __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ a,
                                                             const float* __restrict__ w1,
                                                             float* __restrict__ x,
                                                             const float* __restrict__ w2,
                                                             half_t* __restrict__ hn, int64_t t,
                                                             int64_t d, float eps, float scale, int parts,
-                                                            int64_t part_stride) {
+                                                            int64_t part_stride, int group) {
+    // Every product and sum rounds on its own: no instance may fuse a
+    // multiply into an add where another does not (the x and hn of a row
+    // must not depend on which instance produced them).
+#pragma clang fp contract(off)
     const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
-    const int64_t row = int64_t(blockIdx.x) * 4 + wave;
-    if (row >= t) return;
-    const int64_t nq = d / 4;
+    const int64_t row = int64_t(blockIdx.x) * (4 / W) + wave / W;
+    const int sub = wave % W;
+    __shared__ float red[2][4];  // per-wave sums of squares (W > 1)
+    // Rows past the end still reach the barriers (W > 1); they load and
+    // store nothing.
+    const bool live = row < t;
+    if (W == 1 && !live) return;
+    const int64_t nq = live ? d / 4 : 0;
+    auto col = [&](int j) { return int64_t(WAVE) * (sub + W * j) + lane; };  // this lane's float4 j
     const float* ar = a + row * d;
     float* xr = x + row * d;
-    float4 av[NV], xv[NV], g1[NV], g2[NV];
-    constexpr int PE = PARTS > 1 ? PARTS - 1 : 1;  // extra partials held in registers
-    float4 pv[PE][NV];
+    float4 av[NV], gs[NV], xv[NV], g1[NV], g2[NV];
+    float4 pv[RP][NV];
+    auto load_round = [&](int z0) {
+#pragma unroll
+        for (int u = 0; u < RP; ++u)
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int64_t q = col(j);
+                if (z0 + u < parts && q < nq) pv[u][j] = *reinterpret_cast<const float4*>(ar + (z0 + u) * part_stride + 4 * q);
+            }
+    };
+    load_round(0);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int64_t q = lane + j * WAVE;
+        const int64_t q = col(j);
         if (q < nq) {
-            av[j] = *reinterpret_cast<const float4*>(ar + 4 * q);
-            if constexpr (PARTS > 1) {
-#pragma unroll
-                for (int p = 1; p < PARTS; ++p)
-                    pv[p - 1][j] = *reinterpret_cast<const float4*>(ar + p * part_stride + 4 * q);
-            }
             xv[j] = *reinterpret_cast<const float4*>(xr + 4 * q);
             g1[j] = *reinterpret_cast<const float4*>(w1 + 4 * q);
             if (w2) g2[j] = *reinterpret_cast<const float4*>(w2 + 4 * q);
         }
     }
+    // gi: position inside the current run; si: runs finished so far.
+    int gi = 0, si = 0;
+    for (int z0 = 0; z0 < parts; z0 += RP) {
+        if (z0 > 0) load_round(z0);
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int64_t q = lane + j * WAVE;
-        if (q < nq) {
-            if constexpr (PARTS > 1) {
+        for (int u = 0; u < RP; ++u) {
+            if (z0 + u >= parts) break;
 #pragma unroll
-                for (int p = 0; p < PARTS - 1; ++p) {
-                    const float4 b = pv[p][j];
-                    av[j].x += b.x, av[j].y += b.y, av[j].z += b.z, av[j].w += b.w;
+            for (int j = 0; j < NV; ++j) {
+                if (col(j) >= nq) continue;
+                const float4 b = pv[u][j];
+                if (si == 0) {  // the first run sums straight into the total
+                    if (gi == 0)
+                        av[j] = b;
+                    else
+                        av[j].x += b.x, av[j].y += b.y, av[j].z += b.z, av[j].w += b.w;
+                } else {
+                    if (gi == 0)
+                        gs[j] = b;
+                    else
+                        gs[j].x += b.x, gs[j].y += b.y, gs[j].z += b.z, gs[j].w += b.w;
+                    if (gi + 1 == group) {
+                        const float4 c = gs[j];
+                        av[j].x += c.x, av[j].y += c.y, av[j].z += c.z, av[j].w += c.w;
+                    }
                 }
-            } else if constexpr (PARTS == 0) {
-                for (int p = 1; p < parts; ++p) {
-                    const float4 b = *reinterpret_cast<const float4*>(ar + p * part_stride + 4 * q);
-                    av[j].x += b.x, av[j].y += b.y, av[j].z += b.z, av[j].w += b.w;
-                }
+            }
+            if (++gi == group) {
+                gi = 0;
+                ++si;
             }
         }
     }
+    // The row's sum of squares: this wave's, then (W > 1) the row's waves'
+    // in order through LDS.
+    auto row_sum = [&](float v, int k) {
+        v = wave_sum(v);
+        if constexpr (W > 1) {
+            if (lane == 0) red[k][wave] = v;
+            __syncthreads();
+            const int w0 = wave - sub;
+            v = red[k][w0];
+#pragma unroll
+            for (int s = 1; s < W; ++s) v += red[k][w0 + s];
+        }
+        return v;
+    };
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
-        if (lane + j * WAVE < nq) {
+        if (col(j) < nq) {
             const float4 v = av[j];
             ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-    const float inv = 1.0f / sqrtf(wave_sum(ss) / float(d) + eps);
+    const float inv = 1.0f / sqrtf(row_sum(ss, 0) / float(d) + eps);
     float ss2 = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int64_t q = lane + j * WAVE;
+        const int64_t q = col(j);
         if (q < nq) {
             const float4 v = av[j], g = g1[j];
             float4 o = xv[j];
@@ -149,50 +199,69 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
         if (!hn) return;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int64_t q = lane + j * WAVE;
+            const int64_t q = col(j);
             if (q < nq) {
                 const float4 v = xv[j];
-                *reinterpret_cast<half4*>(hn + row * d + 4 * q) = half4{half_t(v.x), half_t(v.y), half_t(v.z), half_t(v.w)};
+                *reinterpret_cast<half4*>(hn + row * d + 4 * q) =
+                    half4{f16_rounded(v.x), f16_rounded(v.y), f16_rounded(v.z), f16_rounded(v.w)};
             }
         }
         return;
     }
-    const float inv2 = 1.0f / sqrtf(wave_sum(ss2) / float(d) + eps);
+    const float inv2 = 1.0f / sqrtf(row_sum(ss2, 1) / float(d) + eps);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int64_t q = lane + j * WAVE;
+        const int64_t q = col(j);
         if (q < nq) {
             const float4 v = xv[j], g = g2[j];
-            half4 o = {half_t(v.x * inv2 * g.x), half_t(v.y * inv2 * g.y), half_t(v.z * inv2 * g.z),
-                       half_t(v.w * inv2 * g.w)};
+            half4 o = {f16_rounded(v.x * inv2 * g.x), f16_rounded(v.y * inv2 * g.y), f16_rounded(v.z * inv2 * g.z),
+                       f16_rounded(v.w * inv2 * g.w)};
             *reinterpret_cast<half4*>(hn + row * d + 4 * q) = o;
         }
     }
 }
 
+// Waves per row: a function of the width alone.
+// At most three float4 per lane up to 3,072 wide, so up to eight parts load
+// in one round.
+static int rn_waves(int64_t d) { return d <= 768 ? 1 : (d <= 1536 ? 2 : 4); }
+
+// Parts loaded per round: the part count rounded up to a power of two, up
+// to 24 float4 per lane.
+static int rn_round(int nv, int parts) {
+    int r = 1;
+    while (r < parts && r < 8 && 2 * r * nv <= 24) r *= 2;
+    return r;
+}
+
 void launch_residual_norm(hipStream_t s, const float* a, const float* w1, float* x, const float* w2,
                           half_t* hn, int64_t t, int64_t d, float eps, float scale, int parts,
-                          int64_t part_stride) {
+                          int64_t part_stride, int group) {
     if (t <= 0) return;
     if (d % 4 != 0) fail(E_INVALID, "residual_norm: width must be a multiple of 4");
-    if (parts < 1 || (parts > 1 && (part_stride < t * d || part_stride % 4)))
+    if (parts < 1 || group < 1 || parts % group != 0 || (parts > 1 && (part_stride < t * d || part_stride % 4)))
         fail(E_INVALID, "residual_norm: split-K partials");
-    const int nv = int((d / 4 + WAVE - 1) / WAVE);
-    const dim3 grid(unsigned((t + 3) / 4)), block(256);
-    // Partials in registers while nv * parts <= 24 float4 per lane.
-    const int pk = parts == 1 ? 1 : (nv * parts <= 24 && parts <= 4 ? parts : 0);
-#define OMG_RN(N, P)                                                                                           \
-    case N * 8 + P:                                                                                            \
-        residual_norm_kernel<N, P><<<grid, block, 0, s>>>(a, w1, x, w2, hn, t, d, eps, scale, parts, part_stride); \
+    if (d > 4096) fail(E_INVALID, "residual_norm: width above 4096");
+    const int w = rn_waves(d);
+    const int nv = int((d / 4 + WAVE * w - 1) / (WAVE * w));  // float4 per lane
+    const dim3 grid(unsigned((t + 4 / w - 1) / (4 / w))), block(256);
+    const int rp = rn_round(nv, parts);
+#define OMG_RN(N, R, W)                                                                                          \
+    case (N * 16 + R) * 8 + W:                                                                                  \
+        residual_norm_kernel<N, R, W><<<grid, block, 0, s>>>(a, w1, x, w2, hn, t, d, eps, scale, parts,          \
+                                                             part_stride, group);                                \
         break;
-#define OMG_RNP(N) OMG_RN(N, 0) OMG_RN(N, 1) OMG_RN(N, 2) OMG_RN(N, 3) OMG_RN(N, 4)
-    if (nv > 16) fail(E_INVALID, "residual_norm: width above 4096");
-    switch (nv * 8 + pk) {
-        OMG_RNP(1) OMG_RNP(2) OMG_RNP(3) OMG_RNP(4) OMG_RNP(5) OMG_RNP(6) OMG_RNP(7) OMG_RNP(8)
-        OMG_RNP(9) OMG_RNP(10) OMG_RNP(11) OMG_RNP(12) OMG_RNP(13) OMG_RNP(14) OMG_RNP(15) OMG_RNP(16)
+#define OMG_RNR(N, W) OMG_RN(N, 1, W) OMG_RN(N, 2, W) OMG_RN(N, 4, W) OMG_RN(N, 8, W)
+    // one to three float4 per lane on one, two or four waves; four on four
+    // from 3,076 wide
+    switch ((nv * 16 + rp) * 8 + w) {
+        OMG_RNR(1, 1) OMG_RNR(2, 1) OMG_RNR(3, 1) OMG_RNR(2, 2) OMG_RNR(3, 2) OMG_RNR(1, 4) OMG_RNR(2, 4)
+        OMG_RNR(3, 4) OMG_RN(4, 1, 4) OMG_RN(4, 2, 4) OMG_RN(4, 4, 4)
+        OMG_RN(4, 1, 2) OMG_RN(4, 2, 2) OMG_RN(4, 4, 2) OMG_RN(5, 1, 2) OMG_RN(5, 2, 2) OMG_RN(5, 4, 2)
+        OMG_RN(6, 1, 2) OMG_RN(6, 2, 2) OMG_RN(6, 4, 2)
         default: fail(E_INVALID, "residual_norm: unsupported shape");
     }
-#undef OMG_RNP
+#undef OMG_RNR
 #undef OMG_RN
     OMG_HIP(hipGetLastError());
 }
@@ -711,40 +780,6 @@ void launch_label_lse(hipStream_t s, const float* logits, int64_t nrows, int64_t
     if (vocab <= 0 || nlabels <= 0 || nblocks <= 0) fail(E_INVALID, "label_lse: empty row or no labels");
     label_lse_kernel<<<dim3(unsigned(nrows)), dim3(256), 0, s>>>(logits, vocab, part, nblocks, nrows, labels,
                                                                  nlabels, out);
-    OMG_HIP(hipGetLastError());
-}
-
-// ------------------------------------------------------ K-chunk fold
-
-// A thread per four floats of one output part; the chunks' loads go out
-// eight at a time, the adds stay in chunk order.
-__global__ __launch_bounds__(256) void fold_chunks_kernel(const float* __restrict__ in, int64_t in_stride,
-                                                          int chunks, int64_t n, float* __restrict__ out,
-                                                          int64_t out_stride) {
-    const int64_t q = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (q >= n / 4) return;
-    const int64_t p = blockIdx.y;
-    const float* base = in + p * chunks * in_stride + 4 * q;
-    float4 acc = *reinterpret_cast<const float4*>(base);
-    for (int c0 = 1; c0 < chunks; c0 += 8) {
-        float4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (c0 + u < chunks) v[u] = *reinterpret_cast<const float4*>(base + (c0 + u) * in_stride);
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (c0 + u < chunks) acc.x += v[u].x, acc.y += v[u].y, acc.z += v[u].z, acc.w += v[u].w;
-    }
-    *reinterpret_cast<float4*>(out + p * out_stride + 4 * q) = acc;
-}
-
-void launch_fold_chunks(hipStream_t s, const float* in, int64_t in_stride, int chunks, int parts, int64_t n,
-                        float* out, int64_t out_stride) {
-    if (n <= 0 || parts <= 0) return;
-    if (n % 4 || chunks < 1 || in_stride % 4 || out_stride % 4 || in_stride < n || out_stride < n)
-        fail(E_INVALID, "fold_chunks: shape");
-    fold_chunks_kernel<<<dim3(unsigned((n / 4 + 255) / 256), unsigned(parts)), dim3(256), 0, s>>>(
-        in, in_stride, chunks, n, out, out_stride);
     OMG_HIP(hipGetLastError());
 }
 

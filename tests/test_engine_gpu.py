@@ -122,21 +122,25 @@ def test_resident_prefix_matches_full_pass():
             assert all(np.array_equal(x, y) for x, y in zip(a.rows, b.rows))
 
 
-def test_deep_k_chunks_same_rows_in_long_and_short_passes():
-    """A down projection deep enough to sum K in 1,024-wide chunks (width
-    2,304 > 2,048: one split of K 4,096, 4 chunks): the long cold pass folds
-    the chunks in the GEMM's registers, the short warm pass on the resident
-    prefix runs a chunk per workgroup and adds the partials in order —
-    bit-equal rows, and within the f32 oracle's reach."""
-    cfg = gemma3_tiny(d=2304, ff=4096, layers=1, sliding=[False])
+@pytest.mark.parametrize("d,ff", [(2304, 4096), (64, 16384)])
+def test_deep_k_chunks_same_rows_in_long_and_short_passes(d, ff):
+    """Down projections deep enough to sum K in 1,024-wide pieces: width
+    2,304 > 2,048 (one split of K 4,096, four pieces) and width 64 (four
+    splits of 4,096, four pieces each: the residual norm adds the short
+    pass's sixteen parts in four runs of four, over two rounds of loads).
+    The long cold pass adds the pieces in the GEMM's registers, the short
+    warm pass on the resident prefix runs a piece per workgroup and the
+    norm adds the parts in the same order — bit-equal rows, and within the
+    f32 oracle's reach."""
+    cfg = gemma3_tiny(d=d, ff=ff, layers=1, sliding=[False])
     eng, plain, _, _ = build(cfg, 21, g.Q4, g.F16, capacity=1024)
     rng = np.random.default_rng(21)
     prefix = rng.integers(0, 40, 520).tolist()
     branches = [BranchTokens(rng.integers(0, 40, 12).tolist(), [3, 11]), BranchTokens(rng.integers(0, 40, 9).tolist(), [8])]
     eng.evict_resident()
-    cold = eng.evaluate(prefix, branches, Want.HIDDEN)  # 541 rows: folded in registers
+    cold = eng.evaluate(prefix, branches, Want.HIDDEN)  # 541 rows: pieces added in registers
     assert eng.prefix_source() == PrefixSource.DECODED
-    warm = eng.evaluate(prefix, branches, Want.HIDDEN)  # 21 rows: a chunk per workgroup
+    warm = eng.evaluate(prefix, branches, Want.HIDDEN)  # 21 rows: a piece per workgroup
     assert eng.prefix_source() == PrefixSource.RESIDENT
     for a, b in zip(cold, warm):
         assert all(np.array_equal(x, y) for x, y in zip(a.rows, b.rows))
