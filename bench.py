@@ -201,6 +201,59 @@ def c_api_ms(eng, groups, labels, reps: int = 15) -> dict:
             "reps": reps, "calls": "C ABI, arguments marshalled once"}
 
 
+def small_batch_leg(eng, prefix, branch, labels, mc, dtype, P: int, BT: int, reps: int, no_graph: bool) -> dict:
+    """One branch of BT tokens on the resident P-token state, every rep
+    preceded by a device-to-device copy of 512 MiB (1 GiB of traffic, twice
+    the 256 MB MALL) so weights, embedding and K/V come from HBM; one graph
+    replay per rep, timed to its end.  Per-kernel HIP-event times of three
+    more flushed reps (eager launches), and each product's algorithmic bytes
+    and the rate its interval implies."""
+    from grande_amd import Group, Want
+
+    one = [branch]
+    eng.evaluate(prefix, one, Want.LABELS_LSE, labels)  # the state becomes resident
+    eng.prepare([Group(prefix, one)], Want.LABELS_LSE, labels, first_resident=True)
+    if not no_graph:
+        eng.graph(True)
+    eng.launch()
+    eng.sync()
+    flush = MallFlush(512 << 20)
+    times = []
+    for _ in range(reps):
+        flush()
+        t = time.perf_counter()
+        eng.launch()
+        eng.sync()
+        times.append(time.perf_counter() - t)
+    eng.graph(False)
+    eng.profile(True)
+    for _ in range(3):
+        flush()
+        eng.launch()
+        eng.sync()
+    sprof = eng.profile_report()
+    eng.profile(False)
+    flush.close()
+    sb = pass_bytes(mc, dtype, P, 1, BT)
+    s_ms = float(np.median(times)) * 1e3
+    gbs = sb["total"] / (s_ms * 1e-3) / 1e9
+    small = {"branches": 1, "branch_tokens": BT, "reps": reps, "ms_median": round(s_ms, 4),
+             "ms_min": round(min(times) * 1e3, 4), "mall_flush_bytes": 2 * flush.nbytes,
+             "algorithmic_bytes": {k: int(v) for k, v in sb.items()}, "gb_per_s": round(gbs, 1),
+             "hbm_peak_gb_per_s": HBM_PEAK_GBS, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+             "kernels": {name: {"launches_per_step": n // 3, "avg_us": round(ms / n * 1e3, 2)}
+                         for name, (n, ms) in sprof.items()}}
+    # per-launch algorithmic bytes and rate of the products and the norm
+    # (HIP-event intervals: each includes the dispatch gap before it)
+    for name, nbytes in kernel_bytes(mc, dtype, BT).items():
+        k = small["kernels"].get(name)
+        if k and k["avg_us"] > 0:
+            k["bytes"] = int(nbytes)
+            k["gb_per_s"] = round(nbytes / (k["avg_us"] * 1e-6) / 1e9, 1)
+            k["hbm_frac"] = round(k["gb_per_s"] / HBM_PEAK_GBS, 4)
+    return small
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -210,6 +263,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--small-reps", type=int, default=10,
                     help="reps of the small-batch leg (one branch on the resident state, MALL flushed)")
+    ap.add_argument("--no-4b", action="store_true", help="skip the small-batch leg at the 4B shape (C5)")
     ap.add_argument("--no-graph", action="store_true",
                     help="eager launches only (no HIP graph capture or replay): for runs under rocprofv3, whose "
                          "kernel tracing faulted inside hipGraphLaunch")
@@ -334,48 +388,29 @@ def main() -> int:
     # and K/V come from HBM; each rep is one graph launch, timed to its end.
     small = None
     if args.small_reps > 0:
-        one = branches[:1]
-        eng.evaluate(prefix, one, Want.LABELS_LSE, labels)  # resident state stays
-        eng.prepare([Group(prefix, one)], Want.LABELS_LSE, labels, first_resident=True)
-        if not args.no_graph:
-            eng.graph(True)
-        eng.launch()
-        eng.sync()
-        flush = MallFlush(512 << 20)
-        times = []
-        for _ in range(args.small_reps):
-            flush()
-            t = time.perf_counter()
-            eng.launch()
-            eng.sync()
-            times.append(time.perf_counter() - t)
-        eng.graph(False)
-        # per-kernel HIP-event times of flushed reps (eager launches)
-        eng.profile(True)
-        for _ in range(3):
-            flush()
-            eng.launch()
-            eng.sync()
-        sprof = eng.profile_report()
-        eng.profile(False)
-        flush.close()
-        sb = pass_bytes(mc, spec["dtype"], P, 1, BT)
-        s_ms = float(np.median(times)) * 1e3
-        gbs = sb["total"] / (s_ms * 1e-3) / 1e9
-        small = {"branches": 1, "branch_tokens": BT, "reps": args.small_reps, "ms_median": round(s_ms, 4),
-                 "ms_min": round(min(times) * 1e3, 4), "mall_flush_bytes": 2 * flush.nbytes,
-                 "algorithmic_bytes": {k: int(v) for k, v in sb.items()}, "gb_per_s": round(gbs, 1),
-                 "hbm_peak_gb_per_s": HBM_PEAK_GBS, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                 "kernels": {name: {"launches_per_step": n // 3, "avg_us": round(ms / n * 1e3, 2)}
-                             for name, (n, ms) in sprof.items()}}
-        # per-launch algorithmic bytes and rate of the products and the norm
-        # (HIP-event intervals: each includes the dispatch gap before it)
-        for name, nbytes in kernel_bytes(mc, spec["dtype"], BT).items():
-            k = small["kernels"].get(name)
-            if k and k["avg_us"] > 0:
-                k["bytes"] = int(nbytes)
-                k["gb_per_s"] = round(nbytes / (k["avg_us"] * 1e-6) / 1e9, 1)
-                k["hbm_frac"] = round(k["gb_per_s"] / HBM_PEAK_GBS, 4)
+        small = small_batch_leg(eng, prefix, branches[0], labels, mc, spec["dtype"], P, BT, args.small_reps,
+                                args.no_graph)
+    # The same leg at the 4B shape (C5: one 40-token branch over its
+    # 8,000-token state), where the products are large enough to show an
+    # HBM rate: 30 MB gate/up, 16 MB down per launch.
+    small_4b = None
+    if args.small_reps > 0 and args.config == "c2" and not args.no_4b:
+        s5 = g.BASELINE_CONFIGS["c5"]
+        m5 = s5["model"]
+        cfg5 = g.config_json(**m5)
+        P5, BT5 = s5["state"], s5["branch_tokens"]
+        rng5 = np.random.default_rng(SEED + 5)
+        prefix5 = rng5.integers(0, m5["vocab"], P5).tolist()
+        branch5 = BranchTokens(rng5.integers(0, m5["vocab"], BT5).tolist(), [BT5 - 1])
+        w5 = g.Weights.synth(cfg5, SEED + 5, s5["dtype"], s5["dtype"])
+        eng5 = g.Engine.new(w5, P5 + BT5 + 64, 64)
+        del w5
+        small_4b = small_batch_leg(eng5, prefix5, branch5, labels, m5, s5["dtype"], P5, BT5, args.small_reps,
+                                   args.no_graph)
+        w5name = {g.Q4: "Q4_0", g.Q8: "Q8_0", g.F16: "F16"}[s5["dtype"]]
+        small_4b["workload"] = f"c5: Gemma-3-4B-shaped {w5name}, one {BT5}-token branch on the resident " \
+                               f"{P5}-token state"
+        eng5.close()
 
     kernels = {}
     for name, (n, ms) in prof.items():
@@ -441,6 +476,7 @@ def main() -> int:
                           "algorithmic_bytes": int(wb["total"]), "gb_per_s": round(wb["total"] / warm_s / 1e9, 1),
                           "hbm_frac": round(wb["total"] / warm_s / 1e9 / HBM_PEAK_GBS, 4)},
         "small_batch": small,
+        "small_batch_4b": small_4b,
         "load_s": round(load_s, 2),
     }
 
