@@ -529,9 +529,10 @@ struct Cfg32 {
     // floats), eight partial sums of squares and a scale per row in LDS
     // after the K loop.
     static constexpr int QK_TS = 260;
-    static constexpr int QK_LDS = EPI == EPI_QKPREP ? BM * (QK_TS + 9) * 4 : 0;  // + [BM][8] sums, [BM] scales
+    static constexpr int QK_LDS = EPI == EPI_QKPREP ? BM * (QK_TS + 17) * 4 : 0;  // + [BM][16] sums, [BM] scales
     static constexpr int LDS = NS * X_BYTES > QK_LDS ? NS * X_BYTES : QK_LDS;
-    static_assert(EPI != EPI_QKPREP || (BN == 256 && NW == 4), "the q/k/v epilogue: one 256-wide head, a thread per dimension");
+    static_assert(EPI != EPI_QKPREP || (BN == 256 && (NW == 4 || NW == 8)),
+                  "the q/k/v epilogue: one 256-wide head on four or eight waves");
     static_assert(LDS <= 160 * 1024, "ring larger than the LDS");
     static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
     static_assert(NS >= 3, "ring needs >= 3 slots: one read into registers, one landing, one in flight");
@@ -711,9 +712,10 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     };
 
     // EPI_QKPREP, q and k heads: the rope rows of the rows this thread
-    // finishes (8 rows per pass of the workgroup, row p * 8 + tid / 32),
+    // finishes (RP rows per pass of the workgroup, row p * RP + tid / 32),
     // loaded now so their latency hides behind the K loop.
-    constexpr int QK_PASSES = EPI == EPI_QKPREP ? BM / 8 : 1;
+    constexpr int QK_RP = NW * WAVE / 32;  // rows per pass: 32 threads per row
+    constexpr int QK_PASSES = EPI == EPI_QKPREP ? BM / QK_RP : 1;
     int qpos[QK_PASSES];
     if constexpr (EPI == EPI_QKPREP) {
         const QkArgs& a = g.qk;
@@ -724,7 +726,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
             // row, clamped into the pass), so the loads go out back to back
             // with no branch between them; rows outside the pass and the v
             // head take position 0.
-            const int r = p * 8 + tid / 32;
+            const int r = p * QK_RP + tid / 32;
             const int64_t m = m0 + r < 0 ? 0 : (m0 + r < M ? m0 + r : M - 1);
             const int pos = a.meta[4 * (a.base + m)];
             qpos[p] = qk_head && row_ok(r) ? (pos < 0 ? 0 : (pos >= a.rope_rows ? int(a.rope_rows - 1) : pos)) : 0;
@@ -809,11 +811,16 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     }
 
     if constexpr (EPI == EPI_QKPREP) {
+        // Every multiply-add that rounds once is an explicit fmaf and every
+        // f16 comes from an f32 value (nothing for the compiler to fuse in
+        // one tile shape and not another): a row's outputs are the same
+        // bits from the four-wave and the eight-wave tile.
         // qk_prep.wgsl:66-114 on the tile's rows, without cross-lane
-        // traffic: each lane's sum of squares over its 32 accumulators of a
-        // row goes to LDS with the f32 tile (the ring is free: every DMA
-        // landed, every read done); a row's RMS is the sum of its eight
-        // partials in a fixed order.  q and k heads: 32 threads per row,
+        // traffic: each lane's sums of squares over its 16 accumulators of
+        // a row in each 32-column block go to LDS with the f32 tile (the
+        // ring is free: every DMA landed, every read done); a row's RMS is
+        // the sum of its sixteen partials (block, lane half) in a fixed
+        // order, whichever wave held which block.  q and k heads: 32 threads per row,
         // thread c holding head dimensions 4c..4c+3 and their RoPE partners
         // 128 + 4c..: RMS norm with the head's weight, RoPE, query scale,
         // f16 q rows or k cache rows.  v head: (optional) RMS norm, then
@@ -824,22 +831,22 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         constexpr int HD = 256, TS = P::QK_TS, HALF = HD / 2;
         const QkArgs& a = g.qk;
         float* T = reinterpret_cast<float*>(smem);
-        float* ssp = T + BM * TS;  // [BM][8] partial sums of squares
+        float* ssp = T + BM * TS;  // [BM][16] partial sums of squares
         lds_barrier();
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-            float ss = 0.0f;
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j)
+            for (int j = 0; j < NJ; ++j) {
+                float ss = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     *reinterpret_cast<float4*>(T + (i * 32 + lr) * TS + wave * WR + j * 32 + 8 * q + 4 * lh) =
                         make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ss += acc[i][j][4 * q + r] * acc[i][j][4 * q + r];
+                    for (int r = 0; r < 4; ++r) ss = fmaf(acc[i][j][4 * q + r], acc[i][j][4 * q + r], ss);
                 }
-            ssp[(i * 32 + lr) * 8 + 2 * wave + lh] = ss;
-        }
+                ssp[(i * 32 + lr) * 16 + 2 * (wave * NJ + j) + lh] = ss;
+            }
         const int slot = int(n0 / HD);
         const int H = a.heads, KV = a.kv_heads;
         const bool is_v = slot >= H + KV;
@@ -855,13 +862,13 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
             }
         }
         lds_barrier();
-        // Each row's scale once, from the sum of its eight partials in
+        // Each row's scale once, from the sum of its sixteen partials in
         // order; the passes below read it.
-        float* rinv = ssp + BM * 8;  // [BM] row scales
+        float* rinv = ssp + BM * 16;  // [BM] row scales
         if (tid < BM) {
             float ss = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ss += ssp[tid * 8 + k];
+            for (int k = 0; k < 16; ++k) ss += ssp[tid * 16 + k];
             rinv[tid] = 1.0f / sqrtf(ss / float(HD) + a.eps);
         }
         lds_barrier();
@@ -875,7 +882,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
             const int rot = int(a.rope_dims / 2);
 #pragma unroll
             for (int p = 0; p < QK_PASSES; ++p) {
-                const int r = p * 8 + tid / 32;
+                const int r = p * QK_RP + tid / 32;
                 if (!row_ok(r)) continue;
                 const float inv = rinv[r];
                 const float4 vl = *reinterpret_cast<const float4*>(T + r * TS + d0);
@@ -888,8 +895,8 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
                 for (int k = 0; k < 4; ++k) {
                     const float y0 = v_lo[k] * inv * w_lo[k], y1 = v_hi[k] * inv * w_hi[k];
                     if (d0 + k < rot) {
-                        o_lo[k] = y0 * cs[k] - y1 * sn[k];
-                        o_hi[k] = y1 * cs[k] + y0 * sn[k];
+                        o_lo[k] = fmaf(y0, cs[k], -(y1 * sn[k]));
+                        o_hi[k] = fmaf(y1, cs[k], y0 * sn[k]);
                     } else {
                         o_lo[k] = y0;
                         o_hi[k] = y1;
@@ -898,9 +905,11 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
                 const int64_t tok = m0 + r, row = a.base + tok;
                 half_t* dst = is_q ? a.q16 + (tok * H + head) * HD : a.kc + (int64_t(head) * a.cap_pad + row) * HD;
                 *reinterpret_cast<half4*>(dst + d0) =
-                    half4{half_t(o_lo[0] * sc), half_t(o_lo[1] * sc), half_t(o_lo[2] * sc), half_t(o_lo[3] * sc)};
+                    half4{f16_rounded(o_lo[0] * sc), f16_rounded(o_lo[1] * sc), f16_rounded(o_lo[2] * sc),
+                          f16_rounded(o_lo[3] * sc)};
                 *reinterpret_cast<half4*>(dst + HALF + d0) =
-                    half4{half_t(o_hi[0] * sc), half_t(o_hi[1] * sc), half_t(o_hi[2] * sc), half_t(o_hi[3] * sc)};
+                    half4{f16_rounded(o_hi[0] * sc), f16_rounded(o_hi[1] * sc), f16_rounded(o_hi[2] * sc),
+                          f16_rounded(o_hi[3] * sc)};
             }
             return;
         }
@@ -915,8 +924,8 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
             const int64_t t0 = kh / 64 * 64;
             const int hf = int((kh % 64) / 32);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int item = tid + 256 * u;
+            for (int u = 0; u < 1024 / (NW * WAVE); ++u) {
+                const int item = tid + NW * WAVE * u;
                 const int dim = item / 4, cc = item % 4;
                 half_t* dst = a.vt + ((int64_t(head) * (a.cap_pad / 64) + t0 / 64) * HD + dim) * 64 + 8 * (4 * hf + cc);
                 half_t h[8];
@@ -927,7 +936,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
                     const bool in = row_ok(r);
                     all = all && in;
                     const float v = T[r * TS + dim];
-                    h[e] = half_t(a.v_norm ? v * rinv[r] : v);
+                    h[e] = f16_rounded(a.v_norm ? v * rinv[r] : v);
                 }
                 if (!all) {
                     // a pass edge: the chunk's other keys keep the cache's values
@@ -1073,7 +1082,9 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         if (K >= 4096) return run<QUANT, 6, 2, EPI, 2, 4>(s, g);
         return run<QUANT, 8, 1, EPI, 2, 4>(s, g);
     } else if constexpr (EPI == EPI_QKPREP) {
-        if (M <= 512) return run32<QUANT, 1, 2, EPI, 4, 4>(s, g);
+        // short passes: one head on eight waves of one 32-row block each
+        // (half the decode per wave and K stage of the four-wave tile)
+        if (M <= 512) return run32<QUANT, 1, 1, EPI, 4, 8>(s, g);
         return run32<QUANT, 2, 2, EPI, 4, 4>(s, g);
     } else if constexpr (EPI == EPI_F32) {
         // 32x32x16 tiles (gemm32_kernel) for every M: the same sums per element
