@@ -1082,9 +1082,14 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         if (K >= 4096) return run<QUANT, 6, 2, EPI, 2, 4>(s, g);
         return run<QUANT, 8, 1, EPI, 2, 4>(s, g);
     } else if constexpr (EPI == EPI_QKPREP) {
-        // short passes: one head on eight waves of one 32-row block each
-        // (half the decode per wave and K stage of the four-wave tile)
+        // One head on eight waves of one 32-row weight block each (half the
+        // decode per wave and K stage of the four-wave tile): short passes,
+        // and long ones whose 64-row X tile stays resident (K <= 768; the
+        // 270M model's cold q/k/v 15.9 -> 13.3 us, its cold pass -3.2%); at
+        // K 2,560 (the 4B model) eight waves through the ring were slower
+        // (396 -> 522 us a launch) than four of two blocks each.
         if (M <= 512) return run32<QUANT, 1, 1, EPI, 4, 8>(s, g);
+        if (K <= 768) return run32<QUANT, 2, 1, EPI, 4, 8>(s, g);
         return run32<QUANT, 2, 2, EPI, 4, 4>(s, g);
     } else if constexpr (EPI == EPI_F32) {
         // 32x32x16 tiles (gemm32_kernel) for every M: the same sums per element
@@ -1097,10 +1102,18 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
         if (g.ksplit > 1) return run32<QUANT, 3, 1, EPI, 4, 4>(s, g);  // split K: twice the tiles
         return run32<QUANT, 2, 1, EPI, 4, 4>(s, g);
     } else {
-        // Short passes: four ring slots from K 1,024 (one flushed 40-token
-        // branch of the 4B model: gate/up 27.5 -> 24.3 us; two slots are
-        // better at the 270M model's K 640, whose warm pass ran 0.6% slower
-        // with four).  The ring depth does not change any sum.
+        if constexpr (EPI == EPI_GELU_TANH) {
+            // The decoder's gated products on the 32x32x16 kernel, weights
+            // in registers: 96 x 128 outputs, 32 x 128 for short passes
+            // (same box against the 16x16x32 kernel below: the 270M
+            // model's cold gate/up 20.7 -> 20.2 us, warm 9.7 -> 9.0 us; the
+            // 4B model's cold gate/up 1,890 -> 1,565 us, its cold pass
+            // -4.8%, warm -5.4%; E2B's warm pass -8.5%).
+            if (M <= 512) return run32<QUANT, 1, 2, EPI, 4, 4>(s, g);
+            return run32<QUANT, 3, 2, EPI, 4, 4>(s, g);
+        }
+        // Short passes: four ring slots from K 1,024 (two are better at
+        // K 640).  The ring depth does not change any sum.
         if (M <= 512) {
             if (K >= 1024) return run<QUANT, 4, 2, EPI, 4, 4>(s, g);
             return run<QUANT, 4, 2, EPI, 2, 4>(s, g);
