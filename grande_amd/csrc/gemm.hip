@@ -1108,9 +1108,12 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
             // (same box against the 16x16x32 kernel below: the 270M
             // model's cold gate/up 20.7 -> 20.2 us, warm 9.7 -> 9.0 us; the
             // 4B model's cold gate/up 1,890 -> 1,565 us, its cold pass
-            // -4.8%, warm -5.4%; E2B's warm pass -8.5%).
+            // -4.8%, warm -5.4%; E2B's warm pass -8.5%).  Ring slots: three
+            // for long passes (270M cold pass -0.5%), four for short ones
+            // (three: the flushed one-branch passes 1-5% slower); 128-row
+            // or 64-column tiles and five slots were 3-10% slower.
             if (M <= 512) return run32<QUANT, 1, 2, EPI, 4, 4>(s, g);
-            return run32<QUANT, 3, 2, EPI, 4, 4>(s, g);
+            return run32<QUANT, 3, 2, EPI, 3, 4>(s, g);
         }
         // Short passes: four ring slots from K 1,024 (two are better at
         // K 640).  The ring depth does not change any sum.
