@@ -273,7 +273,8 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     // window + branch long), at least 384 keys and at most ~8 chunks over
     // the cache on global layers.  Measured at C2 (same box): global chunks
     // of 384 keys against 512: cold pass -0.4%, warm -0.4%, one-branch -1%;
-    // 256 keys: short passes -1.3 / -1.9% but the cold pass +0.5%; sliding
+    // 256 keys: short passes -1.3 / -1.9% but the cold pass +0.5%; 448 and
+    // 320 keys (after the GEMM changes): cold +0.3% and +1.6%; sliding
     // chunks of 384 or 512 keys: every pass 2.5-6% slower.
     {
         const int64_t kt = attention_key_tile();
