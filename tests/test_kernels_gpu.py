@@ -96,6 +96,29 @@ def test_gemm_rows_are_independent_of_m():
         assert np.array_equal(o, outs[0][:o.shape[0]])
 
 
+@pytest.mark.parametrize("k", [640, 2560])
+def test_gated_rows_are_independent_of_m(k):
+    """The gated product's rows are the same bits whichever tile shape the
+    launch's M selects (96-row tiles for long passes, 32-row tiles with a
+    deeper ring for short ones): the basis of the bit-equal warm and
+    isolated rows through the feed-forward."""
+    rng = np.random.default_rng(11 + k)
+    n = 512
+    tg, _ = weight(rng, n, k, g.Q4, "gate")
+    tu, _ = weight(rng, n, k, g.Q4, "up")
+    wg, wu = g.DeviceWeight(tg), g.DeviceWeight(tu)
+    x = rng.uniform(-1, 1, (2384, k)).astype(np.float16)
+    outs = []
+    for m in (2384, 513, 384, 40, 1):
+        act = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+        xd = dev(x[:m])  # held until the launch has run
+        wg.gemm_geglu(wu, xd.data_ptr(), k, m, act.data_ptr(), n)
+        torch.cuda.synchronize()
+        outs.append(act.cpu().numpy())
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0][:o.shape[0]])
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_embed_gather_bit_exact(dtype):
     """embed.wgsl:15-48 = reference.rs:182-189: x = deq(E[id]) * sqrt(d),
