@@ -66,7 +66,7 @@ void launch_embed_norm(hipStream_t s, const DevWeight& E, const uint32_t* ids, i
 // rmsnorm.wgsl:41-68 in residual mode with the fused second norm: the
 // post-attention / post-feedforward norm of `a` is added into the stream x,
 // then the norm that reads x next writes its f16 input hn.  W waves per row
-// (1 up to 768 wide, 2 up to 1,536, 4 above: a function of the width, so
+// (1 up to 512 wide, 2 up to 1,536, 4 above: a function of the width, so
 // a row's sums do not depend on the pass), the row in registers: lane l of
 // the row's wave s holds float4 q = 64 (s + W j) + l, NV of them.  A row's
 // sums of squares are each wave's wave_sum, added in wave order.
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
 // Waves per row: a function of the width alone.
 // At most three float4 per lane up to 3,072 wide, so up to eight parts load
 // in one round.
-static int rn_waves(int64_t d) { return d <= 768 ? 1 : (d <= 1536 ? 2 : 4); }
+static int rn_waves(int64_t d) { return d <= 512 ? 1 : (d <= 1536 ? 2 : 4); }
 
 // Parts loaded per round: the part count rounded up to a power of two, up
 // to 24 float4 per lane.
