@@ -508,9 +508,13 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm_kernel(GemmArgs g) {
 //   load stage kt + NS - 1's weights into the register slot just used.
 // Every wave issues the same memory instructions in every iteration (past
 // the end they read empty resources), so the wait counts are constants.
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_ = 4>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_ = 4, bool PAIR_ = false>
 struct Cfg32 {
     static constexpr bool GATED = EPI == EPI_GELU_TANH || EPI == EPI_GELU_ERF;
+    // PAIR: a gated tile whose waves hold one matrix each, the first half
+    // the gate blocks and the second half the matching up blocks; the gate
+    // sums go through LDS to the up waves, which finish the tile.
+    static constexpr bool PAIR = PAIR_;
     static constexpr int NW = NW_, T = NW * WAVE;
     static constexpr int BM = 32 * MI;
     static constexpr int WR = 32 * NJ;                 // weight rows per wave
@@ -530,11 +534,14 @@ struct Cfg32 {
     // after the K loop.
     static constexpr int QK_TS = 260;
     static constexpr int QK_LDS = EPI == EPI_QKPREP ? BM * (QK_TS + 17) * 4 : 0;  // + [BM][16] sums, [BM] scales
-    static constexpr int LDS = NS * X_BYTES > QK_LDS ? NS * X_BYTES : QK_LDS;
+    static constexpr int PAIR_LDS = PAIR ? (NW / 2) * MI * NJ * 16 * WAVE * 4 : 0;  // the gate waves' sums
+    static constexpr int EPI_LDS = QK_LDS > PAIR_LDS ? QK_LDS : PAIR_LDS;           // LDS after the K loop
+    static constexpr int LDS = NS * X_BYTES > EPI_LDS ? NS * X_BYTES : EPI_LDS;
     static_assert(EPI != EPI_QKPREP || (BN == 256 && (NW == 4 || NW == 8)),
                   "the q/k/v epilogue: one 256-wide head on four or eight waves");
     static_assert(LDS <= 160 * 1024, "ring larger than the LDS");
-    static_assert(!GATED || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
+    static_assert(!PAIR || (GATED && NW % 2 == 0), "paired tiles: gated, gate and up waves in pairs");
+    static_assert(!GATED || PAIR || NJ % 2 == 0, "gated tiles pair gate and up row blocks");
     static_assert(NS >= 3, "ring needs >= 3 slots: one read into registers, one landing, one in flight");
     static_assert(WL + (NS - 2) * C <= 63, "vmcnt range");
 };
@@ -548,9 +555,9 @@ __device__ inline bool run_phases(F& f, std::index_sequence<I...>) {
 // lands in LDS in the prologue, one slot per stage, and the K loop runs
 // with no barrier and no X wait (the weights are each wave's own).  Same
 // MFMA sequence, same sums; chosen per launch when the tile fits.
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_, bool FOLD, bool XR>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW_, bool FOLD, bool XR, bool PAIR>
 __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
-    using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW_>;
+    using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW_, PAIR>;
     static_assert(!FOLD || EPI == EPI_F32, "K chunks: f32 products only");
     constexpr bool GATED = P::GATED;
     constexpr int NW = P::NW, BM = P::BM, BN = P::BN, WR = P::WR, PK = P::PK, PM = P::PM, R = P::R;
@@ -586,12 +593,17 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
     }
 
     // This wave's row blocks: j < NJ / 2 of the gate matrix and the rest of
-    // the up matrix when gated.  Block j's packet of stage st sits at
+    // the up matrix when gated (PAIR: all NJ of the gate matrix in the
+    // first half of the waves, of the up matrix in the second, wave w and
+    // w + NW / 2 on the same blocks).  Block j's packet of stage st sits at
     // st * PK + bj * stages * PK from the matrix's first block of the tile.
     const int64_t stages = g.w0.stages, rblocks = (N + 31) / 32, rb0 = n0 / 32;
     const int64_t live_blocks = rblocks - rb0;  // > 0: the tile starts inside N
-    auto mat_of = [&](int j) { return GATED && j >= NJ / 2 ? 1 : 0; };
-    auto blk_of = [&](int j) { return GATED ? wave * (NJ / 2) + (j % (NJ / 2)) : wave * NJ + j; };
+    const int pw = PAIR ? wave % (NW / 2) : wave;  // the wave's place among the waves of its matrix
+    auto mat_of = [&](int j) { return PAIR ? (wave >= NW / 2 ? 1 : 0) : (GATED && j >= NJ / 2 ? 1 : 0); };
+    auto blk_of = [&](int j) {
+        return PAIR ? pw * NJ + j : (GATED ? wave * (NJ / 2) + (j % (NJ / 2)) : wave * NJ + j);
+    };
     uint32_t coff[NJ], scoff[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -953,10 +965,34 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
         return;
     }
 
+    // PAIR: the gate waves' sums to the up waves, element for element (the
+    // same lane layout), through LDS that every wave has finished with.
+    floatx16 gsum[PAIR ? MI : 1][PAIR ? NJ : 1];
+    if constexpr (PAIR) {
+        float* E = reinterpret_cast<float*>(smem);
+        lds_barrier();
+        if (wave < NW / 2) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) E[(((pw * MI + i) * NJ + j) * 16 + e) * WAVE + lane] = acc[i][j][e];
+        }
+        lds_barrier();
+        if (wave < NW / 2) return;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) gsum[i][j][e] = E[(((pw * MI + i) * NJ + j) * 16 + e) * WAVE + lane];
+    }
+
     // Epilogue: lane (lr, lh) holds, for activation row lr of block i,
     // output columns 8 q + 4 lh + 0..3 of weight block j (q = 0..3).
-    constexpr int NO = GATED ? NJ / 2 : NJ;
-    const int64_t nw0 = n0 + (GATED ? wave * (WR / 2) : wave * WR);
+    constexpr int NO = GATED && !PAIR ? NJ / 2 : NJ;
+    const int64_t nw0 = n0 + (PAIR ? pw * WR : GATED ? wave * (WR / 2) : wave * WR);
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
         const int64_t m = m0 + i * 32 + lr;
@@ -969,7 +1005,11 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
                 float v[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    if constexpr (EPI == EPI_GELU_TANH)
+                    if constexpr (PAIR && EPI == EPI_GELU_TANH)
+                        v[r] = gelu_tanh(gsum[i][j][4 * q + r]) * acc[i][j][4 * q + r];
+                    else if constexpr (PAIR)
+                        v[r] = gelu_erf(gsum[i][j][4 * q + r]) * acc[i][j][4 * q + r];
+                    else if constexpr (EPI == EPI_GELU_TANH)
                         v[r] = gelu_tanh(acc[i][j][4 * q + r]) * acc[i][j + NJ / 2][4 * q + r];
                     else if constexpr (EPI == EPI_GELU_ERF)
                         v[r] = gelu_erf(acc[i][j][4 * q + r]) * acc[i][j + NJ / 2][4 * q + r];
@@ -977,9 +1017,11 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
                         v[r] = acc[i][j][4 * q + r];
                 }
                 if (n + 3 < N) {
+                    // f16 from the f32 value in every tile shape (no fused
+                    // multiply-convert in one instance and not another)
                     if constexpr (GATED)
                         *reinterpret_cast<half4*>(static_cast<half_t*>(g.y) + m * g.ldy + n) =
-                            half4{half_t(v[0]), half_t(v[1]), half_t(v[2]), half_t(v[3])};
+                            half4{f16_rounded(v[0]), f16_rounded(v[1]), f16_rounded(v[2]), f16_rounded(v[3])};
                     else
                         *reinterpret_cast<float4*>(static_cast<float*>(g.y) + int64_t(blockIdx.y) * g.part_stride +
                                                    m * g.ldy + n) = make_float4(v[0], v[1], v[2], v[3]);
@@ -988,7 +1030,7 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
                     for (int r = 0; r < 4; ++r) {
                         if (n + r >= N) break;
                         if constexpr (GATED)
-                            static_cast<half_t*>(g.y)[m * g.ldy + n + r] = half_t(v[r]);
+                            static_cast<half_t*>(g.y)[m * g.ldy + n + r] = f16_rounded(v[r]);
                         else
                             static_cast<float*>(g.y)[int64_t(blockIdx.y) * g.part_stride + m * g.ldy + n + r] = v[r];
                     }
@@ -1001,20 +1043,20 @@ __global__ __launch_bounds__(NW_ * WAVE) void gemm32_kernel(GemmArgs g) {
 // above half of it).
 constexpr int XR_MAX_LDS = 96 * 1024;
 
-template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4, bool FOLD = false>
+template <int QUANT, int MI, int NJ, int EPI, int NS, int NW = 4, bool FOLD = false, bool PAIR = false>
 static void run32(hipStream_t s, const GemmArgs& g) {
-    using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW>;
+    using P = Cfg32<QUANT, MI, NJ, EPI, NS, NW, PAIR>;
     for (const DevWeight* w : {&g.w0, &g.w1})
         if (!w->tiles || w->stages != (w->cols + G_BK - 1) / G_BK || (QUANT != F16_DT && !w->tscales))
             fail(E_INVALID, "gemm: weight without stage tiles");
     static bool lds_set = false;
     if (!lds_set) {
         OMG_HIP(hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, false>),
+            reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, false, PAIR>),
             hipFuncAttributeMaxDynamicSharedMemorySize, P::LDS));
         OMG_HIP(hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, true>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, XR_MAX_LDS > P::QK_LDS ? XR_MAX_LDS : P::QK_LDS));
+            reinterpret_cast<const void*>(&gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, true, PAIR>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, XR_MAX_LDS > P::EPI_LDS ? XR_MAX_LDS : P::EPI_LDS));
         lds_set = true;
     }
     const int64_t N = g.w0.rows;
@@ -1024,10 +1066,10 @@ static void run32(hipStream_t s, const GemmArgs& g) {
     const int64_t nk = (g.w0.cols / g.ksplit + G_BK - 1) / G_BK;
     const int64_t xr_lds = nk * P::X_BYTES;
     if (xr_lds <= XR_MAX_LDS) {
-        const int lds = int(xr_lds > P::QK_LDS ? xr_lds : P::QK_LDS);
-        gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, true><<<grid, dim3(P::T), lds, s>>>(g);
+        const int lds = int(xr_lds > P::EPI_LDS ? xr_lds : P::EPI_LDS);
+        gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, true, PAIR><<<grid, dim3(P::T), lds, s>>>(g);
     } else {
-        gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, false><<<grid, dim3(P::T), P::LDS, s>>>(g);
+        gemm32_kernel<QUANT, MI, NJ, EPI, NS, NW, FOLD, false, PAIR><<<grid, dim3(P::T), P::LDS, s>>>(g);
     }
     OMG_HIP(hipGetLastError());
 }
@@ -1112,6 +1154,19 @@ static void dispatch(hipStream_t s, const GemmArgs& g) {
             // for long passes (270M cold pass -0.5%), four for short ones
             // (three: the flushed one-branch passes 1-5% slower); 128-row
             // or 64-column tiles and five slots were 3-10% slower.
+            // Branch-sized passes (M <= 64) pair the waves (a gate and an
+            // up wave per 32 columns: half the decode per wave and stage;
+            // flushed one-branch passes, same box, against 32 x 128 on
+            // four waves of gate and up each: the 270M model's gate/up
+            // 9.2 -> 7.4 us and pass 1.064 -> 1.027 ms, the 4B model's
+            // 23.9 -> 21.4 us and 3.60 -> 3.50 ms).  With X resident (K
+            // <= 1,024) nine slots of weights (four: 7.9 us); through the
+            // ring 64 rows on four waves, four slots (32 rows on two: 21.8
+            // us; five to nine slots 26-29 us).
+            if (M <= 64) {
+                if (K <= 1024) return run32<QUANT, 1, 1, EPI, 9, 2, false, true>(s, g);
+                return run32<QUANT, 2, 1, EPI, 4, 4, false, true>(s, g);
+            }
             if (M <= 512) return run32<QUANT, 1, 2, EPI, 4, 4>(s, g);
             return run32<QUANT, 3, 2, EPI, 3, 4>(s, g);
         }

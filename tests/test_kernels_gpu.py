@@ -58,7 +58,8 @@ def test_gemm_matches_cpu(m, n, k, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m,n,k", [(23, 96, 64), (70, 100, 160), (384, 2048, 640), (2384, 2048, 640),
-                                   (600, 256, 1184), (130, 8192, 96), (600, 8192, 96)])
+                                   (600, 256, 1184), (130, 8192, 96), (600, 8192, 96),
+                                   (1, 96, 640), (40, 100, 1184), (64, 320, 2560)])
 def test_gated_matches_cpu(m, n, k, dtype):
     rng = np.random.default_rng(7 * m * n * k + dtype)
     x = rng.uniform(-1, 1, (m, k)).astype(np.float16)
@@ -100,8 +101,9 @@ def test_gemm_rows_are_independent_of_m():
 def test_gated_rows_are_independent_of_m(k):
     """The gated product's rows are the same bits whichever tile shape the
     launch's M selects (96-row tiles for long passes, 32-row tiles with a
-    deeper ring for short ones): the basis of the bit-equal warm and
-    isolated rows through the feed-forward."""
+    deeper ring for short ones, gate and up on paired waves for branch-sized
+    ones): the basis of the bit-equal warm and isolated rows through the
+    feed-forward."""
     rng = np.random.default_rng(11 + k)
     n = 512
     tg, _ = weight(rng, n, k, g.Q4, "gate")
@@ -109,7 +111,7 @@ def test_gated_rows_are_independent_of_m(k):
     wg, wu = g.DeviceWeight(tg), g.DeviceWeight(tu)
     x = rng.uniform(-1, 1, (2384, k)).astype(np.float16)
     outs = []
-    for m in (2384, 513, 384, 40, 1):
+    for m in (2384, 513, 384, 64, 40, 1):
         act = torch.zeros((m, n), dtype=torch.float16, device="cuda")
         xd = dev(x[:m])  # held until the launch has run
         wg.gemm_geglu(wu, xd.data_ptr(), k, m, act.data_ptr(), n)
