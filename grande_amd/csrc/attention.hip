@@ -183,9 +183,25 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a, const in
                                                      16, o, vtile * 2, 0, 0);
         }
     };
-    // The first tile goes out before the query loads.  Key metadata (one
-    // key per lane) travels in registers one tile ahead; rows past the
-    // cache's valid range read as never visible.
+    // The query fragments go out first, then the first tile, then the
+    // tokens' metadata (whose wait then holds up nothing else).  Block b
+    // holds tokens tok0 + b * TPQ .. (lane: token tok0 + b * TPQ + u_lane);
+    // rows past the pass lie beyond the buffer's range and read as zeros.
+    half8 qf[QB][DS];
+    {
+        const __amdgpu_buffer_rsrc_t qr = attn_rsrc(a.q16, a.t * H * HD * 2);
+#pragma unroll
+        for (int b = 0; b < QB; ++b) {
+            const int64_t tq = tok0 + b * TPQ + u_lane;
+            const int64_t qe = tq < a.t ? (tq * H + head) * HD + G * 8 : a.t * H * HD;  // in halves
+            const uint32_t qo = uint32_t(qe > 0x3fffffff ? 0x3fffffff : qe) * 2;
+#pragma unroll
+            for (int s = 0; s < DS; ++s)
+                qf[b][s] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(qr, qo + s * 64, 0, 0));
+        }
+    }
+    // Key metadata (one key per lane) travels in registers one tile ahead;
+    // rows past the cache's valid range read as never visible.
     int4 km_next = make_int4(0, 0, 0, 0);
     if (tb < te) {
         issue(tb, 0);
@@ -202,16 +218,6 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a, const in
         qseq[u] = __builtin_amdgcn_readfirstlane(m.y);
     }
 
-    // Block b holds tokens tok0 + b * TPQ .. (lane: token tok0 + b * TPQ + u_lane).
-    half8 qf[QB][DS];
-#pragma unroll
-    for (int b = 0; b < QB; ++b) {
-        const int64_t tq = tok0 + b * TPQ + u_lane;
-#pragma unroll
-        for (int s = 0; s < DS; ++s)
-            qf[b][s] = tq < a.t ? *reinterpret_cast<const half8*>(a.q16 + (tq * H + head) * HD + s * 32 + G * 8)
-                                : half8{};
-    }
     floatx4 o[QB][CT];
 #pragma unroll
     for (int b = 0; b < QB; ++b)
@@ -680,6 +686,8 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
     if (16 % hpg) fail(E_INVALID, "attention: query heads per KV head must divide 16");
     if (a.cap_pad % 64 || a.base + a.t > a.cap_pad) fail(E_INVALID, "attention: cache rows out of range");
     if (a.window < 0) fail(E_INVALID, "attention: negative window");
+    // the query rows are read through a buffer resource (32-bit byte offsets)
+    if (a.t * a.heads * a.hd * 2 > 0x7fffffff) fail(E_INVALID, "attention: query rows past 2 GiB");
     if (a.hd == 512) {
         const size_t smem = sizeof(AttnSmem<512>);
         switch (hpg) {
