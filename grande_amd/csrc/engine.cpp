@@ -458,9 +458,17 @@ constexpr int64_t SHORT_ATTN_ROWS = 1024;
 // Rows per sub-pass range, at least (Engine::Sub).  Measured (same box):
 // the 4B model's 16,320-token pass in three ranges 169.9 -> 159.0 ms, its
 // 8,320-row warm pass in two 96.3 -> 91.9 ms; the 270M model's 2,384-token
-// pass in two ranges 0.5% slower, in three 6% slower (its kernels are too
-// short for the overlap to pay).
+// pass in three ranges 6% slower (its kernels are too short for the
+// overlap to pay), in two see MID_ROWS.
 constexpr int64_t SUB_ROWS = 4096;
+// Passes of more rows than this and fewer than 2 * SUB_ROWS run as two
+// ranges, the first MID_CUT percent of the rows (rounded up to a 64-row
+// cache tile).  Measured (same box, the 270M model's 2,384-token cold
+// pass): cuts at 40 / 45 / 50 / 55 / 60 / 75 / 86% gave +1.3 / +2.3 /
+// +2.7 / +3.5 / +2.4 / -2.4 / -4.4% questions/s against one range (an
+// even split measured 0.5% slower before this build's kernel changes).
+constexpr int64_t MID_ROWS = 1024;
+constexpr int64_t MID_CUT = 55;
 // Passes of at most this many rows run deep-K products a piece per
 // workgroup (split_plan).
 constexpr int64_t CHUNKED_ROWS = 512;
@@ -483,7 +491,8 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     // A captured pass reads the work lists and buffers this upload may move.
     drop_graph();
     // Row ranges (Engine::Sub): at least SUB_ROWS rows each, at most
-    // MAX_SUB, cut where a cache row is a multiple of 64 (no V^T tile of the
+    // MAX_SUB (two from MID_ROWS, cut at MID_CUT percent), cut where a
+    // cache row is a multiple of 64 (no V^T tile of the
     // cache holds rows of two ranges), each longer than CHUNKED_ROWS (no
     // range takes the short passes' one-chunk-per-workgroup products, whose
     // partials share one area).  One range while profiling: the kernels'
@@ -504,6 +513,13 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     if (ns == 1) {
         sub_[0].r0 = 0;
         sub_[0].r1 = t;
+        const int64_t r = (pk.base + t * MID_CUT / 100 + 63) / 64 * 64 - pk.base;
+        if (!profile_ && t > MID_ROWS && r > CHUNKED_ROWS && t - r > CHUNKED_ROWS) {
+            sub_[0].r1 = r;
+            sub_[1].r0 = r;
+            sub_[1].r1 = t;
+            ns = 2;
+        }
     }
     nsub_ = ns;
     // Attention work lists per range and layer type.  Short ranges run

@@ -573,10 +573,11 @@ def test_evaluate_cancels_a_prepared_pass():
         assert np.array_equal(a.rows[0], b.rows[0])
 
 
-@pytest.mark.parametrize("prefix_len", [8300, 12400])
+@pytest.mark.parametrize("prefix_len", [2000, 8300, 12400])
 def test_pass_split_over_streams_is_bit_equal(prefix_len):
     """A long pass runs as consecutive row ranges on streams of their own
-    (two ranges from 8,192 rows, three from 12,288), each range's attention
+    (two ranges from 1,025 rows, cut at 55%; two equal ones from 8,192
+    rows, three from 12,288), each range's attention
     waiting for the earlier ranges' K/V of the same layer.  Its rows are bit
     for bit those of the same pass as one range (profiling runs passes as
     one range), of the branches over the resident prefix, and of a captured
