@@ -437,7 +437,10 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a, const in
                 half4{half_t(o[b][c][0] * inv), half_t(o[b][c][1] * inv), half_t(o[b][c][2] * inv),
                       half_t(o[b][c][3] * inv)};
         const int row0 = (wave * QB + b) * 16;  // the block's first row of the item
-        const int64_t prow0 = (int64_t(slot) * a.kv_heads + g) * ROWS + row0;
+        // A slot holds A_ROWS rows per KV head whatever the item's width:
+        // row ranges of one pass that run at once on their own streams take
+        // disjoint slot numbers, and items of 2 and 4 waves may meet there.
+        const int64_t prow0 = (int64_t(slot) * a.kv_heads + g) * A_ROWS + row0;
         if (slot >= 0 && G == 0 && ch == 0) {
             // the chunk's max and sum
             a.part_ml[(prow0 + lr) * 2] = m_run[b];
@@ -486,7 +489,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, const 
     const int64_t tq = int64_t(qtile) * tpb + (row / 16) * tpq + (row % 16) / hpg;
     if (tq >= a.t) return;
     const int head = g * hpg + (row % 16) % hpg;
-    auto base = [&](int c) { return (int64_t(slot0 + c) * a.kv_heads + g) * ROWS + row; };
+    auto base = [&](int c) { return (int64_t(slot0 + c) * a.kv_heads + g) * A_ROWS + row; };  // slot stride A_ROWS
     // Running merge over rounds of MAXC chunks (one round for n <= MAXC):
     // (M, L, acc) rescaled when a later round raises the max.
     float M = -INFINITY, L = 0.0f;

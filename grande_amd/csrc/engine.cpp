@@ -746,11 +746,18 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     const hipStream_t s = sub_stream_[k];
     Layer& L = layers_[size_t(l)];
     const int64_t hd = c.head_dim[size_t(l)], qw = c.qkv_width(l), ff = c.ff[size_t(l)];
+    // Range k's part of a per-row buffer starts at r0 rows of the buffer's
+    // widest layer: widths vary by layer (Gemma 4: head_dim 256 / 512, the
+    // double-wide MLP), and ranges run different layers at once, so
+    // offsets of r0 rows of this layer's width would overlap a range still
+    // on a narrower or wider layer.  Within the range rows are contiguous
+    // at this layer's width.
+    const int64_t qw_row = c.max_qkv(), hd_row = c.max_head_dim(), ff_row = c.max_ff();
     const int64_t src = c.kv_source[size_t(l)];
     half_t* hn = hn_.as<half_t>() + r0 * d;
     float* x = x_.as<float>() + r0 * d;
     QkArgs q{};
-    q.qkv = qkv_.as<float>() + r0 * qw;
+    q.qkv = qkv_.as<float>() + r0 * qw_row;
     q.qkv_stride = qw;
     q.meta = meta_.as<int32_t>();
     q.q_norm = L.q_norm.as<float>();
@@ -768,14 +775,14 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     q.t = t;
     q.base = base;
     q.cap_pad = cap_pad_;
-    q.q16 = q16_.as<half_t>() + r0 * c.heads * hd;
+    q.q16 = q16_.as<half_t>() + r0 * c.heads * hd_row;
     q.kc = kc_[size_t(src)].as<half_t>();
     q.vt = vt_[size_t(src)].as<half_t>();
     if (hd == 256) {
         // qk_prep's norms, RoPE and cache writes in the product's epilogue
         step("mm_qkv", k, [&] { launch_gemm_qkprep(s, hn, d, L.qkv.w, q, t); });
     } else {
-        step("mm_qkv", k, [&] { launch_gemm(s, hn, d, L.qkv.w, qkv_.as<float>() + r0 * qw, qw, t); });
+        step("mm_qkv", k, [&] { launch_gemm(s, hn, d, L.qkv.w, qkv_.as<float>() + r0 * qw_row, qw, t); });
         step("qk_prep", k, [&] { launch_qk_prep(s, q); });
     }
     if (nsub_ > 1) {
@@ -789,7 +796,7 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     att.kc = q.kc;
     att.vt = q.vt;
     att.meta = meta_.as<int32_t>();
-    att.out = attn_.as<half_t>() + r0 * c.heads * hd;
+    att.out = attn_.as<half_t>() + r0 * c.heads * hd_row;
     att.t = t;
     att.base = base;
     att.cap_pad = cap_pad_;
@@ -811,7 +818,7 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
         launch_residual_norm(s, no.a, L.post_attn_norm.as<float>(), x, L.ffn_norm.as<float>(), hn, t, d, c.eps, 1.0f,
                              no.parts, no.stride, no.group);
     });
-    half_t* act = act_.as<half_t>() + r0 * ff;
+    half_t* act = act_.as<half_t>() + r0 * ff_row;
     step("mm_gate_up", k, [&] { launch_gemm_geglu(s, hn, d, L.gate.w, L.up.w, act, ff, t); });
     split_product("mm_down", k, act, ff, L.down.w, r0, t, pd);
     // The last layer's stream is normed at the wanted rows only (readout).

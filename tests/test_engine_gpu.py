@@ -10,8 +10,8 @@ import grande_amd as g
 import oracle
 from grande_amd import _lib as L
 from grande_amd import BranchTokens, Group, PrefixSource, Want
-from tests.common import (assert_close, build, gemma3_tiny, gguf_tiny, oracle_rows, rel_diff, tiled_oracle,
-                          worst_rel)
+from tests.common import (assert_close, build, gemma3_tiny, gemma4_tiny, gguf_tiny, oracle_rows, rel_diff,
+                          tiled_oracle, worst_rel)
 
 pytestmark = pytest.mark.gpu
 
@@ -573,16 +573,24 @@ def test_evaluate_cancels_a_prepared_pass():
         assert np.array_equal(a.rows[0], b.rows[0])
 
 
-@pytest.mark.parametrize("prefix_len", [2000, 8300, 12400])
-def test_pass_split_over_streams_is_bit_equal(prefix_len):
+@pytest.mark.parametrize("model,prefix_len,heads,kv", [("gemma3", 2000, 4, 1), ("gemma3", 2000, 8, 2),
+                                                       ("gemma4", 2000, 4, 1), ("gemma3", 8300, 8, 2),
+                                                       ("gemma3", 12400, 8, 2)])
+def test_pass_split_over_streams_is_bit_equal(model, prefix_len, heads, kv):
     """A long pass runs as consecutive row ranges on streams of their own
     (two ranges from 1,025 rows, cut at 55%; two equal ones from 8,192
     rows, three from 12,288), each range's attention
     waiting for the earlier ranges' K/V of the same layer.  Its rows are bit
     for bit those of the same pass as one range (profiling runs passes as
     one range), of the branches over the resident prefix, and of a captured
-    graph of the split pass replayed several times."""
-    cfg = gguf_tiny(8, 2, window=37, vocab=64)
+    graph of the split pass replayed several times.  At 2,000 tokens with
+    one KV head the second range (under 1,024 rows) runs 2-wave attention
+    items on the sliding layers while the first runs 4-wave ones, at the
+    same time: their chunk partials must not share memory.  The Gemma 4
+    model's layers differ in width (head_dim 256 / 512, double-wide MLP),
+    and a range runs one layer while the other runs the next: their rows in
+    the per-row buffers must not meet either."""
+    cfg = (gguf_tiny if model == "gemma3" else gemma4_tiny)(heads, kv, window=37, vocab=64)
     eng, _, _, _ = build(cfg, 47, g.Q4, g.Q8, capacity=prefix_len + 256, oracle_models=False)
     rng = np.random.default_rng(prefix_len)
     prefix = rng.integers(0, 64, prefix_len).tolist()
