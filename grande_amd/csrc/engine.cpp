@@ -461,14 +461,20 @@ constexpr int64_t SHORT_ATTN_ROWS = 1024;
 // pass in three ranges 6% slower (its kernels are too short for the
 // overlap to pay), in two see MID_ROWS.
 constexpr int64_t SUB_ROWS = 4096;
-// Passes of more rows than this and fewer than 2 * SUB_ROWS run as two
-// ranges, the first MID_CUT percent of the rows (rounded up to a 64-row
-// cache tile).  Measured (same box, the 270M model's 2,384-token cold
-// pass): cuts at 40 / 45 / 50 / 55 / 60 / 75 / 86% gave +1.3 / +2.3 /
-// +2.7 / +3.5 / +2.4 / -2.4 / -4.4% questions/s against one range (an
-// even split measured 0.5% slower before this build's kernel changes).
+// Passes of more rows than this and fewer than 2 * SUB_ROWS run as ranges
+// too: two, the first 55% of the rows (each cut rounded up to a 64-row
+// cache tile), and three, cut at 40% and 72%, for models at least
+// WIDE_D wide.  Measured (same box): the 270M model's 2,384-token cold
+// pass with two ranges cut at 40 / 45 / 50 / 55 / 60 / 75 / 86% gave
+// +1.3 / +2.3 / +2.7 / +3.5 / +2.4 / -2.4 / -4.4% questions/s against one
+// range (an even split measured 0.5% slower before this build's kernel
+// changes), three at 40 / 72% 6.6% below two; two at 55% took the 1B
+// model's 2,384-token pass 5.78 -> 5.45 ms and E2B's 2,663-token pass
+// 17.17 -> 15.96 ms, three at 40 / 72% another -1.2% and -3.7%.  Three
+// ranges of the 4B model's 16,320-token pass cut at 40 / 72% rather than
+// evenly: 150.1 -> 149.4 ms.
 constexpr int64_t MID_ROWS = 1024;
-constexpr int64_t MID_CUT = 55;
+constexpr int64_t WIDE_D = 1024;
 // Passes of at most this many rows run deep-K products a piece per
 // workgroup (split_plan).
 constexpr int64_t CHUNKED_ROWS = 512;
@@ -490,20 +496,31 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     if (resident_ && int64_t(resident_->size()) > pk.base) resident_.reset();
     // A captured pass reads the work lists and buffers this upload may move.
     drop_graph();
-    // Row ranges (Engine::Sub): at least SUB_ROWS rows each, at most
-    // MAX_SUB (two from MID_ROWS, cut at MID_CUT percent), cut where a
+    // Row ranges (Engine::Sub): one per SUB_ROWS rows, at most MAX_SUB
+    // (from MID_ROWS rows two or three, see there), cut where a
     // cache row is a multiple of 64 (no V^T tile of the
     // cache holds rows of two ranges), each longer than CHUNKED_ROWS (no
     // range takes the short passes' one-chunk-per-workgroup products, whose
     // partials share one area).  One range while profiling: the kernels'
     // times are then those of the pass's launches alone.
-    int ns = profile_ ? 1 : int(std::min<int64_t>(MAX_SUB, std::max<int64_t>(1, t / SUB_ROWS)));
+    int ns = 1;
+    if (!profile_) {
+        if (t >= 2 * SUB_ROWS)
+            ns = int(std::min<int64_t>(MAX_SUB, t / SUB_ROWS));
+        else if (t > MID_ROWS)
+            ns = cfg_.d >= WIDE_D ? 3 : 2;
+    }
+    // First row of range k of n (pass-relative), k = 1 .. n - 1.
+    auto cut = [&](int k, int n) -> int64_t {
+        const int64_t pct = n == 3 ? (k == 1 ? 40 : 72) : (t >= 2 * SUB_ROWS ? 50 : 55);
+        return (pk.base + t * pct / 100 + 63) / 64 * 64 - pk.base;
+    };
     for (; ns > 1; --ns) {
         bool ok = true;
         int64_t prev = 0;
         for (int k = 1; k <= ns; ++k) {
-            const int64_t r = k == ns ? t : ((pk.base + k * t / ns + 63) / 64 * 64 - pk.base);
-            ok = ok && r - prev > CHUNKED_ROWS && (k == ns || (pk.base + r) % 64 == 0);
+            const int64_t r = k == ns ? t : cut(k, ns);
+            ok = ok && r - prev > CHUNKED_ROWS;
             sub_[k - 1].r0 = prev;
             sub_[k - 1].r1 = r;
             prev = r;
@@ -513,13 +530,6 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     if (ns == 1) {
         sub_[0].r0 = 0;
         sub_[0].r1 = t;
-        const int64_t r = (pk.base + t * MID_CUT / 100 + 63) / 64 * 64 - pk.base;
-        if (!profile_ && t > MID_ROWS && r > CHUNKED_ROWS && t - r > CHUNKED_ROWS) {
-            sub_[0].r1 = r;
-            sub_[1].r0 = r;
-            sub_[1].r1 = t;
-            ns = 2;
-        }
     }
     nsub_ = ns;
     // Attention work lists per range and layer type.  Short ranges run

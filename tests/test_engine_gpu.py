@@ -574,12 +574,13 @@ def test_evaluate_cancels_a_prepared_pass():
 
 
 @pytest.mark.parametrize("model,prefix_len,heads,kv", [("gemma3", 2000, 4, 1), ("gemma3", 2000, 8, 2),
-                                                       ("gemma4", 2000, 4, 1), ("gemma3", 8300, 8, 2),
-                                                       ("gemma3", 12400, 8, 2)])
+                                                       ("gemma3-wide", 2000, 4, 1), ("gemma4", 2000, 4, 1),
+                                                       ("gemma3", 8300, 8, 2), ("gemma3", 12400, 8, 2)])
 def test_pass_split_over_streams_is_bit_equal(model, prefix_len, heads, kv):
     """A long pass runs as consecutive row ranges on streams of their own
-    (two ranges from 1,025 rows, cut at 55%; two equal ones from 8,192
-    rows, three from 12,288), each range's attention
+    (from 1,025 rows two ranges cut at 55%, three cut at 40% and 72% for
+    models 1,024 wide; two equal ones from 8,192 rows, three cut at 40% and
+    72% from 12,288), each range's attention
     waiting for the earlier ranges' K/V of the same layer.  Its rows are bit
     for bit those of the same pass as one range (profiling runs passes as
     one range), of the branches over the resident prefix, and of a captured
@@ -590,7 +591,10 @@ def test_pass_split_over_streams_is_bit_equal(model, prefix_len, heads, kv):
     model's layers differ in width (head_dim 256 / 512, double-wide MLP),
     and a range runs one layer while the other runs the next: their rows in
     the per-row buffers must not meet either."""
-    cfg = (gguf_tiny if model == "gemma3" else gemma4_tiny)(heads, kv, window=37, vocab=64)
+    if model == "gemma4":
+        cfg = gemma4_tiny(heads, kv, window=37, vocab=64)
+    else:
+        cfg = gguf_tiny(heads, kv, window=37, vocab=64, **({"d": 1024} if model == "gemma3-wide" else {}))
     eng, _, _, _ = build(cfg, 47, g.Q4, g.Q8, capacity=prefix_len + 256, oracle_models=False)
     rng = np.random.default_rng(prefix_len)
     prefix = rng.integers(0, 64, prefix_len).tolist()
