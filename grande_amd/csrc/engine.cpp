@@ -455,16 +455,13 @@ Packed Engine::pack_checked(const GroupIn* groups, int64_t n, int64_t first, boo
 
 // Passes of at most this many tokens run 2-wave attention items.
 constexpr int64_t SHORT_ATTN_ROWS = 1024;
-// Rows per sub-pass range, at least (Engine::Sub).  Measured (same box):
-// the 4B model's 16,320-token pass in three ranges 169.9 -> 159.0 ms, its
-// 8,320-row warm pass in two 96.3 -> 91.9 ms; the 270M model's 2,384-token
-// pass in three ranges 6% slower (its kernels are too short for the
-// overlap to pay), in two see MID_ROWS.
-constexpr int64_t SUB_ROWS = 4096;
-// Passes of more rows than this and fewer than 2 * SUB_ROWS run as ranges
-// too: two, the first 55% of the rows (each cut rounded up to a 64-row
-// cache tile), and three, cut at 40% and 72%, for models at least
-// WIDE_D wide.  Measured (same box): the 270M model's 2,384-token cold
+// Row ranges (Engine::Sub): passes of more than MID_ROWS rows run as two
+// ranges, the first 55% of the rows (each cut rounded up to a 64-row cache
+// tile), or as three cut at 40% and 72% when the model is at least WIDE_D
+// wide or the pass at least 3 * SUB_ROWS rows.  Measured (same box): the
+// 4B model's 16,320-token pass in three even ranges 169.9 -> 159.0 ms (an
+// earlier build), its 8,320-row warm pass in two even ones 96.3 -> 91.9
+// ms, in three at 40 / 72% another 87.1 -> 85.3 ms; the 270M model's 2,384-token cold
 // pass with two ranges cut at 40 / 45 / 50 / 55 / 60 / 75 / 86% gave
 // +1.3 / +2.3 / +2.7 / +3.5 / +2.4 / -2.4 / -4.4% questions/s against one
 // range (an even split measured 0.5% slower before this build's kernel
@@ -475,6 +472,7 @@ constexpr int64_t SUB_ROWS = 4096;
 // evenly: 150.1 -> 149.4 ms.
 constexpr int64_t MID_ROWS = 1024;
 constexpr int64_t WIDE_D = 1024;
+constexpr int64_t SUB_ROWS = 4096;
 // Passes of at most this many rows run deep-K products a piece per
 // workgroup (split_plan).
 constexpr int64_t CHUNKED_ROWS = 512;
@@ -496,23 +494,19 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     if (resident_ && int64_t(resident_->size()) > pk.base) resident_.reset();
     // A captured pass reads the work lists and buffers this upload may move.
     drop_graph();
-    // Row ranges (Engine::Sub): one per SUB_ROWS rows, at most MAX_SUB
-    // (from MID_ROWS rows two or three, see there), cut where a
+    // Row ranges (Engine::Sub): from MID_ROWS rows two or three (see
+    // there), cut where a
     // cache row is a multiple of 64 (no V^T tile of the
     // cache holds rows of two ranges), each longer than CHUNKED_ROWS (no
     // range takes the short passes' one-chunk-per-workgroup products, whose
     // partials share one area).  One range while profiling: the kernels'
     // times are then those of the pass's launches alone.
+    static_assert(MAX_SUB == 3, "three ranges at most");
     int ns = 1;
-    if (!profile_) {
-        if (t >= 2 * SUB_ROWS)
-            ns = int(std::min<int64_t>(MAX_SUB, t / SUB_ROWS));
-        else if (t > MID_ROWS)
-            ns = cfg_.d >= WIDE_D ? 3 : 2;
-    }
+    if (!profile_ && t > MID_ROWS) ns = cfg_.d >= WIDE_D || t >= 3 * SUB_ROWS ? 3 : 2;
     // First row of range k of n (pass-relative), k = 1 .. n - 1.
     auto cut = [&](int k, int n) -> int64_t {
-        const int64_t pct = n == 3 ? (k == 1 ? 40 : 72) : (t >= 2 * SUB_ROWS ? 50 : 55);
+        const int64_t pct = n == 3 ? (k == 1 ? 40 : 72) : 55;
         return (pk.base + t * pct / 100 + 63) / 64 * 64 - pk.base;
     };
     for (; ns > 1; --ns) {

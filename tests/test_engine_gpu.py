@@ -578,9 +578,9 @@ def test_evaluate_cancels_a_prepared_pass():
                                                        ("gemma3", 8300, 8, 2), ("gemma3", 12400, 8, 2)])
 def test_pass_split_over_streams_is_bit_equal(model, prefix_len, heads, kv):
     """A long pass runs as consecutive row ranges on streams of their own
-    (from 1,025 rows two ranges cut at 55%, three cut at 40% and 72% for
-    models 1,024 wide; two equal ones from 8,192 rows, three cut at 40% and
-    72% from 12,288), each range's attention
+    (from 1,025 rows two ranges cut at 55%, or three cut at 40% and 72%
+    for models 1,024 wide and for passes from 12,288 rows), each range's
+    attention
     waiting for the earlier ranges' K/V of the same layer.  Its rows are bit
     for bit those of the same pass as one range (profiling runs passes as
     one range), of the branches over the resident prefix, and of a captured
