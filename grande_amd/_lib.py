@@ -110,6 +110,7 @@ _SIGS = {
     "omg_pass_read": (C.c_int, [_P, _P, C.c_size_t, C.POINTER(C.c_size_t)]),
     "omg_sync": (C.c_int, [_P]),
     "omg_profile": (C.c_int, [_P, C.c_int]),
+    "omg_set_full_last_layer": (C.c_int, [_P, C.c_int]),
     "omg_profile_report": (C.c_size_t, [_P, C.c_char_p, C.c_size_t]),
     "omg_weight_upload": (_P, [C.c_int, C.c_int64, C.c_int64, _P, _P]),
     "omg_weight_free": (None, [_P]),

@@ -423,6 +423,10 @@ int omg_profile(omg_engine* e, int on) {
     return guard([&] { eng(e).set_profile(on != 0); });
 }
 
+int omg_set_full_last_layer(omg_engine* e, int on) {
+    return guard([&] { eng(e).set_full_last_layer(on != 0); });
+}
+
 size_t omg_profile_report(omg_engine* e, char* buf, size_t len) {
     if (!e || !e->e) return 0;
     const std::string s = e->e->profile_report();

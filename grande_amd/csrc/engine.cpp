@@ -256,6 +256,20 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.a_ = DevBuf(size_t(cap * d) * 4 * OMG_KSPLIT);
     E.act_ = DevBuf(size_t(cap * c.max_ff()) * 2);
     E.rows_ = DevBuf(size_t(max_rows * d) * 4);
+    // the last layer on the answer rows (layer_out)
+    E.attn_w_ = DevBuf(size_t(max_rows * c.heads * hd) * 2);
+    E.x_w_ = DevBuf(size_t(max_rows * d) * 4);
+    E.hn_w_ = DevBuf(size_t(max_rows * d) * 2);
+    E.act_w_ = DevBuf(size_t(max_rows * c.max_ff()) * 2);
+    {
+        int most = OMG_KSPLIT;  // the most parts of an o / down product (K splits x pieces)
+        for (int64_t l = 0; l < c.layers; ++l)
+            for (const int64_t kd : {c.heads * c.head_dim[size_t(l)], c.ff[size_t(l)]}) {
+                const Engine::SplitPlan p = E.split_plan(kd, d, 1);
+                most = std::max(most, p.splits * p.group);
+            }
+        E.a_w_ = DevBuf(size_t(max_rows * d) * 4 * size_t(most));
+    }
     const int64_t width = std::max(c.vocab, d);
     E.logits_ = DevBuf(size_t(max_rows * width) * 4);
     E.label_lse_ = DevBuf(size_t(max_rows * (c.vocab + 1)) * 4);
@@ -395,6 +409,11 @@ void Engine::set_profile(bool on) {
     sync();
     profile_ = on;
     totals_.clear();
+}
+
+void Engine::set_full_last_layer(bool on) {
+    sync();
+    full_last_layer_ = on;
 }
 
 std::string Engine::profile_report() const {
@@ -554,6 +573,36 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         }
         slots += most;
     }
+    // The last layer on the answer rows only (layer_out): models without
+    // the per-layer-input block, wanted rows in ascending order (each
+    // range's share is one run of the list).  Its attention runs the items
+    // of the query tiles that hold those rows, the same items a full pass
+    // runs for them.
+    bool asc = true;
+    for (int64_t r = 1; r < nr; ++r) asc = asc && pk.wanted[size_t(r)][3] >= pk.wanted[size_t(r - 1)][3];
+    out_rows_ = !full_last_layer_ && cfg_.per_layer_dim == 0 && nr > 0 && asc;
+    if (out_rows_) {
+        const int64_t last = cfg_.layers - 1;
+        const int kind = (cfg_.sliding[size_t(last)] && cfg_.window > 0) ? 0 : 1;
+        int64_t i = 0;
+        for (int k = 0; k < ns; ++k) {
+            Sub& sb = sub_[k];
+            sb.w0 = i;
+            while (i < nr && pk.wanted[size_t(i)][3] < sb.r1) ++i;
+            sb.w1 = i;
+            const AttnWork& w = sb.work[kind];
+            const int64_t tpb = int64_t(w.nw) * 16 / (cfg_.heads / cfg_.kv_heads);
+            std::vector<char> tile(size_t((sb.r1 - sb.r0 + tpb - 1) / tpb), 0);
+            for (int64_t j = sb.w0; j < sb.w1; ++j) tile[size_t((pk.wanted[size_t(j)][3] - sb.r0) / tpb)] = 1;
+            sb.out_work.items.clear();
+            sb.out_work.merges.clear();
+            sb.out_work.nw = w.nw;
+            for (const int4& it : w.items)
+                if (it.x >= 0 && tile[size_t(it.x)]) sb.out_work.items.push_back(it);
+            for (const int4& m : w.merges)
+                if (tile[size_t(m.x)]) sb.out_work.merges.push_back(m);
+        }
+    }
     // The pass's inputs go to the device in two copies: the cache metadata
     // of its rows, and one block [ids | wanted rows | labels | per range and
     // layer type: work items, merges] (16-byte aligned parts).
@@ -565,12 +614,15 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         return o;
     };
     const size_t o_ids = part(size_t(t) * 4), o_wanted = part(size_t(nr) * 4), o_labels = part(size_t(nlabels) * 4);
-    size_t o_items[MAX_SUB][2], o_merges[MAX_SUB][2];
-    for (int k = 0; k < ns; ++k)
+    size_t o_items[MAX_SUB][2], o_merges[MAX_SUB][2], o_out_items[MAX_SUB], o_out_merges[MAX_SUB];
+    for (int k = 0; k < ns; ++k) {
         for (int kind = 0; kind < 2; ++kind) {
             o_items[k][kind] = part(sub_[k].work[kind].items.size() * 16);
             o_merges[k][kind] = part(sub_[k].work[kind].merges.size() * 16);
         }
+        o_out_items[k] = part(out_rows_ ? sub_[k].out_work.items.size() * 16 : 0);
+        o_out_merges[k] = part(out_rows_ ? sub_[k].out_work.merges.size() * 16 : 0);
+    }
     const size_t meta_bytes = a16(size_t(t) * 16);
     // The previous pass may still read the staging buffer; from here the
     // stream is idle (its ranges' streams joined it), so buffers can grow.
@@ -605,6 +657,12 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
             if (!wk.items.empty()) std::memcpy(hb + o_items[k][kind], wk.items.data(), wk.items.size() * 16);
             if (!wk.merges.empty()) std::memcpy(hb + o_merges[k][kind], wk.merges.data(), wk.merges.size() * 16);
         }
+    if (out_rows_)
+        for (int k = 0; k < ns; ++k) {
+            const AttnWork& wk = sub_[k].out_work;
+            if (!wk.items.empty()) std::memcpy(hb + o_out_items[k], wk.items.data(), wk.items.size() * 16);
+            if (!wk.merges.empty()) std::memcpy(hb + o_out_merges[k], wk.merges.data(), wk.merges.size() * 16);
+        }
     OMG_HIP(hipMemcpyAsync(meta_.as<uint8_t>() + pk.base * 16, h, size_t(t) * 16, hipMemcpyHostToDevice, stream_));
     OMG_HIP(hipMemcpyAsync(in_.p, hb, in_bytes, hipMemcpyHostToDevice, stream_));
     uint8_t* d = in_.as<uint8_t>();
@@ -619,6 +677,10 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
             sb.n_items[kind] = int64_t(sb.work[kind].items.size());
             sb.n_merges[kind] = int64_t(sb.work[kind].merges.size());
         }
+    for (int k = 0; k < ns; ++k) {
+        sub_[k].d_out_items = reinterpret_cast<const int4*>(d + o_out_items[k]);
+        sub_[k].d_out_merges = reinterpret_cast<const int4*>(d + o_out_merges[k]);
+    }
 }
 
 // K splits of the o / down products (output width n <= 2048): their tiles
@@ -812,6 +874,15 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     att.part_ml = part_ml_.as<float>();
     const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
     const int nw = sb.work[kind].nw;
+    if (out_rows_ && l + 1 == c.layers) {
+        // The last layer: attention for the query tiles of the answer rows,
+        // then the rest on those rows alone.
+        const int64_t ni = int64_t(sb.out_work.items.size()), nm = int64_t(sb.out_work.merges.size());
+        if (ni > 0) step("attention_out", k, [&] { launch_attention(s, att, sb.d_out_items, ni, nw); });
+        if (nm > 0) step("attention_merge_out", k, [&] { launch_attention_merge(s, att, sb.d_out_merges, nm, nw); });
+        layer_out(k, att.out, x, r0);
+        return;
+    }
     step("attention", k, [&] { launch_attention(s, att, sb.d_items[kind], sb.n_items[kind], nw); });
     if (sb.n_merges[kind] > 0)
         step("attention_merge", k, [&] { launch_attention_merge(s, att, sb.d_merges[kind], sb.n_merges[kind], nw); });
@@ -854,12 +925,58 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     });
 }
 
+// Range k's answer rows [w0, w1) through the last layer past its
+// attention: gathered (attention output f16, stream f32) into rows w0.. of
+// the answer-row buffers, then o, the residual norms, gate/up and down on
+// those rows only.  The products' K splits are the full pass's (a function
+// of the shape); deep K pieces add in the GEMM's registers, the sums a
+// piece-per-workgroup pass gives as well.  Every step is per row and does
+// not depend on the other rows of its launch, so the rows are those of the
+// full last layer.
+void Engine::layer_out(int k, const half_t* attn, const float* x, int64_t r0) {
+    const Config& c = cfg_;
+    const Sub& sb = sub_[k];
+    const int64_t n = sb.w1 - sb.w0;
+    if (n == 0) return;
+    const int64_t l = c.layers - 1, d = c.d;
+    const Layer& L = layers_[size_t(l)];
+    const int64_t W = c.heads * c.head_dim[size_t(l)], ff = c.ff[size_t(l)];
+    const hipStream_t s = sub_stream_[k];
+    half_t* aw = attn_w_.as<half_t>() + sb.w0 * W;
+    float* xw = x_w_.as<float>() + sb.w0 * d;
+    half_t* hw = hn_w_.as<half_t>() + sb.w0 * d;
+    half_t* actw = act_w_.as<half_t>() + sb.w0 * ff;
+    float* pw = a_w_.as<float>() + sb.w0 * d;
+    const int64_t stride = max_rows_ * d;
+    step("gather_out", k, [&] { launch_gather_out(s, attn, W, x, d, d_wanted_ + sb.w0, r0, n, aw, xw); });
+    // A deep product's K pieces run a workgroup each (the rows are few),
+    // their parts [splits x group][max_rows][d] in a_w_.
+    auto product = [&](const char* name, const half_t* in, int64_t kd, const DevWeight& w) {
+        const SplitPlan p = split_plan(kd, d, n);
+        const int parts = p.splits * p.group;
+        step(name, k, [&] { launch_gemm_splitk(s, in, kd, w, pw, d, n, parts, stride); });
+        return NormParts{pw, parts, stride, p.group};
+    };
+    const NormParts no = product("mm_o_out", aw, W, L.o.w);
+    step("norm_out", k, [&] {
+        launch_residual_norm(s, no.a, L.post_attn_norm.as<float>(), xw, L.ffn_norm.as<float>(), hw, n, d, c.eps,
+                             1.0f, no.parts, no.stride, no.group);
+    });
+    step("mm_gate_up_out", k, [&] { launch_gemm_geglu(s, hw, d, L.gate.w, L.up.w, actw, ff, n); });
+    const NormParts nd = product("mm_down_out", actw, ff, L.down.w);
+    step("norm_out", k, [&] {
+        launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), xw, nullptr, nullptr, n, d, c.eps, 1.0f, nd.parts,
+                             nd.stride, nd.group);
+    });
+}
+
 void Engine::readout(const PassPlan& p) {
     if (p.nrows == 0) return;
     const Config& c = cfg_;
+    // (after layer_out the answer rows' stream is x_w_, in wanted order)
     step("final_rows", 0, [&] {
-        launch_final_rows(stream_, x_.as<float>(), d_wanted_, p.nrows, c.d, final_norm_.as<float>(),
-                          c.eps, rows_.as<float>());
+        launch_final_rows(stream_, out_rows_ ? x_w_.as<float>() : x_.as<float>(), out_rows_ ? nullptr : d_wanted_,
+                          p.nrows, c.d, final_norm_.as<float>(), c.eps, rows_.as<float>());
     });
     if (p.want == WANT_LOGITS) {
         step("logits", 0, [&] {

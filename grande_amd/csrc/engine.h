@@ -135,6 +135,11 @@ class Engine {
     void sync();
     void set_profile(bool on);
     std::string profile_report() const;
+    // The last layer past its attention for every row of the pass (on) or,
+    // the default, for the rows a request reads out only (their tiles'
+    // attention, then o, norms, gate/up and down on the gathered rows): the
+    // same rows either way.  Takes effect from the next pass.
+    void set_full_last_layer(bool on);
     hipStream_t stream() const { return stream_; }
 
    private:
@@ -240,6 +245,13 @@ class Engine {
         const int4* d_items[2] = {nullptr, nullptr};
         const int4* d_merges[2] = {nullptr, nullptr};
         int64_t n_items[2] = {0, 0}, n_merges[2] = {0, 0};
+        // The last layer on the answer rows only (out_rows_): the range's
+        // share [w0, w1) of the pass's wanted rows and its attention work
+        // restricted to the query tiles that hold them.
+        int64_t w0 = 0, w1 = 0;
+        AttnWork out_work;
+        const int4* d_out_items = nullptr;
+        const int4* d_out_merges = nullptr;
     };
     Sub sub_[MAX_SUB];
     int nsub_ = 1;
@@ -247,6 +259,14 @@ class Engine {
     hipEvent_t ev_fork_ = nullptr, ev_join_[MAX_SUB] = {};
     std::vector<hipEvent_t> ev_kv_;  // [range][layer]: the range's K/V rows of the layer are in the cache
     void layer(int64_t l, int k, int64_t base);
+    // The last layer past its attention on the gathered answer rows
+    // (range k's wanted rows [w0, w1)).
+    void layer_out(int k, const half_t* attn, const float* x, int64_t r0);
+    bool full_last_layer_ = false;  // set_full_last_layer
+    bool out_rows_ = false;         // this pass runs the last layer on its answer rows
+    // [max_rows] rows: attention output, stream, normed stream, gated
+    // activations, product parts (OMG_KSPLIT of them)
+    DevBuf attn_w_, x_w_, hn_w_, act_w_, a_w_;
     std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
     // pinned host staging
     void* h_in_ = nullptr;

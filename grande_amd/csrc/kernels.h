@@ -104,8 +104,13 @@ void launch_gemm_qkprep(hipStream_t s, const half_t* x, int64_t ldx, const DevWe
 // out[p][i] = (cos, sin)(float(p) * inv_freq[i]) for p < rows, i < half.
 void launch_rope_table(hipStream_t s, const float* inv_freq, int64_t rows, int64_t half, float2* out);
 // rows[i] = rmsnorm(x[wanted[i]]) * w, f32.
+// rows[i] = final norm of x row wanted[i] (row i without a list).
 void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int64_t n, int64_t d,
                        const float* w, float eps, float* rows);
+// aw[i] = a[rows[i] - r0] (f16, width wa), xw[i] = x[rows[i] - r0] (f32,
+// width wx), i < n.
+void launch_gather_out(hipStream_t s, const half_t* a, int64_t wa, const float* x, int64_t wx, const int32_t* rows,
+                       int64_t r0, int64_t n, half_t* aw, float* xw);
 // out[r][j] = rows[r] . deq(E[col(j)]) in f32 (+ softcap), col(j) = cols ? cols[j] : j.
 // logits[r][j] = rows[r] . deq(E[cols ? cols[j] : j]) (softcap applied),
 // f32 [nrows][ncols]; with `part` (logits_blocks(ncols) x nrows pairs) each

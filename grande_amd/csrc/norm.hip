@@ -569,7 +569,7 @@ __global__ __launch_bounds__(256) void final_rows_kernel(const float* __restrict
     const int wave = int(threadIdx.x) / WAVE, lane = int(threadIdx.x) % WAVE;
     const int64_t i = int64_t(blockIdx.x) * 4 + wave;
     if (i >= n) return;
-    const float* xr = x + int64_t(wanted[i]) * d;
+    const float* xr = x + (wanted ? int64_t(wanted[i]) : i) * d;  // no list: row i
     float ss = 0.0f;
     for (int64_t q = lane; q < d / 4; q += WAVE) {
         const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
@@ -588,6 +588,30 @@ void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int
                        const float* w, float eps, float* rows) {
     if (n <= 0) return;
     final_rows_kernel<<<dim3(unsigned((n + 3) / 4)), dim3(256), 0, s>>>(x, wanted, n, d, w, eps, rows);
+    OMG_HIP(hipGetLastError());
+}
+
+// Rows rows[i] - r0 (i < n) of an f16 matrix of width wa and an f32 matrix
+// of width wx, copied to rows i of aw and xw: one workgroup per row, 16
+// bytes per thread and step.
+__global__ __launch_bounds__(256) void gather_out_kernel(const half_t* __restrict__ a, int64_t wa,
+                                                         const float* __restrict__ x, int64_t wx,
+                                                         const int32_t* __restrict__ rows, int64_t r0,
+                                                         half_t* __restrict__ aw, float* __restrict__ xw) {
+    const int64_t i = blockIdx.x, r = int64_t(rows[i]) - r0;
+    const uint4* as = reinterpret_cast<const uint4*>(a + r * wa);
+    uint4* ad = reinterpret_cast<uint4*>(aw + i * wa);
+    for (int64_t q = threadIdx.x; q < wa / 8; q += blockDim.x) ad[q] = as[q];
+    const float4* xs = reinterpret_cast<const float4*>(x + r * wx);
+    float4* xd = reinterpret_cast<float4*>(xw + i * wx);
+    for (int64_t q = threadIdx.x; q < wx / 4; q += blockDim.x) xd[q] = xs[q];
+}
+
+void launch_gather_out(hipStream_t s, const half_t* a, int64_t wa, const float* x, int64_t wx, const int32_t* rows,
+                       int64_t r0, int64_t n, half_t* aw, float* xw) {
+    if (n <= 0) return;
+    if (wa % 8 != 0 || wx % 4 != 0) fail(E_INVALID, "gather_out: widths must be multiples of 8 (f16) and 4 (f32)");
+    gather_out_kernel<<<dim3(unsigned(n)), dim3(256), 0, s>>>(a, wa, x, wx, rows, r0, aw, xw);
     OMG_HIP(hipGetLastError());
 }
 

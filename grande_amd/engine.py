@@ -394,6 +394,11 @@ class Engine:
     def profile(self, on: bool) -> None:
         L.check(L.lib().omg_profile(self._h, int(on)))
 
+    def full_last_layer(self, on: bool) -> None:
+        """Run the last layer for every row (on) instead of the read-out
+        rows only (the default); the returned rows are the same bits."""
+        L.check(L.lib().omg_set_full_last_layer(self._h, int(on)))
+
     def profile_report(self) -> dict[str, tuple[int, float]]:
         """kernel name -> (launches, total ms) since profiling was switched on."""
         buf = C.create_string_buffer(1 << 16)

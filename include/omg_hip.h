@@ -240,6 +240,14 @@ int omg_sync(omg_engine *e);
  * "name launches total_ms". */
 int omg_profile(omg_engine *e, int on);
 size_t omg_profile_report(omg_engine *e, char *buf, size_t len);
+/* No counterpart in the reference, whose pass runs every layer for every
+ * row (engine.rs:1674-1751).  By default the last layer runs past its
+ * attention for the rows a request reads out only (the query tiles that
+ * hold them, then o, norms, gate/up and down on the gathered rows; every
+ * layer's K/V is still written for every row); on != 0 runs it for every
+ * row as the reference does.  The rows a pass returns are the same bits
+ * either way.  From the next pass on. */
+int omg_set_full_last_layer(omg_engine *e, int on);
 
 /* Kernel-level entry points on device pointers (the reference's matmul.rs
  * kernel tests): a weight uploaded in the device layout, then

@@ -619,3 +619,60 @@ def test_pass_split_over_streams_is_bit_equal(model, prefix_len, heads, kv):
         eng.launch()
         got = eng.read_prepared(1 << 14)
         assert np.array_equal(got, exp), f"graph replay {rep}"
+
+
+@pytest.mark.parametrize("case", ["split-global", "split-sliding", "short", "deep-k", "groups"])
+def test_last_layer_on_answer_rows_is_bit_equal(case):
+    """The last layer past its attention runs for the read-out rows only
+    (the query tiles that hold them, then o, the norms, gate/up and down on
+    the gathered rows) unless the engine is told to run it for every row,
+    as the reference does: the rows a pass returns are bit for bit the same
+    — split passes on two streams whose last layer is global or sliding, a
+    short pass, deep-K down products (pieces a workgroup each in the full
+    short pass, added in registers on the gathered rows), several groups —
+    and so are the label logits and log-sum-exp, cold and over the
+    resident prefix."""
+    rng = np.random.default_rng(61)
+    if case == "deep-k":
+        cfg = gemma3_tiny(d=2304, ff=4096, layers=2, sliding=[True, False])
+        plen, sizes = 300, (12, 9)
+    elif case == "split-sliding":
+        cfg = gguf_tiny(4, 1, window=37, vocab=64, layers=3, sliding=[False, True, True])
+        plen, sizes = 2000, (9, 40, 17)
+    else:
+        cfg = gguf_tiny(4, 1, window=37, vocab=64)
+        plen, sizes = (2000, (9, 40, 17)) if case in ("split-global", "groups") else (120, (9, 40, 17))
+    vocab = 40 if case == "deep-k" else 64
+    eng, _, _, _ = build(cfg, 53, g.Q4, g.Q8, capacity=2 * plen + 256, max_rows=32, oracle_models=False)
+    prefix = rng.integers(0, vocab, plen).tolist()
+    branches = [BranchTokens(rng.integers(0, vocab, n).tolist(), [0, n // 2, n - 1]) for n in sizes]
+    labels = list(range(1, 9))
+
+    def passes():
+        if case == "groups":
+            other = rng.integers(0, vocab, 300).tolist()
+            groups = [Group(prefix, branches), Group(other, branches[:2])]
+            eng.evict_resident()
+            return [eng.evaluate_groups(groups, Want.HIDDEN)]
+        eng.evict_resident()
+        cold = eng.evaluate(prefix, branches, Want.HIDDEN)
+        warm = eng.evaluate(prefix, branches, Want.HIDDEN)
+        assert eng.prefix_source() == PrefixSource.RESIDENT
+        eng.evict_resident()
+        lse = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
+        return [cold, warm, lse]
+
+    state = rng.bit_generator.state
+    answer = passes()
+    eng.full_last_layer(True)
+    rng.bit_generator.state = state
+    full = passes()
+    eng.full_last_layer(False)
+    def rows(out):  # a pass's rows in order, for branch or group outputs
+        return [r for o in out for b in (o.branches if hasattr(o, "branches") else [o]) for r in b.rows]
+
+    for a, b in zip(answer, full):
+        ra, rb = rows(a), rows(b)
+        assert len(ra) == len(rb) > 0
+        for u, v in zip(ra, rb):
+            assert np.array_equal(u, v), f"{case}: answer-row last layer differs from the full one"

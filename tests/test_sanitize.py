@@ -38,9 +38,13 @@ def harness() -> Path:
     exe = BUILD / "parsers_asan"
     deps = SOURCES + list(CSRC.glob("*.h"))
     if not exe.exists() or exe.stat().st_mtime < max(p.stat().st_mtime for p in deps):
+        # built under a name of this process, then moved into place: parallel
+        # test workers never run a half-written binary
+        tmp = exe.with_name(f"{exe.name}.{os.getpid()}")
         cmd = ["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
-               "-fno-sanitize-recover=all", f"-I{CSRC}", *map(str, SOURCES), "-o", str(exe)]
+               "-fno-sanitize-recover=all", f"-I{CSRC}", *map(str, SOURCES), "-o", str(tmp)]
         subprocess.run(cmd, check=True)
+        os.replace(tmp, exe)
     return exe
 
 
