@@ -261,6 +261,12 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.x_w_ = DevBuf(size_t(max_rows * d) * 4);
     E.hn_w_ = DevBuf(size_t(max_rows * d) * 2);
     E.act_w_ = DevBuf(size_t(max_rows * c.max_ff()) * 2);
+    if (c.per_layer_dim > 0) {
+        E.x16_w_ = DevBuf(size_t(max_rows * d) * 2);
+        E.plg_w_ = DevBuf(size_t(max_rows * c.per_layer_dim) * 4);
+        E.pl16_w_ = DevBuf(size_t(max_rows * c.per_layer_dim) * 2);
+        E.pli_w_ = DevBuf(size_t(max_rows * c.per_layer_dim) * 4);
+    }
     {
         int most = OMG_KSPLIT;  // the most parts of an o / down product (K splits x pieces)
         for (int64_t l = 0; l < c.layers; ++l)
@@ -573,14 +579,13 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         }
         slots += most;
     }
-    // The last layer on the answer rows only (layer_out): models without
-    // the per-layer-input block, wanted rows in ascending order (each
-    // range's share is one run of the list).  Its attention runs the items
+    // The last layer on the answer rows only (layer_out): wanted rows in
+    // ascending order (each range's share is one run of the list).  Its attention runs the items
     // of the query tiles that hold those rows, the same items a full pass
     // runs for them.
     bool asc = true;
     for (int64_t r = 1; r < nr; ++r) asc = asc && pk.wanted[size_t(r)][3] >= pk.wanted[size_t(r - 1)][3];
-    out_rows_ = !full_last_layer_ && cfg_.per_layer_dim == 0 && nr > 0 && asc;
+    out_rows_ = !full_last_layer_ && nr > 0 && asc;
     if (out_rows_) {
         const int64_t last = cfg_.layers - 1;
         const int kind = (cfg_.sliding[size_t(last)] && cfg_.window > 0) ? 0 : 1;
@@ -948,7 +953,13 @@ void Engine::layer_out(int k, const half_t* attn, const float* x, int64_t r0) {
     half_t* actw = act_w_.as<half_t>() + sb.w0 * ff;
     float* pw = a_w_.as<float>() + sb.w0 * d;
     const int64_t stride = max_rows_ * d;
-    step("gather_out", k, [&] { launch_gather_out(s, attn, W, x, d, d_wanted_ + sb.w0, r0, n, aw, xw); });
+    const int64_t P = c.per_layer_dim;
+    float* pliw = P > 0 ? pli_w_.as<float>() + sb.w0 * P : nullptr;
+    step("gather_out", k, [&] {
+        // (with per-layer inputs also the rows' slice of this layer's inputs)
+        launch_gather_out(s, attn, W, x, d, d_wanted_ + sb.w0, r0, n, aw, xw,
+                          P > 0 ? pli_.as<float>() + r0 * P * c.layers : nullptr, P * c.layers, l * P, P, pliw);
+    });
     // A deep product's K pieces run a workgroup each (the rows are few),
     // their parts [splits x group][max_rows][d] in a_w_.
     auto product = [&](const char* name, const half_t* in, int64_t kd, const DevWeight& w) {
@@ -964,9 +975,26 @@ void Engine::layer_out(int k, const half_t* attn, const float* x, int64_t r0) {
     });
     step("mm_gate_up_out", k, [&] { launch_gemm_geglu(s, hw, d, L.gate.w, L.up.w, actw, ff, n); });
     const NormParts nd = product("mm_down_out", actw, ff, L.down.w);
+    if (P == 0) {
+        step("norm_out", k, [&] {
+            launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), xw, nullptr, nullptr, n, d, c.eps, 1.0f,
+                                 nd.parts, nd.stride, nd.group);
+        });
+        return;
+    }
+    // The per-layer input block on the rows (as in layer()).
+    half_t* x16w = x16_w_.as<half_t>() + sb.w0 * d;
+    float* plgw = plg_w_.as<float>() + sb.w0 * P;
+    half_t* pl16w = pl16_w_.as<half_t>() + sb.w0 * P;
     step("norm_out", k, [&] {
-        launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), xw, nullptr, nullptr, n, d, c.eps, 1.0f, nd.parts,
+        launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), xw, nullptr, x16w, n, d, c.eps, 1.0f, nd.parts,
                              nd.stride, nd.group);
+    });
+    step("mm_pl_gate_out", k, [&] { launch_gemm(s, x16w, d, L.pl_gate.w, plgw, P, n); });
+    step("pl_gate_out", k, [&] { launch_pl_gate(s, plgw, pliw, pl16w, n, P, 1, 0); });
+    step("mm_pl_proj_out", k, [&] { launch_gemm(s, pl16w, P, L.pl_proj.w, pw, d, n); });
+    step("norm_out", k, [&] {
+        launch_residual_norm(s, pw, L.pl_norm.as<float>(), xw, nullptr, nullptr, n, d, c.eps, L.out_scale);
     });
 }
 

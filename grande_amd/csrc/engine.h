@@ -267,6 +267,9 @@ class Engine {
     // [max_rows] rows: attention output, stream, normed stream, gated
     // activations, product parts (OMG_KSPLIT of them)
     DevBuf attn_w_, x_w_, hn_w_, act_w_, a_w_;
+    // ... and with per-layer inputs: f16(x), the gate's product, the gated
+    // inputs (f16) and the rows' last-layer slice of the inputs
+    DevBuf x16_w_, plg_w_, pl16_w_, pli_w_;
     std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
     // pinned host staging
     void* h_in_ = nullptr;

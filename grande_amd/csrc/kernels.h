@@ -108,9 +108,11 @@ void launch_rope_table(hipStream_t s, const float* inv_freq, int64_t rows, int64
 void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int64_t n, int64_t d,
                        const float* w, float eps, float* rows);
 // aw[i] = a[rows[i] - r0] (f16, width wa), xw[i] = x[rows[i] - r0] (f32,
-// width wx), i < n.
+// width wx), i < n; with p, pw[i] = p[rows[i] - r0][po .. po + wp) (row
+// stride ps).
 void launch_gather_out(hipStream_t s, const half_t* a, int64_t wa, const float* x, int64_t wx, const int32_t* rows,
-                       int64_t r0, int64_t n, half_t* aw, float* xw);
+                       int64_t r0, int64_t n, half_t* aw, float* xw, const float* p = nullptr, int64_t ps = 0,
+                       int64_t po = 0, int64_t wp = 0, float* pw = nullptr);
 // out[r][j] = rows[r] . deq(E[col(j)]) in f32 (+ softcap), col(j) = cols ? cols[j] : j.
 // logits[r][j] = rows[r] . deq(E[cols ? cols[j] : j]) (softcap applied),
 // f32 [nrows][ncols]; with `part` (logits_blocks(ncols) x nrows pairs) each

@@ -591,13 +591,16 @@ void launch_final_rows(hipStream_t s, const float* x, const int32_t* wanted, int
     OMG_HIP(hipGetLastError());
 }
 
-// Rows rows[i] - r0 (i < n) of an f16 matrix of width wa and an f32 matrix
-// of width wx, copied to rows i of aw and xw: one workgroup per row, 16
-// bytes per thread and step.
+// Rows rows[i] - r0 (i < n) of an f16 matrix of width wa, an f32 matrix of
+// width wx and (p non-null) wp f32 columns from column po of an f32 matrix
+// of row stride ps, copied to rows i of aw, xw and pw: one workgroup per
+// row, 16 bytes per thread and step.
 __global__ __launch_bounds__(256) void gather_out_kernel(const half_t* __restrict__ a, int64_t wa,
                                                          const float* __restrict__ x, int64_t wx,
-                                                         const int32_t* __restrict__ rows, int64_t r0,
-                                                         half_t* __restrict__ aw, float* __restrict__ xw) {
+                                                         const float* __restrict__ p, int64_t ps, int64_t po,
+                                                         int64_t wp, const int32_t* __restrict__ rows, int64_t r0,
+                                                         half_t* __restrict__ aw, float* __restrict__ xw,
+                                                         float* __restrict__ pw) {
     const int64_t i = blockIdx.x, r = int64_t(rows[i]) - r0;
     const uint4* as = reinterpret_cast<const uint4*>(a + r * wa);
     uint4* ad = reinterpret_cast<uint4*>(aw + i * wa);
@@ -605,13 +608,20 @@ __global__ __launch_bounds__(256) void gather_out_kernel(const half_t* __restric
     const float4* xs = reinterpret_cast<const float4*>(x + r * wx);
     float4* xd = reinterpret_cast<float4*>(xw + i * wx);
     for (int64_t q = threadIdx.x; q < wx / 4; q += blockDim.x) xd[q] = xs[q];
+    if (p) {
+        const float4* ps4 = reinterpret_cast<const float4*>(p + r * ps + po);
+        float4* pd = reinterpret_cast<float4*>(pw + i * wp);
+        for (int64_t q = threadIdx.x; q < wp / 4; q += blockDim.x) pd[q] = ps4[q];
+    }
 }
 
 void launch_gather_out(hipStream_t s, const half_t* a, int64_t wa, const float* x, int64_t wx, const int32_t* rows,
-                       int64_t r0, int64_t n, half_t* aw, float* xw) {
+                       int64_t r0, int64_t n, half_t* aw, float* xw, const float* p, int64_t ps, int64_t po,
+                       int64_t wp, float* pw) {
     if (n <= 0) return;
-    if (wa % 8 != 0 || wx % 4 != 0) fail(E_INVALID, "gather_out: widths must be multiples of 8 (f16) and 4 (f32)");
-    gather_out_kernel<<<dim3(unsigned(n)), dim3(256), 0, s>>>(a, wa, x, wx, rows, r0, aw, xw);
+    if (wa % 8 != 0 || wx % 4 != 0 || (p && (wp % 4 != 0 || ps % 4 != 0 || po % 4 != 0 || !pw)))
+        fail(E_INVALID, "gather_out: widths must be multiples of 8 (f16) and 4 (f32)");
+    gather_out_kernel<<<dim3(unsigned(n)), dim3(256), 0, s>>>(a, wa, x, wx, p, ps, po, wp, rows, r0, aw, xw, pw);
     OMG_HIP(hipGetLastError());
 }
 

@@ -621,21 +621,26 @@ def test_pass_split_over_streams_is_bit_equal(model, prefix_len, heads, kv):
         assert np.array_equal(got, exp), f"graph replay {rep}"
 
 
-@pytest.mark.parametrize("case", ["split-global", "split-sliding", "short", "deep-k", "groups"])
+@pytest.mark.parametrize("case", ["split-global", "split-sliding", "short", "deep-k", "groups", "gemma4-split",
+                                  "gemma4-short"])
 def test_last_layer_on_answer_rows_is_bit_equal(case):
     """The last layer past its attention runs for the read-out rows only
     (the query tiles that hold them, then o, the norms, gate/up and down on
     the gathered rows) unless the engine is told to run it for every row,
     as the reference does: the rows a pass returns are bit for bit the same
     — split passes on two streams whose last layer is global or sliding, a
-    short pass, deep-K down products (pieces a workgroup each in the full
-    short pass, added in registers on the gathered rows), several groups —
-    and so are the label logits and log-sum-exp, cold and over the
-    resident prefix."""
+    short pass, deep-K down products (a piece per workgroup on the gathered
+    rows, added in registers in the full long pass), several groups, and
+    Gemma 4 (a head_dim 512 last layer reading shared K/V, the per-layer
+    input block on the gathered rows) — and so are the label logits and
+    log-sum-exp, cold and over the resident prefix."""
     rng = np.random.default_rng(61)
-    if case == "deep-k":
+    if case.startswith("gemma4"):
+        cfg = gemma4_tiny(4, 1, window=37, vocab=64)
+        plen, sizes = (2000 if case == "gemma4-split" else 120), (9, 40, 17)
+    elif case == "deep-k":
         cfg = gemma3_tiny(d=2304, ff=4096, layers=2, sliding=[True, False])
-        plen, sizes = 300, (12, 9)
+        plen, sizes = 600, (12, 9)  # 621 rows: the full pass adds the pieces in registers
     elif case == "split-sliding":
         cfg = gguf_tiny(4, 1, window=37, vocab=64, layers=3, sliding=[False, True, True])
         plen, sizes = 2000, (9, 40, 17)
@@ -662,11 +667,20 @@ def test_last_layer_on_answer_rows_is_bit_equal(case):
         lse = eng.evaluate(prefix, branches, Want.LABELS_LSE, labels)
         return [cold, warm, lse]
 
+    def gathers() -> bool:  # whether a (profiled, one-range) pass runs the answer-row last layer
+        eng.profile(True)
+        eng.evaluate(prefix, branches, Want.HIDDEN)
+        ran = "gather_out" in eng.profile_report()
+        eng.profile(False)
+        return ran
+
     state = rng.bit_generator.state
     answer = passes()
+    assert gathers()
     eng.full_last_layer(True)
     rng.bit_generator.state = state
     full = passes()
+    assert not gathers()
     eng.full_last_layer(False)
     def rows(out):  # a pass's rows in order, for branch or group outputs
         return [r for o in out for b in (o.branches if hasattr(o, "branches") else [o]) for r in b.rows]
