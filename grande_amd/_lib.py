@@ -145,6 +145,7 @@ _SIGS = {
     "omg_laya_launch": (C.c_int, [_P]),
     "omg_laya_sync": (C.c_int, [_P]),
     "omg_laya_profile": (C.c_int, [_P, C.c_int]),
+    "omg_laya_set_full_last_layer": (C.c_int, [_P, C.c_int]),
     "omg_laya_profile_report": (C.c_size_t, [_P, C.c_char_p, C.c_size_t]),
 }
 

@@ -758,6 +758,10 @@ int omg_laya_profile(omg_laya* e, int on) {
     return guard([&] { laya(e).set_profile(on != 0); });
 }
 
+int omg_laya_set_full_last_layer(omg_laya* e, int on) {
+    return guard([&] { laya(e).set_full_last_layer(on != 0); });
+}
+
 size_t omg_laya_profile_report(omg_laya* e, char* buf, size_t len) {
     std::string s;
     guard([&] { s = laya(e).profile_report(); });

@@ -409,6 +409,11 @@ std::unique_ptr<LayaEngine> LayaBuilder::finish(int64_t capacity, int64_t max_ro
     E.act16_ = DevBuf(size_t(cap * std::max(c.ff, 4 * d)) * 2);
     E.rows_ = DevBuf(size_t(max_rows * d) * 4);
     E.wanted_ = DevBuf(size_t(max_rows) * 4);
+    E.attn_w_ = DevBuf(size_t(max_rows * d) * 2);
+    E.x_w_ = DevBuf(size_t(max_rows * d) * 4);
+    E.a_w_ = DevBuf(size_t(max_rows * d) * 4);
+    E.h16_w_ = DevBuf(size_t(max_rows * d) * 2);
+    E.act_w_ = DevBuf(size_t(max_rows * 4 * d) * 2);
     E.h_in_bytes_ = size_t(cap) * (4 + 4 + 16) + size_t(max_rows) * 4;
     OMG_HIP(hipHostMalloc(&E.h_in_, E.h_in_bytes_, hipHostMallocDefault));
     E.h_out_bytes_ = size_t(max_rows * d) * 4;
@@ -610,6 +615,28 @@ void LayaEngine::forward() {
         const bool last = hl + 1 == head_.size();
         step("mm_in", [&] { launch_gemm_qkv_heads(stream_, h16, d, H.in_proj.w, H.in_proj_b16.as<uint16_t>(), qh, t); });
         step("head_attention", [&] { launch_attention_bi(stream_, qh, heads, t, 0, attn); });
+        if (last && !full_last_layer_ && nrows_ > 0) {
+            // Past its attention the last layer feeds only the read-out
+            // rows: they are gathered (attention output, stream) and the
+            // rest of the layer runs on them; every step is per row, so
+            // they come out as the full layer leaves them.
+            const int64_t n = nrows_;
+            half_t* aw = attn_w_.as<half_t>();
+            float* xw = x_w_.as<float>();
+            float* pw = a_w_.as<float>();
+            half_t* hw = h16_w_.as<half_t>();
+            half_t* actw = act_w_.as<half_t>();
+            step("gather_out", [&] { launch_gather_out(stream_, attn, d, x, d, wanted_.as<int32_t>(), 0, n, aw, xw); });
+            step("mm_out_out", [&] { launch_gemm(stream_, aw, d, H.out_proj.w, pw, d, n); });
+            step("add_out_norm2_out", [&] {
+                launch_add_ln(stream_, xw, pw, H.out_proj_b.as<float>(), H.norm2_w.as<float>(), H.norm2_b.as<float>(),
+                              c.eps, n, d, hw);
+            });
+            step("mm_l1_out", [&] { launch_gemm_bias_relu(stream_, hw, d, H.l1.w, H.l1_b16.as<uint16_t>(), actw, 4 * d, n); });
+            step("mm_l2_out", [&] { launch_gemm(stream_, actw, 4 * d, H.l2.w, pw, d, n); });
+            step("rows", [&] { launch_gather_rows(stream_, xw, pw, H.l2_b.as<float>(), nullptr, n, d, rows_.as<float>()); });
+            break;
+        }
         step("mm_out", [&] { launch_gemm(stream_, attn, d, H.out_proj.w, a, d, t); });
         step("add_out_norm2", [&] {
             launch_add_ln(stream_, x, a, H.out_proj_b.as<float>(), H.norm2_w.as<float>(), H.norm2_b.as<float>(), c.eps,
@@ -635,6 +662,11 @@ void LayaEngine::forward() {
 }
 
 void LayaEngine::prepare(const LayaSeq* seqs, int64_t n) { pack(seqs, n); }
+
+void LayaEngine::set_full_last_layer(bool on) {
+    sync();
+    full_last_layer_ = on;
+}
 
 void LayaEngine::launch_prepared() {
     if (t_ == 0) fail(E_INVALID, "nothing prepared");

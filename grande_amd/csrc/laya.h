@@ -120,6 +120,9 @@ class LayaEngine {
     void set_profile(bool on);
     std::string profile_report() const;
     int64_t prepared_rows() const { return nrows_; }
+    // The last decision-head layer past its attention for every row (on)
+    // or, the default, for the read-out rows only; the same rows either way.
+    void set_full_last_layer(bool on);
 
    private:
     friend class LayaBuilder;
@@ -151,6 +154,10 @@ class LayaEngine {
     DevBuf rope_local_, rope_global_;
     // workspace
     DevBuf ids_, qtypes_, meta_, x_, a_, h16_, q16_, k16_, vt_, attn16_, act16_, rows_, wanted_;
+    // The last head layer on the read-out rows: [max_rows] rows of the
+    // attention output, stream, product, normed stream and activations.
+    bool full_last_layer_ = false;
+    DevBuf attn_w_, x_w_, a_w_, h16_w_, act_w_;
     void* h_in_ = nullptr;
     size_t h_in_bytes_ = 0;
     void* h_out_ = nullptr;

@@ -377,14 +377,14 @@ __global__ __launch_bounds__(256) void add_ln_final_kernel(float* __restrict__ x
 }
 
 // out[i] = (a[r] + bias) + x[r] (bias_act.wgsl mode 0 with `residual`,
-// laya.rs:1385-1387), or x[r]; r = rows[i].
+// laya.rs:1385-1387), or x[r]; r = rows[i] (i without a list).
 __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restrict__ x, const float* __restrict__ a,
                                                           const float* __restrict__ bias,
                                                           const int32_t* __restrict__ rows, int64_t n, int64_t d,
                                                           float* __restrict__ out) {
     const int64_t i = int64_t(blockIdx.x) * 4 + threadIdx.x / WAVE;
     if (i >= n) return;
-    const int64_t r = rows[i];
+    const int64_t r = rows ? rows[i] : i;
     for (int64_t c = int64_t(threadIdx.x % WAVE) * 4; c < d; c += WAVE * 4) {
         float4 v = *reinterpret_cast<const float4*>(x + r * d + c);
         if (a) {

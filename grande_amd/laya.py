@@ -241,6 +241,11 @@ class LayaEngine:
     def profile(self, on: bool) -> None:
         L.check(L.lib().omg_laya_profile(self._h, int(on)))
 
+    def full_last_layer(self, on: bool) -> None:
+        """Run the last head layer for every row (on) instead of the read-out
+        rows only (the default); the returned rows are the same bits."""
+        L.check(L.lib().omg_laya_set_full_last_layer(self._h, int(on)))
+
     def profile_report(self) -> dict[str, tuple[int, float]]:
         n = L.lib().omg_laya_profile_report(self._h, None, 0)
         buf = C.create_string_buffer(n + 1)

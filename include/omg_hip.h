@@ -379,6 +379,12 @@ int omg_laya_launch(omg_laya *e);
 int omg_laya_sync(omg_laya *e);
 int omg_laya_profile(omg_laya *e, int on);
 size_t omg_laya_profile_report(omg_laya *e, char *buf, size_t len);
+/* No counterpart in the reference, whose head layers run every row
+ * (laya.rs:1346-1392).  By default the last decision-head layer runs past
+ * its attention for the read-out rows only (o projection, LayerNorm, l1,
+ * l2 on the gathered [CLS] and marker rows); on != 0 runs it for every row.
+ * The rows are the same bits either way.  From the next pass on. */
+int omg_laya_set_full_last_layer(omg_laya *e, int on);
 
 #ifdef __cplusplus
 }

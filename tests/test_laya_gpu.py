@@ -255,6 +255,31 @@ def test_sequence_rows_do_not_depend_on_the_batch():
         assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("head_layers", [1, 2])
+def test_last_head_layer_on_read_out_rows_is_bit_equal(head_layers):
+    """The last decision-head layer past its attention runs for the [CLS]
+    and marker rows only unless the engine is told to run it for every row:
+    hidden rows and scores are bit for bit the same."""
+    cfg = tiny(layers=3, head_layers=head_layers)
+    w = ly.synth_weights(cfg, 17, g.Q8, g.Q8)
+    eng = ly.LayaEngine.new(w, 2048, 64)
+    seqs = random_seqs(np.random.default_rng(23), 300, 12, 3, 150)
+    eng.profile(True)
+    rows = eng.hidden(seqs)
+    assert "gather_out" in eng.profile_report()
+    eng.profile(False)
+    outs = eng.evaluate(seqs)
+    eng.full_last_layer(True)
+    full_rows = eng.hidden(seqs)
+    full_outs = eng.evaluate(seqs)
+    eng.full_last_layer(False)
+    for a, b in zip(rows, full_rows):
+        assert np.array_equal(a, b)
+    for a, b in zip(outs, full_outs):
+        assert np.array_equal(a.logits, b.logits)
+        assert (a.act_probability is None and b.act_probability is None) or a.act_probability == b.act_probability
+
+
 def test_no_head_layers_and_no_type_embedding():
     cfg = tiny(head_layers=0, type_emb=False, act_costs=None)
     eng, orc = engine_and_oracle(cfg, 2, g.Q8, 512, 32)
