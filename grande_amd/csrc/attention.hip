@@ -154,6 +154,8 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a, const in
     const int u_lane = lr / HPG;  // the lane's token within each block
     const int head = g * HPG + lr % HPG;
     const int4* meta = reinterpret_cast<const int4*>(a.meta);
+    const int4* qmeta = a.qmeta ? reinterpret_cast<const int4*>(a.qmeta) : meta + a.base;  // the queries' rows
+    const int64_t kend = a.kend > 0 ? a.kend : a.base + a.t;                                 // keys before this row
 
     const half_t* kbase = a.kc + int64_t(g) * a.cap_pad * HD;
     const half_t* vbase = a.vt + int64_t(g) * (a.cap_pad / 64) * HD * 64;
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a, const in
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
         int4 m = make_int4(-1, -2, 0, 0);  // past the pass: sees nothing (positions are >= 0)
-        if (tok0 + u < a.t) m = meta[a.base + tok0 + u];
+        if (tok0 + u < a.t) m = qmeta[tok0 + u];
         qpos[u] = __builtin_amdgcn_readfirstlane(m.x);
         qseq[u] = __builtin_amdgcn_readfirstlane(m.y);
     }
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a, const in
         // Each condition of `visible` is one lane ballot (a vector compare
         // into a scalar mask); the masks combine in scalar code.
         constexpr uint64_t KEYS = A_KT == 64 ? ~0ull : 0xffffffffull;
-        const uint64_t ok = __ballot(int64_t(tile) * A_KT + (lane % A_KT) < a.base + a.t) & KEYS;
+        const uint64_t ok = __ballot(int64_t(tile) * A_KT + (lane % A_KT) < kend) & KEYS;
         const uint64_t prefix_keys = __ballot((km.y & 0xfff) == 0);
         const int kgroup = km.y >> 12;
         const unsigned reach = a.window > 0 ? unsigned(a.window) : 0x7fffffffu;
@@ -687,7 +689,8 @@ void launch_attention(hipStream_t s, const AttnArgs& a, const int4* items, int64
     if (a.kv_heads <= 0 || a.heads % a.kv_heads) fail(E_INVALID, "attention: heads / kv_heads");
     const int hpg = a.heads / a.kv_heads;
     if (16 % hpg) fail(E_INVALID, "attention: query heads per KV head must divide 16");
-    if (a.cap_pad % 64 || a.base + a.t > a.cap_pad) fail(E_INVALID, "attention: cache rows out of range");
+    if (a.cap_pad % 64 || a.base + a.t > a.cap_pad || a.kend > a.cap_pad)
+        fail(E_INVALID, "attention: cache rows out of range");
     if (a.window < 0) fail(E_INVALID, "attention: negative window");
     // the query rows are read through a buffer resource (32-bit byte offsets)
     if (a.t * a.heads * a.hd * 2 > 0x7fffffff) fail(E_INVALID, "attention: query rows past 2 GiB");

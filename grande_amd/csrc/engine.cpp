@@ -261,12 +261,18 @@ std::unique_ptr<Engine> Builder::finish(int64_t capacity, int64_t max_rows) {
     E.x_w_ = DevBuf(size_t(max_rows * d) * 4);
     E.hn_w_ = DevBuf(size_t(max_rows * d) * 2);
     E.act_w_ = DevBuf(size_t(max_rows * c.max_ff()) * 2);
+    E.q16_w_ = DevBuf(size_t(max_rows * c.heads * hd) * 2);
+    E.qkv_w_ = DevBuf(size_t(max_rows * c.max_qkv()) * 4);
     if (c.per_layer_dim > 0) {
         E.x16_w_ = DevBuf(size_t(max_rows * d) * 2);
         E.plg_w_ = DevBuf(size_t(max_rows * c.per_layer_dim) * 4);
         E.pl16_w_ = DevBuf(size_t(max_rows * c.per_layer_dim) * 2);
-        E.pli_w_ = DevBuf(size_t(max_rows * c.per_layer_dim) * 4);
+        E.pli_w_ = DevBuf(size_t(max_rows * c.per_layer_dim * c.layers) * 4);
     }
+    // The answer-row path starts at the last layer that writes K/V (Gemma
+    // 4's K/V-sharing layers read an earlier layer's cache).
+    for (int64_t l = 0; l < c.layers; ++l)
+        if (c.has_kv(l)) E.out_layer_ = l;
     {
         int most = OMG_KSPLIT;  // the most parts of an o / down product (K splits x pieces)
         for (int64_t l = 0; l < c.layers; ++l)
@@ -587,8 +593,8 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     for (int64_t r = 1; r < nr; ++r) asc = asc && pk.wanted[size_t(r)][3] >= pk.wanted[size_t(r - 1)][3];
     out_rows_ = !full_last_layer_ && nr > 0 && asc;
     if (out_rows_) {
-        const int64_t last = cfg_.layers - 1;
-        const int kind = (cfg_.sliding[size_t(last)] && cfg_.window > 0) ? 0 : 1;
+        const int64_t ol = out_layer_;
+        const int kind = (cfg_.sliding[size_t(ol)] && cfg_.window > 0) ? 0 : 1;
         int64_t i = 0;
         for (int k = 0; k < ns; ++k) {
             Sub& sb = sub_[k];
@@ -608,6 +614,32 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
                 if (tile[size_t(m.x)]) sb.out_work.merges.push_back(m);
         }
     }
+    // The layers after out_layer_ on the answer rows alone: their metadata
+    // rows, and per layer type attention items over them (partial slots
+    // after the ranges').
+    std::vector<int32_t> tail_meta;
+    tail_rows_ = 0;
+    if (out_rows_ && out_layer_ + 1 < cfg_.layers) {
+        tail_rows_ = nr;
+        tail_meta.resize(size_t(nr) * 4);
+        for (int64_t i = 0; i < nr; ++i)
+            std::memcpy(&tail_meta[size_t(i) * 4], pk.meta.data() + 4 * pk.wanted[size_t(i)][3], 16);
+        int64_t most = 0;
+        for (int kind = 0; kind < 2; ++kind) {
+            AttnWork& w = tail_work_[kind];
+            const int window = kind == 0 ? int(cfg_.window) : 0;
+            attention_work(tail_meta.data(), nr, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind], 2, w);
+            if (!w.aligned || int64_t(w.items.size()) * cfg_.kv_heads > cus_)
+                attention_work(tail_meta.data(), nr, int(cfg_.heads), int(cfg_.kv_heads), window, attn_chunk_[kind],
+                               4, w);
+            for (int4& it : w.items)
+                if (it.w >= 0) it.w += int(slots);
+            for (int4& m : w.merges) m.y += int(slots);
+            most = std::max<int64_t>(most, w.slots);
+        }
+        slots += most;
+    }
+    tail_kend_ = pk.base + t;
     // The pass's inputs go to the device in two copies: the cache metadata
     // of its rows, and one block [ids | wanted rows | labels | per range and
     // layer type: work items, merges] (16-byte aligned parts).
@@ -627,6 +659,12 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
         }
         o_out_items[k] = part(out_rows_ ? sub_[k].out_work.items.size() * 16 : 0);
         o_out_merges[k] = part(out_rows_ ? sub_[k].out_work.merges.size() * 16 : 0);
+    }
+    const size_t o_tail_meta = part(tail_meta.size() * 4);
+    size_t o_tail_items[2], o_tail_merges[2];
+    for (int kind = 0; kind < 2; ++kind) {
+        o_tail_items[kind] = part(tail_rows_ ? tail_work_[kind].items.size() * 16 : 0);
+        o_tail_merges[kind] = part(tail_rows_ ? tail_work_[kind].merges.size() * 16 : 0);
     }
     const size_t meta_bytes = a16(size_t(t) * 16);
     // The previous pass may still read the staging buffer; from here the
@@ -668,6 +706,14 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
             if (!wk.items.empty()) std::memcpy(hb + o_out_items[k], wk.items.data(), wk.items.size() * 16);
             if (!wk.merges.empty()) std::memcpy(hb + o_out_merges[k], wk.merges.data(), wk.merges.size() * 16);
         }
+    if (tail_rows_) {
+        std::memcpy(hb + o_tail_meta, tail_meta.data(), tail_meta.size() * 4);
+        for (int kind = 0; kind < 2; ++kind) {
+            const AttnWork& wk = tail_work_[kind];
+            if (!wk.items.empty()) std::memcpy(hb + o_tail_items[kind], wk.items.data(), wk.items.size() * 16);
+            if (!wk.merges.empty()) std::memcpy(hb + o_tail_merges[kind], wk.merges.data(), wk.merges.size() * 16);
+        }
+    }
     OMG_HIP(hipMemcpyAsync(meta_.as<uint8_t>() + pk.base * 16, h, size_t(t) * 16, hipMemcpyHostToDevice, stream_));
     OMG_HIP(hipMemcpyAsync(in_.p, hb, in_bytes, hipMemcpyHostToDevice, stream_));
     uint8_t* d = in_.as<uint8_t>();
@@ -685,6 +731,11 @@ void Engine::upload(const Packed& pk, const uint32_t* labels, int64_t nlabels) {
     for (int k = 0; k < ns; ++k) {
         sub_[k].d_out_items = reinterpret_cast<const int4*>(d + o_out_items[k]);
         sub_[k].d_out_merges = reinterpret_cast<const int4*>(d + o_out_merges[k]);
+    }
+    d_tail_meta_ = reinterpret_cast<const int32_t*>(d + o_tail_meta);
+    for (int kind = 0; kind < 2; ++kind) {
+        d_tail_items_[kind] = reinterpret_cast<const int4*>(d + o_tail_items[kind]);
+        d_tail_merges_[kind] = reinterpret_cast<const int4*>(d + o_tail_merges[kind]);
     }
 }
 
@@ -798,7 +849,8 @@ void Engine::forward(int64_t base) {
             });
         }
     }
-    for (int64_t l = 0; l < c.layers; ++l)
+    const int64_t full_layers = out_rows_ ? out_layer_ + 1 : c.layers;
+    for (int64_t l = 0; l < full_layers; ++l)
         for (int k = 0; k < ns; ++k) layer(l, k, base);
     if (ns > 1) {
         for (int k = 1; k < ns; ++k) {
@@ -806,6 +858,9 @@ void Engine::forward(int64_t base) {
             OMG_HIP(hipStreamWaitEvent(stream_, ev_join_[k], 0));
         }
     }
+    // Past the last layer that writes K/V, the answer rows alone.
+    if (tail_rows_ > 0)
+        for (int64_t l = full_layers; l < c.layers; ++l) layer_tail(l);
 }
 
 // Layer l of range k (rows [r0, r1) of the pass, cache rows from base + r0).
@@ -879,9 +934,9 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     att.part_ml = part_ml_.as<float>();
     const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
     const int nw = sb.work[kind].nw;
-    if (out_rows_ && l + 1 == c.layers) {
-        // The last layer: attention for the query tiles of the answer rows,
-        // then the rest on those rows alone.
+    if (out_rows_ && l == out_layer_) {
+        // The last layer that writes K/V: attention for the query tiles of
+        // the answer rows, then the rest on those rows alone.
         const int64_t ni = int64_t(sb.out_work.items.size()), nm = int64_t(sb.out_work.merges.size());
         if (ni > 0) step("attention_out", k, [&] { launch_attention(s, att, sb.d_out_items, ni, nw); });
         if (nm > 0) step("attention_merge_out", k, [&] { launch_attention_merge(s, att, sb.d_out_merges, nm, nw); });
@@ -930,72 +985,162 @@ void Engine::layer(int64_t l, int k, int64_t pass_base) {
     });
 }
 
-// Range k's answer rows [w0, w1) through the last layer past its
-// attention: gathered (attention output f16, stream f32) into rows w0.. of
-// the answer-row buffers, then o, the residual norms, gate/up and down on
-// those rows only.  The products' K splits are the full pass's (a function
-// of the shape); deep K pieces add in the GEMM's registers, the sums a
-// piece-per-workgroup pass gives as well.  Every step is per row and does
-// not depend on the other rows of its launch, so the rows are those of the
-// full last layer.
+// Range k's answer rows [w0, w1) through layer out_layer_ (the last that
+// writes K/V) past its attention: gathered (attention output f16, stream
+// f32, with per-layer inputs the rows' inputs of every layer) into rows
+// w0.. of the answer-row buffers, then the rest of the layer on them.
 void Engine::layer_out(int k, const half_t* attn, const float* x, int64_t r0) {
     const Config& c = cfg_;
     const Sub& sb = sub_[k];
     const int64_t n = sb.w1 - sb.w0;
     if (n == 0) return;
-    const int64_t l = c.layers - 1, d = c.d;
+    const int64_t l = out_layer_, d = c.d, P = c.per_layer_dim;
+    const int64_t W = c.heads * c.head_dim[size_t(l)];
+    const hipStream_t s = sub_stream_[k];
+    RowBufs b = row_bufs(sb.w0, W, c.ff[size_t(l)]);
+    step("gather_out", k, [&] {
+        launch_gather_out(s, attn, W, x, d, d_wanted_ + sb.w0, r0, n, b.aw, b.xw,
+                          P > 0 ? pli_.as<float>() + r0 * P * c.layers : nullptr, P * c.layers, 0, P * c.layers,
+                          b.pliw);
+    });
+    rows_post(l, k, s, n, b);
+}
+
+// The answer-row buffers from row w0 on, for a layer of attention width W
+// and feed-forward width ff.
+Engine::RowBufs Engine::row_bufs(int64_t w0, int64_t W, int64_t ff) {
+    const Config& c = cfg_;
+    const int64_t d = c.d, P = c.per_layer_dim;
+    RowBufs b;
+    b.aw = attn_w_.as<half_t>() + w0 * W;
+    b.xw = x_w_.as<float>() + w0 * d;
+    b.hw = hn_w_.as<half_t>() + w0 * d;
+    b.actw = act_w_.as<half_t>() + w0 * ff;
+    b.pw = a_w_.as<float>() + w0 * d;
+    if (P > 0) {
+        b.pliw = pli_w_.as<float>() + w0 * P * c.layers;
+        b.x16w = x16_w_.as<half_t>() + w0 * d;
+        b.plgw = plg_w_.as<float>() + w0 * P;
+        b.pl16w = pl16_w_.as<half_t>() + w0 * P;
+    }
+    return b;
+}
+
+// Layer l past its attention on n gathered rows (attention output b.aw),
+// on stream s: o, the residual norms, gate/up, down and the per-layer-input
+// block, the last norm writing the next layer's normed rows to b.hw (after
+// the model's last layer only the stream).  The products' K splits are the
+// full pass's (a function of the shape); a deep product's K pieces run a
+// workgroup each, their parts [splits x group][max_rows][d] in a_w_, and
+// the norm adds them in the long pass's order.  Every step is per row and
+// does not depend on the other rows of its launch, so the rows are those of
+// the full layer.
+void Engine::rows_post(int64_t l, int k, hipStream_t s, int64_t n, const RowBufs& b) {
+    const Config& c = cfg_;
+    const int64_t d = c.d, P = c.per_layer_dim;
     const Layer& L = layers_[size_t(l)];
     const int64_t W = c.heads * c.head_dim[size_t(l)], ff = c.ff[size_t(l)];
-    const hipStream_t s = sub_stream_[k];
-    half_t* aw = attn_w_.as<half_t>() + sb.w0 * W;
-    float* xw = x_w_.as<float>() + sb.w0 * d;
-    half_t* hw = hn_w_.as<half_t>() + sb.w0 * d;
-    half_t* actw = act_w_.as<half_t>() + sb.w0 * ff;
-    float* pw = a_w_.as<float>() + sb.w0 * d;
     const int64_t stride = max_rows_ * d;
-    const int64_t P = c.per_layer_dim;
-    float* pliw = P > 0 ? pli_w_.as<float>() + sb.w0 * P : nullptr;
-    step("gather_out", k, [&] {
-        // (with per-layer inputs also the rows' slice of this layer's inputs)
-        launch_gather_out(s, attn, W, x, d, d_wanted_ + sb.w0, r0, n, aw, xw,
-                          P > 0 ? pli_.as<float>() + r0 * P * c.layers : nullptr, P * c.layers, l * P, P, pliw);
-    });
-    // A deep product's K pieces run a workgroup each (the rows are few),
-    // their parts [splits x group][max_rows][d] in a_w_.
     auto product = [&](const char* name, const half_t* in, int64_t kd, const DevWeight& w) {
         const SplitPlan p = split_plan(kd, d, n);
         const int parts = p.splits * p.group;
-        step(name, k, [&] { launch_gemm_splitk(s, in, kd, w, pw, d, n, parts, stride); });
-        return NormParts{pw, parts, stride, p.group};
+        step(name, k, [&] { launch_gemm_splitk(s, in, kd, w, b.pw, d, n, parts, stride); });
+        return NormParts{b.pw, parts, stride, p.group};
     };
-    const NormParts no = product("mm_o_out", aw, W, L.o.w);
+    const NormParts no = product("mm_o_out", b.aw, W, L.o.w);
     step("norm_out", k, [&] {
-        launch_residual_norm(s, no.a, L.post_attn_norm.as<float>(), xw, L.ffn_norm.as<float>(), hw, n, d, c.eps,
+        launch_residual_norm(s, no.a, L.post_attn_norm.as<float>(), b.xw, L.ffn_norm.as<float>(), b.hw, n, d, c.eps,
                              1.0f, no.parts, no.stride, no.group);
     });
-    step("mm_gate_up_out", k, [&] { launch_gemm_geglu(s, hw, d, L.gate.w, L.up.w, actw, ff, n); });
-    const NormParts nd = product("mm_down_out", actw, ff, L.down.w);
+    step("mm_gate_up_out", k, [&] { launch_gemm_geglu(s, b.hw, d, L.gate.w, L.up.w, b.actw, ff, n); });
+    const NormParts nd = product("mm_down_out", b.actw, ff, L.down.w);
+    const float* next = l + 1 < c.layers ? layers_[size_t(l + 1)].attn_norm.as<float>() : nullptr;
+    half_t* next_hn = next ? b.hw : nullptr;
     if (P == 0) {
         step("norm_out", k, [&] {
-            launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), xw, nullptr, nullptr, n, d, c.eps, 1.0f,
+            launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), b.xw, next, next_hn, n, d, c.eps, 1.0f,
                                  nd.parts, nd.stride, nd.group);
         });
         return;
     }
     // The per-layer input block on the rows (as in layer()).
-    half_t* x16w = x16_w_.as<half_t>() + sb.w0 * d;
-    float* plgw = plg_w_.as<float>() + sb.w0 * P;
-    half_t* pl16w = pl16_w_.as<half_t>() + sb.w0 * P;
     step("norm_out", k, [&] {
-        launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), xw, nullptr, x16w, n, d, c.eps, 1.0f, nd.parts,
-                             nd.stride, nd.group);
+        launch_residual_norm(s, nd.a, L.post_ffn_norm.as<float>(), b.xw, nullptr, b.x16w, n, d, c.eps, 1.0f,
+                             nd.parts, nd.stride, nd.group);
     });
-    step("mm_pl_gate_out", k, [&] { launch_gemm(s, x16w, d, L.pl_gate.w, plgw, P, n); });
-    step("pl_gate_out", k, [&] { launch_pl_gate(s, plgw, pliw, pl16w, n, P, 1, 0); });
-    step("mm_pl_proj_out", k, [&] { launch_gemm(s, pl16w, P, L.pl_proj.w, pw, d, n); });
+    step("mm_pl_gate_out", k, [&] { launch_gemm(s, b.x16w, d, L.pl_gate.w, b.plgw, P, n); });
+    step("pl_gate_out", k, [&] { launch_pl_gate(s, b.plgw, b.pliw, b.pl16w, n, P, c.layers, l); });
+    step("mm_pl_proj_out", k, [&] { launch_gemm(s, b.pl16w, P, L.pl_proj.w, b.pw, d, n); });
     step("norm_out", k, [&] {
-        launch_residual_norm(s, pw, L.pl_norm.as<float>(), xw, nullptr, nullptr, n, d, c.eps, L.out_scale);
+        launch_residual_norm(s, b.pw, L.pl_norm.as<float>(), b.xw, next, next_hn, n, d, c.eps, L.out_scale);
     });
+}
+
+// Layer l after the last layer that writes K/V, on the answer rows alone
+// (every range's, gathered by layer_out; their normed rows in hn_w_): no
+// other row's output reaches them any more, since the layer's keys and
+// values are an earlier layer's cache.  Its queries are those rows', with
+// their own metadata (d_tail_meta_); the attention items are built over
+// them alone.
+void Engine::layer_tail(int64_t l) {
+    const Config& c = cfg_;
+    const int64_t n = tail_rows_, d = c.d;
+    const hipStream_t s = stream_;
+    Layer& L = layers_[size_t(l)];
+    const int64_t hd = c.head_dim[size_t(l)], qw = c.qkv_width(l);
+    const int64_t src = c.kv_source[size_t(l)];
+    RowBufs b = row_bufs(0, c.heads * hd, c.ff[size_t(l)]);
+    QkArgs q{};
+    q.qkv = qkv_w_.as<float>();
+    q.qkv_stride = qw;
+    q.meta = d_tail_meta_;
+    q.q_norm = L.q_norm.as<float>();
+    q.k_norm = nullptr;
+    q.rope = rope_tabs_[size_t(rope_of_[size_t(l)])].as<float2>();
+    q.rope_rows = rope_rows_;
+    q.rope_dims = c.rope_dims[size_t(l)];
+    q.eps = c.eps;
+    q.q_scale = c.query_scale;
+    q.heads = int(c.heads);
+    q.kv_heads = int(c.kv_heads);
+    q.hd = int(hd);
+    q.has_kv = false;
+    q.v_norm = c.v_norm;
+    q.t = n;
+    q.base = 0;
+    q.cap_pad = cap_pad_;
+    q.q16 = q16_w_.as<half_t>();
+    q.kc = kc_[size_t(src)].as<half_t>();
+    q.vt = vt_[size_t(src)].as<half_t>();
+    if (hd == 256) {
+        step("mm_qkv_out", 0, [&] { launch_gemm_qkprep(s, b.hw, d, L.qkv.w, q, n); });
+    } else {
+        step("mm_qkv_out", 0, [&] { launch_gemm(s, b.hw, d, L.qkv.w, qkv_w_.as<float>(), qw, n); });
+        step("qk_prep_out", 0, [&] { launch_qk_prep(s, q); });
+    }
+    AttnArgs att{};
+    att.q16 = q.q16;
+    att.kc = q.kc;
+    att.vt = q.vt;
+    att.meta = meta_.as<int32_t>();
+    att.qmeta = d_tail_meta_;
+    att.kend = tail_kend_;
+    att.out = b.aw;
+    att.t = n;
+    att.base = 0;
+    att.cap_pad = cap_pad_;
+    att.heads = int(c.heads);
+    att.kv_heads = int(c.kv_heads);
+    att.hd = int(hd);
+    att.window = c.sliding[size_t(l)] ? int(c.window) : 0;
+    att.part_o = part_o_.as<half_t>();
+    att.part_ml = part_ml_.as<float>();
+    const int kind = (c.sliding[size_t(l)] && c.window > 0) ? 0 : 1;
+    const AttnWork& w = tail_work_[kind];
+    const int64_t ni = int64_t(w.items.size()), nm = int64_t(w.merges.size());
+    if (ni > 0) step("attention_out", 0, [&] { launch_attention(s, att, d_tail_items_[kind], ni, w.nw); });
+    if (nm > 0) step("attention_merge_out", 0, [&] { launch_attention_merge(s, att, d_tail_merges_[kind], nm, w.nw); });
+    rows_post(l, 0, s, n, b);
 }
 
 void Engine::readout(const PassPlan& p) {

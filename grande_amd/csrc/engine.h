@@ -259,16 +259,44 @@ class Engine {
     hipEvent_t ev_fork_ = nullptr, ev_join_[MAX_SUB] = {};
     std::vector<hipEvent_t> ev_kv_;  // [range][layer]: the range's K/V rows of the layer are in the cache
     void layer(int64_t l, int k, int64_t base);
-    // The last layer past its attention on the gathered answer rows
-    // (range k's wanted rows [w0, w1)).
+    // The answer rows: from layer out_layer_ (the last one that writes K/V)
+    // past its attention on, the rest of the pass runs for the rows a
+    // request reads out only, gathered into max_rows-row buffers.
+    struct RowBufs {
+        half_t* aw = nullptr;    // attention output
+        float* xw = nullptr;     // stream
+        half_t* hw = nullptr;    // normed stream (f16)
+        half_t* actw = nullptr;  // gated activations
+        float* pw = nullptr;     // product parts
+        float* pliw = nullptr;   // per-layer inputs of every layer
+        half_t* x16w = nullptr;  // f16(stream)
+        float* plgw = nullptr;   // the per-layer gate's product
+        half_t* pl16w = nullptr; // gated per-layer inputs
+    };
+    RowBufs row_bufs(int64_t w0, int64_t W, int64_t ff);
+    // Range k's answer rows through layer out_layer_ past its attention.
     void layer_out(int k, const half_t* attn, const float* x, int64_t r0);
+    // Layer l past its attention on n gathered rows.
+    void rows_post(int64_t l, int k, hipStream_t s, int64_t n, const RowBufs& b);
+    // A layer after out_layer_ on the answer rows alone.
+    void layer_tail(int64_t l);
     bool full_last_layer_ = false;  // set_full_last_layer
-    bool out_rows_ = false;         // this pass runs the last layer on its answer rows
+    bool out_rows_ = false;         // this pass runs the answer-row path
+    int64_t out_layer_ = 0;         // the last layer with K/V of its own
+    int64_t tail_rows_ = 0;         // answer rows of the pass
+    int64_t tail_kend_ = 0;         // end of the pass's cache rows
+    // the layers after out_layer_: the answer rows' metadata and attention
+    // work over them, per layer type
+    const int32_t* d_tail_meta_ = nullptr;
+    AttnWork tail_work_[2];
+    const int4* d_tail_items_[2] = {nullptr, nullptr};
+    const int4* d_tail_merges_[2] = {nullptr, nullptr};
     // [max_rows] rows: attention output, stream, normed stream, gated
-    // activations, product parts (OMG_KSPLIT of them)
-    DevBuf attn_w_, x_w_, hn_w_, act_w_, a_w_;
+    // activations, product parts (the most any o / down product makes),
+    // queries and (head_dim 512) the f32 q/k/v product
+    DevBuf attn_w_, x_w_, hn_w_, act_w_, a_w_, q16_w_, qkv_w_;
     // ... and with per-layer inputs: f16(x), the gate's product, the gated
-    // inputs (f16) and the rows' last-layer slice of the inputs
+    // inputs (f16) and the rows' inputs of every layer
     DevBuf x16_w_, plg_w_, pl16_w_, pli_w_;
     std::vector<DevBuf> kc_, vt_;  // per layer that owns K/V
     // pinned host staging

@@ -229,6 +229,12 @@ struct AttnArgs {
     int64_t t, base, cap_pad;
     int heads, kv_heads, hd;
     int window;          // 0 = global layer
+    // Queries that are not the cache rows [base, base + t) (rows gathered
+    // from a pass): their metadata, one int4 per query row, and the end of
+    // the cache rows their keys may come from.  Null / 0: meta + base and
+    // base + t.
+    const int32_t* qmeta;
+    int64_t kend;
 };
 // The pass's attention work: items (query tile, first key tile, end key
 // tile, partial slot or -1) and, for split tiles, merges (query tile, first
