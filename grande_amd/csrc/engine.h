@@ -135,10 +135,11 @@ class Engine {
     void sync();
     void set_profile(bool on);
     std::string profile_report() const;
-    // The last layer past its attention for every row of the pass (on) or,
-    // the default, for the rows a request reads out only (their tiles'
-    // attention, then o, norms, gate/up and down on the gathered rows): the
-    // same rows either way.  Takes effect from the next pass.
+    // Every layer for every row of the pass (on) or, the default, from the
+    // last layer that writes K/V past its attention on, the rows a request
+    // reads out only (their tiles' attention, then the rest of that layer
+    // and every later layer on the gathered rows): the same rows either
+    // way.  Takes effect from the next pass.
     void set_full_last_layer(bool on);
     hipStream_t stream() const { return stream_; }
 

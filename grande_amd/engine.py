@@ -395,8 +395,9 @@ class Engine:
         L.check(L.lib().omg_profile(self._h, int(on)))
 
     def full_last_layer(self, on: bool) -> None:
-        """Run the last layer for every row (on) instead of the read-out
-        rows only (the default); the returned rows are the same bits."""
+        """Run every layer for every row (on) instead of, the default, the
+        read-out rows only from the last layer that writes K/V past its
+        attention on; the returned rows are the same bits."""
         L.check(L.lib().omg_set_full_last_layer(self._h, int(on)))
 
     def profile_report(self) -> dict[str, tuple[int, float]]:

@@ -241,12 +241,16 @@ int omg_sync(omg_engine *e);
 int omg_profile(omg_engine *e, int on);
 size_t omg_profile_report(omg_engine *e, char *buf, size_t len);
 /* No counterpart in the reference, whose pass runs every layer for every
- * row (engine.rs:1674-1751).  By default the last layer runs past its
- * attention for the rows a request reads out only (the query tiles that
- * hold them, then o, norms, gate/up and down on the gathered rows; every
- * layer's K/V is still written for every row); on != 0 runs it for every
- * row as the reference does.  The rows a pass returns are the same bits
- * either way.  From the next pass on. */
+ * row (engine.rs:1674-1751).  By default, from the last layer that writes
+ * K/V (the model's last layer, or with Gemma 4's K/V-sharing layers the
+ * last layer before them) past its attention, the pass runs for the rows a
+ * request reads out only: that layer's attention for the query tiles that
+ * hold them, then o, norms, gate/up, down and the per-layer block on the
+ * gathered rows, and every later layer on those rows alone (its keys and
+ * values are an earlier layer's cache, so no other row reaches them).
+ * Every K/V cache is still written for every row.  on != 0 runs every
+ * layer for every row as the reference does.  The rows a pass returns are
+ * the same bits either way.  From the next pass on. */
 int omg_set_full_last_layer(omg_engine *e, int on);
 
 /* Kernel-level entry points on device pointers (the reference's matmul.rs
