@@ -761,10 +761,10 @@ static int ksplit(int64_t k, int64_t n) {
 }
 
 // K pieces of the o / down products, a function of the shape only: a
-// split of deep K (at least 4,096, in whole 1,024-wide pieces: the 4B
-// model's down projection) is cut into `group` pieces whose products
-// accumulate from zero; the pieces' sums are added in K order, then the
-// splits' sums in order.  Long passes add a split's pieces in the GEMM's
+// split of deep K (at least 3,072, in whole 1,024-wide pieces: the 4B
+// model's down projection, the E2B double-wide down in its 4 splits) is
+// cut into `group` pieces whose products accumulate from zero; the pieces'
+// sums are added in K order, then the splits' sums in order.  Long passes add a split's pieces in the GEMM's
 // registers (kfold, one partial per split); short ones run a piece per
 // workgroup, which fills the chip (10 x 20 x 2 = 400 workgroups at the 4B
 // one-branch pass instead of 40), and the residual norm adds the pieces in
@@ -776,7 +776,9 @@ static int ksplit(int64_t k, int64_t n) {
 // 155.9 -> 160.8 ms, E2B cold 16.55 -> 16.71 ms, warm 7.58 -> 7.67 ms;
 // pieces of 4 stages on the 270M model's o and down: its cold pass 1.0 and
 // 1.3 us slower per product, its warm pass 0.5 and 1.1 us faster.
-constexpr int64_t DEEP_PIECE_K = 1024, DEEP_MIN_K = 4096;
+// 3,072 rather than 4,096 (same box): the E2B double-wide down on its
+// answer rows 19.4 -> 10.3 us, cold pass 8.05 -> 7.98 ms, warm 4.92 -> 4.83 ms.
+constexpr int64_t DEEP_PIECE_K = 1024, DEEP_MIN_K = 3072;
 
 Engine::SplitPlan Engine::split_plan(int64_t k, int64_t n, int64_t t) const {
     SplitPlan p;
